@@ -1,0 +1,291 @@
+"""Benchmark of the MI355X FP8 paged-attention decode (one JSON line).
+
+Metric: KV-read HBM GB/s (and % of the 8 TB/s MI355X peak) plus us per
+decode step, on the Llama-3-8B-shaped configuration (batch 64, 32 query / 8
+KV heads, head 128, 16-token pages, every context 4096, per-tensor fp8
+scales) unless ``--config`` names another.
+
+A step is one ``pa_decode_ps_launch`` call (partition pass + LSE reduce)
+with scratch preallocated.  Inputs are resident in HBM; the timed steps
+rotate over several independent KV-cache copies whose total exceeds twice
+the 256 MB Infinity Cache, so no step reads KV that the previous step left
+in the cache.  ``value`` = attended K+V bytes / step time.
+
+``roofline`` is measured live: the partition kernel alone is launched K
+times through the C ABI between HIP events on the stream it runs on; its
+algorithmic bytes per launch / average duration is ``achieved``.
+``traffic`` (HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE,
+scaled by a copy-kernel calibration) is read from profiles/ when present.
+
+``cpu_baseline``: the CPU oracle (restated torch reference, float32, per
+sequence as tests/kernels/test_pa.py:302-330) timed on this host over a
+bounded sample of the same workload's sequences.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBPS = 8000.0
+MALL_BYTES = 256 * 1024 * 1024
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--config", default="c2_llama8b", help="c1_tiny|c2_llama8b|c3_ragged|c4_window|c5_mtp|all")
+    p.add_argument("--seed", type=int, default=7)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
+    p.add_argument("--copies", type=int, default=0, help="KV-cache copies to rotate (0 = auto)")
+    return p.parse_args()
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def cpu_baseline(case_gpu, cfg, budget_s: float) -> dict:
+    """Time the CPU oracle on sequences of the same workload until the budget
+    is spent; scaled to KV GB/s over the sequences it finished."""
+    import torch
+
+    from flydsl_amd import workloads
+    from oracle import torch_ref
+
+    ctx_all = case_gpu["context_lengths"].cpu().tolist()
+    bs = cfg.block_size
+    hkv = cfg.num_kv_heads
+    ql = cfg.query_length
+    kc = case_gpu["key_cache"]
+    vc = case_gpu["value_cache"]
+    per_token = case_gpu["key_scale"].dim() > 1
+    done_bytes = 0
+    done_seqs = 0
+    spent = 0.0
+    order = list(range(cfg.batch))
+    for b in order:
+        n = math.ceil(ctx_all[b] / bs)
+        pages = case_gpu["block_tables"][b, :n].long()
+        # compact copy of this sequence's pages (the oracle's input), not timed
+        k = kc.index_select(0, pages).cpu()
+        v = vc.index_select(0, pages).cpu()
+        nbp = k.shape[0]
+        if per_token:
+            ks = case_gpu["key_scale"].index_select(0, pages).cpu().reshape(nbp, hkv, bs).permute(1, 0, 2).reshape(hkv, -1)
+            vs = case_gpu["value_scale"].index_select(0, pages).cpu().reshape(nbp, hkv, bs).permute(1, 0, 2).reshape(hkv, -1)
+        else:
+            ks = case_gpu["key_scale"].cpu().expand(hkv, nbp * bs)
+            vs = case_gpu["value_scale"].cpu().expand(hkv, nbp * bs)
+        q = case_gpu["query"][b * ql : (b + 1) * ql].cpu()
+        bt = torch.arange(nbp, dtype=torch.int32).reshape(1, -1)
+        cl = torch.tensor([ctx_all[b]], dtype=torch.int32)
+        ind = torch.tensor([0, ql], dtype=torch.int32)
+        t0 = time.perf_counter()
+        torch_ref.torch_mha_extend(q, k, v, bt, cl, ind, ks, vs, sliding_window=cfg.sliding_window,
+                                   softmax_scale=case_gpu["softmax_scale"])
+        spent += time.perf_counter() - t0
+        done_bytes += workloads.kv_bytes(cfg, [ctx_all[b]])
+        done_seqs += 1
+        if spent >= budget_s:
+            break
+    return {
+        "value": round(done_bytes / spent / 1e9, 4),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{done_seqs} of {cfg.batch} sequences of {cfg.name} through the float32 torch oracle "
+        f"(oracle/torch_ref.py torch_mha_extend), {spent:.1f} s; host {cpu_model()}, "
+        f"affinity {len(os.sched_getaffinity(0))} cpus, os.cpu_count {os.cpu_count()}",
+    }
+
+
+def load_traffic(name: str):
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def run_config(name: str, args) -> dict:
+    import torch
+
+    from flydsl_amd import _lib, get_recommended_splits, pa_decode_ps_launch, workloads
+
+    cfg = workloads.CONFIGS[name]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    case = workloads.build_inputs(cfg, device=dev, seed=args.seed)
+    ctx = case["context_lengths"].cpu().tolist()
+    kv = workloads.kv_bytes(cfg, ctx)
+    kv_sc = workloads.kv_bytes(cfg, ctx, include_scales=True)
+    cache_bytes = case["key_cache"].numel() + case["value_cache"].numel()
+    copies = args.copies or max(3, math.ceil(2 * MALL_BYTES / max(cache_bytes, 1)) + 1)
+    caches = [(case["key_cache"], case["value_cache"], case["key_scale"], case["value_scale"])]
+    for _ in range(copies - 1):
+        caches.append(tuple(t.clone() for t in caches[0]))
+
+    B, hkv, ql = cfg.batch, cfg.num_kv_heads, cfg.query_length
+    eq = ql * cfg.gqa
+    if cfg.sliding_window:
+        P = get_recommended_splits(B, hkv, sliding_window=cfg.sliding_window, query_length=ql)
+    else:
+        P = get_recommended_splits(B, hkv, split_kv_blocks=max(1, 256 // cfg.block_size))
+    es = torch.empty((B, hkv, P, eq), device=dev)
+    ml = torch.empty_like(es)
+    tmp = torch.empty((B, hkv, P, eq, 128), device=dev, dtype=torch.bfloat16)
+    out = torch.empty(case["query"].shape, device=dev, dtype=torch.bfloat16)
+
+    def step(i):
+        k, v, ks, vs = caches[i % copies]
+        return pa_decode_ps_launch(out, case["query"], k, v, case["context_lengths"], None, None,
+                                   case["softmax_scale"], ks, vs, sliding_window=cfg.sliding_window,
+                                   block_tables=case["block_tables"], max_context_partition_num=P,
+                                   exp_sums=es, max_logits=ml, temporary_output=tmp)
+
+    route = None
+    for i in range(args.warmup):
+        route = step(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+
+    # Live per-kernel timing of the partition pass (the dominant kernel),
+    # launched through the C ABI on this same stream.
+    lib = _lib.load()
+    pargs = []
+    for k, v, ks, vs in caches:
+        a = _lib.PartitionArgs()
+        a.abi_version = _lib.ABI_VERSION
+        a.exp_sums, a.max_logits, a.tmp_out = es.data_ptr(), ml.data_ptr(), tmp.data_ptr()
+        a.query, a.key_cache, a.value_cache = case["query"].data_ptr(), k.data_ptr(), v.data_ptr()
+        a.block_tables, a.context_lengths = case["block_tables"].data_ptr(), case["context_lengths"].data_ptr()
+        a.key_scale, a.value_scale = ks.data_ptr(), vs.data_ptr()
+        a.stride_q_tok, a.stride_q_head = case["query"].stride(0), case["query"].stride(1)
+        a.stride_k_block, a.stride_k_head = k.stride(0), k.stride(1)
+        a.stride_v_block, a.stride_v_head = v.stride(0), v.stride(1)
+        a.stride_es_seq, a.stride_es_head, a.stride_es_part = es.stride()[:3]
+        a.stride_to_seq, a.stride_to_head, a.stride_to_part, a.stride_to_group = tmp.stride()[:4]
+        a.stride_bt_seq = case["block_tables"].stride(0)
+        if ks.dim() > 1:
+            a.stride_ks_block, a.stride_ks_head = ks.stride(0), ks.stride(1)
+        a.num_seqs, a.num_kv_heads, a.num_partitions = B, hkv, P
+        a.query_length, a.query_group_size, a.head_size = ql, cfg.gqa, 128
+        a.block_size, a.num_blocks = cfg.block_size, k.shape[0]
+        a.max_blocks_per_seq = case["block_tables"].shape[1]
+        a.sliding_window, a.per_token_kv, a.trans_v = cfg.sliding_window, int(ks.dim() > 1), 1
+        a.query_dtype, a.tmp_dtype = _lib.DTYPE_BF16, _lib.DTYPE_BF16
+        a.softmax_scale = case["softmax_scale"]
+        pargs.append(a)
+    sh = ctypes.c_void_p(stream.cuda_stream)
+    for i in range(max(3, args.warmup)):
+        _lib.check(lib.pa_fp8_decode_partition(ctypes.byref(pargs[i % copies]), sh), "partition")
+    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    k0.record(stream)
+    for i in range(args.steps):
+        lib.pa_fp8_decode_partition(ctypes.byref(pargs[i % copies]), sh)
+    k1.record(stream)
+    torch.cuda.synchronize()
+    kern_ms = k0.elapsed_time(k1) / args.steps
+
+    achieved = kv / (kern_ms * 1e-3) / 1e9
+    value = kv / (ms * 1e-3) / 1e9
+    line = {
+        "metric": "KV-read HBM GB/s (% of peak) + us/decode step, 8B-shaped fp8 paged decode",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_step": round(ms * 1e3, 2),
+        "pct_of_peak": round(100.0 * value / PEAK_HBM_GBPS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8",
+        "data": "synthetic (seeded N(0,1) K/V quantised to fp8 e4m3fn, bf16 queries, permuted pages)",
+        "config": {
+            "workload": name,
+            "batch": B,
+            "query_length": ql,
+            "num_query_heads": cfg.num_query_heads,
+            "num_kv_heads": hkv,
+            "head_size": 128,
+            "block_size": cfg.block_size,
+            "sliding_window": cfg.sliding_window,
+            "kv_scales": "per_token" if cfg.per_token else "per_tensor",
+            "context": cfg.ctx,
+            "sum_context": int(sum(ctx)),
+            "num_partitions": P,
+            "route": route,
+            "kv_bytes_per_step": kv,
+            "kv_plus_scale_bytes_per_step": kv_sc,
+            "kv_copies_rotated": copies,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "pa_fp8_partition_kernel",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            "traffic": load_traffic(name),
+            "kernel_us": round(kern_ms * 1e3, 2),
+            "algorithmic_bytes": kv,
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(
+            {k2: case[k2] for k2 in ("context_lengths", "block_tables", "key_cache", "value_cache", "key_scale",
+                                     "value_scale", "query", "softmax_scale")}, cfg, args.cpu_seconds)
+    del caches
+    return line
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus N > 1 is not supported "
+                                   "(the decode path shards by sequence / kv head with no communication)"}))
+        sys.exit(2)
+    names = ["c2_llama8b", "c3_ragged", "c4_window", "c5_mtp"] if args.config == "all" else [args.config]
+    for n in names:
+        line = run_config(n, args)
+        print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

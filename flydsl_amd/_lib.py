@@ -1,0 +1,196 @@
+"""ctypes binding of ``libpa_fp8.so`` (the C ABI in ``include/pa_fp8.h``).
+
+The library is built in-tree by :func:`flydsl_amd.build.build_library`.  A
+missing library is an error: there is no fallback implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+LIB_NAME = "libpa_fp8.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+ABI_VERSION = 1
+
+DTYPE_BF16 = 0
+DTYPE_F16 = 1
+DTYPE_F32 = 2
+
+ERRORS = {
+    -1: "PA_ERR_NULL_ARG",
+    -2: "PA_ERR_HEAD_SIZE",
+    -3: "PA_ERR_BLOCK_SIZE",
+    -4: "PA_ERR_GROUP",
+    -5: "PA_ERR_DTYPE",
+    -6: "PA_ERR_SHAPE",
+    -7: "PA_ERR_ALIGN",
+    -8: "PA_ERR_ABI",
+}
+
+EXPORTED_SYMBOLS = (
+    "pa_fp8_decode_partition",
+    "pa_fp8_decode_reduce",
+    "pa_fp8_recommended_splits",
+    "pa_fp8_plan_slot",
+    "pa_fp8_plan_visible",
+    "pa_fp8_version",
+    "pa_fp8_error_string",
+)
+
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+
+
+class PartitionArgs(ctypes.Structure):
+    """Mirror of ``pa_fp8_partition_args`` (field order matters)."""
+
+    _fields_ = [
+        ("abi_version", _i32),
+        ("exp_sums", _vp),
+        ("max_logits", _vp),
+        ("tmp_out", _vp),
+        ("output", _vp),
+        ("query", _vp),
+        ("key_cache", _vp),
+        ("value_cache", _vp),
+        ("block_tables", _vp),
+        ("kv_indptr", _vp),
+        ("context_lengths", _vp),
+        ("key_scale", _vp),
+        ("value_scale", _vp),
+        ("stride_q_tok", _i64),
+        ("stride_q_head", _i64),
+        ("stride_k_block", _i64),
+        ("stride_k_head", _i64),
+        ("stride_v_block", _i64),
+        ("stride_v_head", _i64),
+        ("stride_es_seq", _i64),
+        ("stride_es_head", _i64),
+        ("stride_es_part", _i64),
+        ("stride_to_seq", _i64),
+        ("stride_to_head", _i64),
+        ("stride_to_part", _i64),
+        ("stride_to_group", _i64),
+        ("stride_bt_seq", _i64),
+        ("stride_ks_block", _i64),
+        ("stride_ks_head", _i64),
+        ("stride_out_tok", _i64),
+        ("stride_out_head", _i64),
+        ("num_seqs", _i32),
+        ("num_kv_heads", _i32),
+        ("num_partitions", _i32),
+        ("query_length", _i32),
+        ("query_group_size", _i32),
+        ("head_size", _i32),
+        ("block_size", _i32),
+        ("num_blocks", _i32),
+        ("max_blocks_per_seq", _i32),
+        ("sliding_window", _i32),
+        ("per_token_kv", _i32),
+        ("trans_v", _i32),
+        ("query_dtype", _i32),
+        ("tmp_dtype", _i32),
+        ("output_dtype", _i32),
+        ("softmax_scale", ctypes.c_float),
+    ]
+
+
+class ReduceArgs(ctypes.Structure):
+    """Mirror of ``pa_fp8_reduce_args``."""
+
+    _fields_ = [
+        ("abi_version", _i32),
+        ("output", _vp),
+        ("exp_sums", _vp),
+        ("max_logits", _vp),
+        ("tmp_out", _vp),
+        ("stride_out_seq", _i64),
+        ("stride_out_ql", _i64),
+        ("stride_out_kv_head", _i64),
+        ("stride_out_group", _i64),
+        ("stride_es_seq", _i64),
+        ("stride_es_head", _i64),
+        ("stride_es_part", _i64),
+        ("stride_to_seq", _i64),
+        ("stride_to_head", _i64),
+        ("stride_to_part", _i64),
+        ("stride_to_group", _i64),
+        ("num_seqs", _i32),
+        ("num_kv_heads", _i32),
+        ("num_partitions", _i32),
+        ("query_length", _i32),
+        ("query_group_size", _i32),
+        ("head_size", _i32),
+        ("output_dtype", _i32),
+        ("tmp_dtype", _i32),
+    ]
+
+
+_LIB: Optional[ctypes.CDLL] = None
+
+
+class LibraryNotBuilt(RuntimeError):
+    pass
+
+
+def load(path: Optional[str] = None) -> ctypes.CDLL:
+    """Load (once) and type the shared library; raise if it is not built."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    p = path or LIB_PATH
+    if not os.path.exists(p):
+        raise LibraryNotBuilt(
+            f"{p} is missing: build the HIP library first (python -c 'import __graft_entry__ as g; g.build()')"
+        )
+    lib = ctypes.CDLL(p)
+    lib.pa_fp8_decode_partition.argtypes = [ctypes.POINTER(PartitionArgs), _vp]
+    lib.pa_fp8_decode_partition.restype = ctypes.c_int
+    lib.pa_fp8_decode_reduce.argtypes = [ctypes.POINTER(ReduceArgs), _vp]
+    lib.pa_fp8_decode_reduce.restype = ctypes.c_int
+    lib.pa_fp8_recommended_splits.argtypes = [ctypes.c_int] * 7
+    lib.pa_fp8_recommended_splits.restype = ctypes.c_int
+    lib.pa_fp8_plan_slot.argtypes = [ctypes.c_int] * 5 + [ctypes.POINTER(ctypes.c_int)] * 2
+    lib.pa_fp8_plan_slot.restype = ctypes.c_int
+    lib.pa_fp8_plan_visible.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_int)] * 2
+    lib.pa_fp8_plan_visible.restype = ctypes.c_int
+    lib.pa_fp8_version.argtypes = []
+    lib.pa_fp8_version.restype = ctypes.c_char_p
+    lib.pa_fp8_error_string.argtypes = [ctypes.c_int]
+    lib.pa_fp8_error_string.restype = ctypes.c_char_p
+    if path is None:
+        _LIB = lib
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().pa_fp8_error_string(rc).decode()
+        raise RuntimeError(f"{what} failed: {ERRORS.get(rc, 'hipError')} ({rc}): {msg}")
+
+
+def plan_slot(context_length: int, num_partitions: int, slot: int, sliding_window: int, query_length: int):
+    t0, t1 = ctypes.c_int(), ctypes.c_int()
+    check(
+        load().pa_fp8_plan_slot(context_length, num_partitions, slot, sliding_window, query_length, t0, t1),
+        "pa_fp8_plan_slot",
+    )
+    return t0.value, t1.value
+
+
+def plan_visible(context_length: int, qi: int, query_length: int, sliding_window: int):
+    lo, hi = ctypes.c_int(), ctypes.c_int()
+    check(load().pa_fp8_plan_visible(context_length, qi, query_length, sliding_window, lo, hi), "pa_fp8_plan_visible")
+    return lo.value, hi.value
+
+
+def recommended_splits(num_seqs, num_kv_heads, split_kv_blocks, sliding_window, partition_tokens, query_length, num_cu):
+    return int(
+        load().pa_fp8_recommended_splits(
+            num_seqs, num_kv_heads, split_kv_blocks, sliding_window, partition_tokens, query_length, num_cu
+        )
+    )

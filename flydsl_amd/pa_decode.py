@@ -1,0 +1,455 @@
+"""Host launcher of the MI355X FP8 paged-attention decode.
+
+Drop-in for the reference's Python API in kernels/pa_decode_fp8.py:
+``pa_decode_ps_launch`` (:2812-3202), ``get_recommended_splits``
+(:1922-1949) and ``get_pa_metadata`` (:1729-1859).  Same argument names,
+defaults, tensor layouts, validation errors and route strings; the device
+work is done by the HIP kernels of ``libpa_fp8.so`` through its C ABI.
+
+Routes (same dispatch order as the reference, :2883 / :3010 / :3123):
+  * ``sliding_window > 0``    -> window partition pass + LSE reduce
+                                 ("ps_sw_partitioned"), or the fused
+                                 single-slot pass ("ps_sw_fused_partitioned")
+                                 when only one slot is asked for.  Works for
+                                 every supported page size (the reference
+                                 kernel is correct for 1024-token pages only,
+                                 kernels/pa_decode_swa.py:1228).
+  * page size 16 or 64        -> split-context partition pass + LSE reduce
+                                 ("ps_small_block").
+  * other page sizes (1024)   -> the same partition pass over the flat
+                                 ``kv_page_indices``/``kv_indptr`` page list
+                                 + LSE reduce ("ps_split_reduce").
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import DTYPE_BF16, DTYPE_F16, DTYPE_F32
+
+KV_COMPUTE_BLOCK = 256  # tokens per context sub-partition
+_PA_DECODE_PS_SMALL_BLOCK_SIZES = (16, 64)
+
+_PACKED_FP8_QUERY_DTYPES = tuple(
+    d
+    for d in (
+        torch.uint8,
+        getattr(torch, "float8_e4m3fn", None),
+        getattr(torch, "float8_e4m3fnuz", None),
+    )
+    if d is not None
+)
+
+
+def _cdiv(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+@functools.lru_cache(maxsize=None)
+def _device_cu_count(index: int) -> int:
+    return int(torch.cuda.get_device_properties(index).multi_processor_count)
+
+
+def _cu_count(device: Optional[torch.device] = None) -> int:
+    dev = torch.device("cuda") if device is None else torch.device(device)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    return _device_cu_count(idx)
+
+
+def get_recommended_splits(
+    num_sequences: int,
+    num_kv_heads: int,
+    split_kv_blocks: int = 1,
+    *,
+    sliding_window: int = 0,
+    context_partition_size: int = KV_COMPUTE_BLOCK,
+    query_length: int = 1,
+    num_cu: Optional[int] = None,
+) -> int:
+    """Slots (``max_context_partition_num``) for the partitioned routes.
+
+    Same result as the reference (kernels/pa_decode_fp8.py:1922-1949): for a
+    window, ``cdiv(W + ql - 1, cps) + 1``; otherwise two workgroups per CU
+    spread over ``B * Hkv * split_kv_blocks`` units, clamped to [4, 8].
+    ``num_cu`` defaults to the current device's CU count (256 on MI355X);
+    pass it to plan without a GPU.
+    """
+    if sliding_window > 0:
+        cu = 1
+    else:
+        cu = num_cu if num_cu is not None else _cu_count()
+    return _lib.recommended_splits(
+        int(num_sequences),
+        int(num_kv_heads),
+        int(split_kv_blocks),
+        int(sliding_window),
+        int(context_partition_size),
+        int(query_length),
+        int(cu),
+    )
+
+
+def _is_current_stream_capturing() -> bool:
+    if not torch.cuda.is_available():
+        return False
+    try:
+        return torch.cuda.is_current_stream_capturing()
+    except RuntimeError:
+        return False
+
+
+def _prepare_scale_tensor(name: str, scale, *, device: torch.device, is_graph_capturing: bool) -> torch.Tensor:
+    """float / tensor -> float32 tensor on ``device`` (kernels/pa_decode_fp8.py:1871-1895)."""
+    if isinstance(scale, torch.Tensor):
+        if is_graph_capturing:
+            if scale.device != device:
+                raise ValueError(f"CUDA graph capture requires `{name}` to already be on {device}, got {scale.device}.")
+            if scale.dtype != torch.float32:
+                raise ValueError(f"CUDA graph capture requires `{name}` to already be float32, got {scale.dtype}.")
+            return scale
+        return scale.to(device=device, dtype=torch.float32)
+    if is_graph_capturing:
+        raise ValueError(
+            f"CUDA graph capture requires `{name}` to be passed as a pre-created float32 tensor on the target device."
+        )
+    return torch.tensor([float(scale or 1.0)], device=device, dtype=torch.float32)
+
+
+def _get_query_input_dtype(query: torch.Tensor) -> str:
+    if query.dtype in _PACKED_FP8_QUERY_DTYPES:
+        return "packed_fp8"
+    if query.dtype == torch.bfloat16:
+        return "bf16"
+    if query.dtype == torch.float16:
+        return "f16"
+    raise ValueError(
+        f"Unsupported query dtype for pa_decode_ps_launch: {query.dtype}. Expected packed FP8/uint8, bf16, or f16."
+    )
+
+
+def _get_output_dtype_code(output: torch.Tensor) -> int:
+    if output.dtype == torch.bfloat16:
+        return DTYPE_BF16
+    if output.dtype == torch.float16:
+        return DTYPE_F16
+    if output.dtype == torch.float32:
+        return DTYPE_F32
+    raise ValueError(
+        f"Unsupported output dtype for pa_decode_ps_launch reduce: {output.dtype}. Expected bf16, f16, or f32."
+    )
+
+
+def _tmp_dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.bfloat16:
+        return DTYPE_BF16
+    if t.dtype == torch.float32:
+        return DTYPE_F32
+    raise ValueError(f"temporary_output must be bfloat16 or float32, got {t.dtype}")
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _check_int32(name: str, t: torch.Tensor, device: torch.device) -> None:
+    if t.dtype != torch.int32:
+        raise ValueError(f"`{name}` must be int32, got {t.dtype}")
+    if t.device != device:
+        raise ValueError(f"`{name}` must be on {device}, got {t.device}")
+
+
+def _check_partials(exp_sums, max_logits, tmp, shape, head_size):
+    if tuple(exp_sums.shape) != shape or tuple(max_logits.shape) != shape:
+        raise ValueError(f"exp_sums/max_logits must have shape {shape}, got {tuple(exp_sums.shape)}")
+    if tuple(tmp.shape) != shape + (head_size,):
+        raise ValueError(f"temporary_output must have shape {shape + (head_size,)}, got {tuple(tmp.shape)}")
+    if exp_sums.dtype != torch.float32 or max_logits.dtype != torch.float32:
+        raise ValueError("exp_sums and max_logits must be float32")
+    if exp_sums.stride() != max_logits.stride() or exp_sums.stride(-1) != 1:
+        raise ValueError("exp_sums and max_logits must share strides with a contiguous last dimension")
+    if tmp.stride(-1) != 1:
+        raise ValueError("temporary_output must be contiguous in its last dimension")
+
+
+def pa_decode_ps_launch(
+    output: torch.Tensor,
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    context_lengths: torch.Tensor,
+    kv_page_indices: torch.Tensor,
+    kv_indptr: torch.Tensor,
+    softmax_scale: float,
+    key_scale: torch.Tensor = None,
+    value_scale: torch.Tensor = None,
+    *,
+    sliding_window: int = 0,
+    metadata: dict = None,
+    block_tables: torch.Tensor = None,
+    max_context_partition_num: int = 0,
+    exp_sums: torch.Tensor = None,
+    max_logits: torch.Tensor = None,
+    temporary_output: torch.Tensor = None,
+    stream=None,
+) -> str:
+    """FP8 paged-attention decode (drop-in for kernels/pa_decode_fp8.py:2812).
+
+    output [B*ql, Hq, D] (bf16/f16/f32) is written in place.  query
+    [B*ql, Hq, D] bf16/f16; key_cache [NB, Hkv, D/16, bs, 16] fp8; value_cache
+    trans [NB, Hkv, bs/16, D, 16] (or [NB, Hkv, D, bs]); context_lengths [B]
+    int32; block_tables [B, max_blocks] int32 (page sizes 16/64 and windows);
+    kv_page_indices / kv_indptr: flat page list (other page sizes).
+    key/value_scale: float, [1] tensor (per tensor) or [NB, Hkv, bs, 1]
+    (per token per head).  Returns the route name.
+    """
+    num_query_heads = query.shape[1]
+    num_kv_heads = key_cache.shape[1]
+    trans_v = value_cache.dim() == 5
+    query_input_dtype = _get_query_input_dtype(query)
+    dev = query.device
+    is_graph_capturing = _is_current_stream_capturing()
+
+    key_scale = _prepare_scale_tensor("key_scale", key_scale, device=dev, is_graph_capturing=is_graph_capturing)
+    value_scale = _prepare_scale_tensor("value_scale", value_scale, device=dev, is_graph_capturing=is_graph_capturing)
+    if query_input_dtype == "packed_fp8":
+        raise ValueError(
+            "`pa_decode_ps_launch` no longer accepts host query_scale and only supports "
+            "bf16/f16 query inputs with kernel-internal query scale computation."
+        )
+    per_token_kv = key_scale.dim() > 1
+
+    batch_size = int(context_lengths.shape[0])
+    if batch_size == 0:
+        return "ps_small_block"
+    query_length = query.shape[0] // batch_size
+    if query_length * batch_size != query.shape[0]:
+        raise ValueError(f"query rows ({query.shape[0]}) must be a multiple of the batch size ({batch_size})")
+    if num_query_heads % num_kv_heads != 0:
+        raise ValueError("Query heads must be divisible by KV heads")
+    query_group_size = num_query_heads // num_kv_heads
+    head_size = int(query.shape[-1])
+    if head_size % 64 != 0:
+        raise ValueError(f"Unsupported head_dim={head_size}; must be a multiple of 64.")
+    if head_size != 128:
+        raise NotImplementedError(f"head_dim={head_size} is not built; this library supports head_dim=128.")
+    eqgs = query_length * query_group_size
+    if eqgs > 64:
+        raise NotImplementedError(f"query_length * query_group_size = {eqgs} > 64 is not supported.")
+    block_size = int(key_cache.shape[-2])
+    if tuple(key_cache.shape[2:]) != (head_size // 16, block_size, 16):
+        raise ValueError(f"key_cache must be [NB, Hkv, {head_size // 16}, bs, 16], got {tuple(key_cache.shape)}")
+    if key_cache.element_size() != 1 or value_cache.element_size() != 1:
+        raise ValueError("key_cache and value_cache must be 1-byte fp8 (e4m3fn) tensors")
+    if trans_v:
+        if tuple(value_cache.shape[2:]) != (block_size // 16, head_size, 16):
+            raise ValueError(f"trans value_cache must be [NB, Hkv, bs/16, D, 16], got {tuple(value_cache.shape)}")
+    elif tuple(value_cache.shape[2:]) != (head_size, block_size):
+        raise ValueError(f"value_cache must be [NB, Hkv, D, bs], got {tuple(value_cache.shape)}")
+    for t, name in ((key_cache, "key_cache"), (value_cache, "value_cache"), (query, "query"), (output, "output")):
+        if t.stride(-1) != 1:
+            raise ValueError(f"`{name}` must be contiguous in its last dimension")
+    if tuple(output.shape) != tuple(query.shape):
+        raise ValueError(f"output shape {tuple(output.shape)} must match query shape {tuple(query.shape)}")
+    if per_token_kv:
+        if key_scale.dim() != 4 or tuple(key_scale.shape[:3]) != (key_cache.shape[0], num_kv_heads, block_size):
+            raise ValueError(f"per-token key_scale must be [NB, Hkv, bs, 1], got {tuple(key_scale.shape)}")
+        if key_scale.stride() != value_scale.stride() or key_scale.stride(2) != 1:
+            raise ValueError("key_scale and value_scale must share strides with a contiguous token dimension")
+    output_dtype = _get_output_dtype_code(output)
+    _check_int32("context_lengths", context_lengths, dev)
+
+    s = stream or torch.cuda.current_stream(dev)
+    stream_handle = ctypes.c_void_p(s.cuda_stream)
+
+    kv_ind = None
+    if sliding_window > 0:
+        route = "sw"
+        if block_tables is None:
+            raise ValueError("pa_decode_ps_launch: sliding_window > 0 requires `block_tables`.")
+        needed = get_recommended_splits(
+            batch_size,
+            num_kv_heads,
+            sliding_window=sliding_window,
+            context_partition_size=KV_COMPUTE_BLOCK,
+            query_length=query_length,
+        )
+        if max_context_partition_num == 0:
+            max_context_partition_num = needed
+        elif 1 < max_context_partition_num < needed:
+            raise ValueError(
+                f"max_context_partition_num={max_context_partition_num} cannot cover a window of {sliding_window} "
+                f"tokens (needs {needed} slots)."
+            )
+    elif block_size in _PA_DECODE_PS_SMALL_BLOCK_SIZES:
+        route = "small"
+        if block_tables is None:
+            raise ValueError(
+                f"pa_decode_ps_launch: block_size={block_size} requires `block_tables` "
+                "(per-sequence physical block index table)."
+            )
+        if max_context_partition_num == 0:
+            max_context_partition_num = get_recommended_splits(
+                batch_size, num_kv_heads, split_kv_blocks=KV_COMPUTE_BLOCK // block_size
+            )
+    else:
+        route = "flat"
+        if kv_page_indices is None or kv_indptr is None:
+            raise ValueError(f"pa_decode_ps_launch: block_size={block_size} requires `kv_page_indices` and `kv_indptr`.")
+        _check_int32("kv_page_indices", kv_page_indices, dev)
+        _check_int32("kv_indptr", kv_indptr, dev)
+        if is_graph_capturing and metadata is None and (exp_sums is None or max_logits is None or temporary_output is None):
+            raise ValueError(
+                "CUDA graph capture requires precomputed `metadata`; "
+                "call `get_pa_metadata()` before capture and pass it via `metadata=`."
+            )
+        if max_context_partition_num == 0:
+            max_context_partition_num = get_recommended_splits(batch_size, num_kv_heads, split_kv_blocks=1)
+        kv_ind = kv_indptr
+        if metadata is not None and exp_sums is None and "exp_sums" in metadata:
+            exp_sums = metadata["exp_sums"]
+            max_logits = metadata["max_logits"]
+            temporary_output = metadata["temporary_output"]
+            max_context_partition_num = int(exp_sums.shape[2])
+    if route != "flat":
+        _check_int32("block_tables", block_tables, dev)
+        if block_tables.dim() != 2 or block_tables.stride(-1) != 1:
+            raise ValueError("block_tables must be a 2-D int32 tensor with a contiguous last dimension")
+    P = int(max_context_partition_num)
+
+    fused = route == "sw" and P <= 1
+    shape = (batch_size, num_kv_heads, P, eqgs)
+    if not fused:
+        if is_graph_capturing and (exp_sums is None or max_logits is None or temporary_output is None):
+            which = "sliding-window" if route == "sw" else "small-block PS"
+            raise ValueError(
+                "CUDA graph capture requires preallocated `exp_sums`, `max_logits`, "
+                f"and `temporary_output` for the {which} path."
+            )
+        # Every slot writes all of its cells (empty slots write 0 / -inf /
+        # zeros), so uninitialised buffers are fine: no fill kernels.
+        if exp_sums is None:
+            exp_sums = torch.empty(shape, device=dev, dtype=torch.float32)
+        if max_logits is None:
+            max_logits = torch.empty(shape, device=dev, dtype=torch.float32)
+        if temporary_output is None:
+            temporary_output = torch.empty(shape + (head_size,), device=dev, dtype=torch.bfloat16)
+        _check_partials(exp_sums, max_logits, temporary_output, shape, head_size)
+
+    pa = _lib.PartitionArgs()
+    pa.abi_version = _lib.ABI_VERSION
+    pa.query = query.data_ptr()
+    pa.key_cache = key_cache.data_ptr()
+    pa.value_cache = value_cache.data_ptr()
+    if route == "flat":
+        pa.block_tables = kv_page_indices.data_ptr()
+        pa.kv_indptr = kv_ind.data_ptr()
+        pa.stride_bt_seq = 0
+        pa.max_blocks_per_seq = max(1, int(kv_page_indices.numel()))
+    else:
+        pa.block_tables = block_tables.data_ptr()
+        pa.kv_indptr = None
+        pa.stride_bt_seq = block_tables.stride(0)
+        pa.max_blocks_per_seq = int(block_tables.shape[1])
+    pa.context_lengths = context_lengths.data_ptr()
+    pa.key_scale = key_scale.data_ptr()
+    pa.value_scale = value_scale.data_ptr()
+    pa.stride_q_tok, pa.stride_q_head = query.stride(0), query.stride(1)
+    pa.stride_k_block, pa.stride_k_head = key_cache.stride(0), key_cache.stride(1)
+    pa.stride_v_block, pa.stride_v_head = value_cache.stride(0), value_cache.stride(1)
+    if per_token_kv:
+        pa.stride_ks_block, pa.stride_ks_head = key_scale.stride(0), key_scale.stride(1)
+    pa.num_seqs = batch_size
+    pa.num_kv_heads = num_kv_heads
+    pa.num_partitions = P
+    pa.query_length = query_length
+    pa.query_group_size = query_group_size
+    pa.head_size = head_size
+    pa.block_size = block_size
+    pa.num_blocks = int(key_cache.shape[0])
+    pa.sliding_window = int(sliding_window)
+    pa.per_token_kv = int(per_token_kv)
+    pa.trans_v = int(trans_v)
+    pa.query_dtype = DTYPE_BF16 if query_input_dtype == "bf16" else DTYPE_F16
+    pa.softmax_scale = float(softmax_scale)
+    if fused:
+        pa.output = output.data_ptr()
+        pa.output_dtype = output_dtype
+        pa.stride_out_tok, pa.stride_out_head = output.stride(0), output.stride(1)
+        pa.tmp_dtype = DTYPE_BF16
+    else:
+        pa.exp_sums = exp_sums.data_ptr()
+        pa.max_logits = max_logits.data_ptr()
+        pa.tmp_out = temporary_output.data_ptr()
+        pa.stride_es_seq, pa.stride_es_head, pa.stride_es_part = exp_sums.stride()[:3]
+        (pa.stride_to_seq, pa.stride_to_head, pa.stride_to_part, pa.stride_to_group) = temporary_output.stride()[:4]
+        pa.tmp_dtype = _tmp_dtype_code(temporary_output)
+    lib = _lib.load()
+    _lib.check(lib.pa_fp8_decode_partition(ctypes.byref(pa), stream_handle), "pa_fp8_decode_partition")
+    if fused:
+        return "ps_sw_fused_partitioned"
+
+    ra = _lib.ReduceArgs()
+    ra.abi_version = _lib.ABI_VERSION
+    ra.output = output.data_ptr()
+    ra.exp_sums = exp_sums.data_ptr()
+    ra.max_logits = max_logits.data_ptr()
+    ra.tmp_out = temporary_output.data_ptr()
+    # output [B*ql, Hq, D] addressed as [B, ql, Hkv, gqa, D]
+    so0, so1 = output.stride(0), output.stride(1)
+    ra.stride_out_seq, ra.stride_out_ql = query_length * so0, so0
+    ra.stride_out_kv_head, ra.stride_out_group = query_group_size * so1, so1
+    ra.stride_es_seq, ra.stride_es_head, ra.stride_es_part = exp_sums.stride()[:3]
+    (ra.stride_to_seq, ra.stride_to_head, ra.stride_to_part, ra.stride_to_group) = temporary_output.stride()[:4]
+    ra.num_seqs = batch_size
+    ra.num_kv_heads = num_kv_heads
+    ra.num_partitions = P
+    ra.query_length = query_length
+    ra.query_group_size = query_group_size
+    ra.head_size = head_size
+    ra.output_dtype = output_dtype
+    ra.tmp_dtype = _tmp_dtype_code(temporary_output)
+    _lib.check(lib.pa_fp8_decode_reduce(ctypes.byref(ra), stream_handle), "pa_fp8_decode_reduce")
+    return {"sw": "ps_sw_partitioned", "small": "ps_small_block", "flat": "ps_split_reduce"}[route]
+
+
+def get_pa_metadata(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    context_lengths: torch.Tensor,
+    kv_indptr: torch.Tensor,
+    num_query_heads: int,
+    num_kv_heads: int,
+    partition_size: int = KV_COMPUTE_BLOCK,
+):
+    """Preallocate the partial buffers of the flat-page-list route.
+
+    Returns a dict that ``pa_decode_ps_launch(metadata=...)`` consumes, so the
+    call is graph-capturable.  Keys ``partition_indptr``, ``num_sm`` and
+    ``query_length`` follow kernels/pa_decode_fp8.py:1844-1859;
+    ``exp_sums``/``max_logits``/``temporary_output`` are the slot partials
+    this build's partition pass writes.
+    """
+    dev = query.device
+    batch_size = int(context_lengths.shape[0])
+    query_length = query.shape[0] // max(batch_size, 1)
+    head_size = int(query.shape[-1])
+    eqgs = query_length * (num_query_heads // num_kv_heads)
+    P = get_recommended_splits(batch_size, num_kv_heads, split_kv_blocks=1)
+    parts = (context_lengths.to(torch.int32) + (partition_size - 1)) // partition_size
+    partition_indptr = torch.zeros(batch_size + 1, dtype=torch.int32, device=dev)
+    partition_indptr[1:] = torch.cumsum(parts, dim=0).to(torch.int32)
+    shape = (batch_size, num_kv_heads, P, eqgs)
+    return {
+        "partition_indptr": partition_indptr,
+        "num_sm": _cu_count(dev),
+        "query_length": query_length,
+        "exp_sums": torch.empty(shape, device=dev, dtype=torch.float32),
+        "max_logits": torch.empty(shape, device=dev, dtype=torch.float32),
+        "temporary_output": torch.empty(shape + (head_size,), device=dev, dtype=torch.bfloat16),
+    }

@@ -1,0 +1,175 @@
+"""Synthetic inputs for the benchmark configurations (seeded, any device).
+
+Shapes follow the reference's decode layouts (kernels/pa_decode_fp8.py:
+2812-2832; tests/kernels/test_pa.py:177-211, 334-429): query [B*ql, Hq, 128]
+bf16; K [NB, Hkv, 8, bs, 16] fp8 e4m3fn; trans V [NB, Hkv, bs/16, 128, 16]
+fp8; per-tensor scales [1] or per-token-per-head scales [NB, Hkv, bs, 1]
+(amax / 448); block tables of randomly permuted physical pages.
+
+  c1_tiny    B4,   ql1, Hq8/Hkv2,   bs16, ctx U[1, 512], per tensor, NB = 256
+  c2_llama8b B64,  ql1, Hq32/Hkv8,  bs16, ctx 4096,      per tensor
+  c3_ragged  B128, ql1, Hq32/Hkv8,  bs16, ctx lognormal(median 2048, sigma 1)
+                                          clipped to [16, 32768], per token
+  c4_window  B32,  ql1, Hq32/Hkv8,  bs16, W 4096, ctx U[8192, 32768], per tensor
+  c5_mtp     B256, ql4, Hq64/Hkv4,  bs64, ctx U[4096, 8192], per token
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import math
+from typing import Dict, List, Optional
+
+import numpy as np
+import torch
+
+FP8 = torch.float8_e4m3fn
+FP8_MAX = 448.0
+HEAD = 128
+
+
+@dataclasses.dataclass(frozen=True)
+class DecodeConfig:
+    name: str
+    batch: int
+    query_length: int
+    num_query_heads: int
+    num_kv_heads: int
+    block_size: int
+    ctx: str  # "fixed:N" | "uniform:LO:HI" | "lognormal:MEDIAN:SIGMA:LO:HI"
+    per_token: bool
+    sliding_window: int = 0
+    num_blocks: Optional[int] = None  # physical pages; default = pages needed
+    head_size: int = HEAD
+
+    @property
+    def gqa(self) -> int:
+        return self.num_query_heads // self.num_kv_heads
+
+
+CONFIGS: Dict[str, DecodeConfig] = {
+    "c1_tiny": DecodeConfig("c1_tiny", 4, 1, 8, 2, 16, "uniform:1:512", False, num_blocks=256),
+    "c2_llama8b": DecodeConfig("c2_llama8b", 64, 1, 32, 8, 16, "fixed:4096", False),
+    "c3_ragged": DecodeConfig("c3_ragged", 128, 1, 32, 8, 16, "lognormal:2048:1.0:16:32768", True),
+    "c4_window": DecodeConfig("c4_window", 32, 1, 32, 8, 16, "uniform:8192:32768", False, sliding_window=4096),
+    "c5_mtp": DecodeConfig("c5_mtp", 256, 4, 64, 4, 64, "uniform:4096:8192", True),
+}
+
+
+def sample_context_lengths(cfg: DecodeConfig, seed: int) -> List[int]:
+    rng = np.random.default_rng(seed)
+    kind, *params = cfg.ctx.split(":")
+    if kind == "fixed":
+        return [int(params[0])] * cfg.batch
+    if kind == "uniform":
+        lo, hi = int(params[0]), int(params[1])
+        return [int(x) for x in rng.integers(lo, hi + 1, size=cfg.batch)]
+    if kind == "lognormal":
+        med, sigma, lo, hi = float(params[0]), float(params[1]), int(params[2]), int(params[3])
+        x = np.exp(rng.normal(math.log(med), sigma, size=cfg.batch))
+        return [int(v) for v in np.clip(np.round(x), lo, hi)]
+    raise ValueError(cfg.ctx)
+
+
+def _quant_per_tensor(x: torch.Tensor):
+    amax = x.abs().amax().float()
+    scale = torch.where(amax > 0, amax / FP8_MAX, torch.ones_like(amax))
+    return (x / scale).to(FP8), scale.reshape(1).to(torch.float32)
+
+
+def _quant_rows(x: torch.Tensor):
+    """Quantise along the last dim (one scale per row): returns q, scale[..., 1]."""
+    amax = x.abs().amax(dim=-1, keepdim=True).float()
+    scale = torch.where(amax > 0, amax / FP8_MAX, torch.ones_like(amax))
+    return (x / scale).to(FP8), scale
+
+
+def build_inputs(
+    cfg: DecodeConfig,
+    device="cpu",
+    seed: int = 0,
+    context_lengths: Optional[List[int]] = None,
+    dist: str = "normal",
+) -> dict:
+    """All tensors of one decode call for ``cfg``; random values from ``seed``.
+
+    K and V are drawn per (page, head) in float32 and quantised to fp8
+    e4m3fn (per tensor or per token and head).  Pages are a random
+    permutation of the physical cache, dealt to sequences in order.
+    """
+    device = torch.device(device)
+    ctx = context_lengths if context_lengths is not None else sample_context_lengths(cfg, seed)
+    bs = cfg.block_size
+    pages_per_seq = [math.ceil(c / bs) for c in ctx]
+    need = sum(pages_per_seq)
+    nb = cfg.num_blocks if cfg.num_blocks is not None else max(need, 1)
+    if nb < need:
+        raise ValueError(f"{cfg.name}: {nb} pages cannot hold {need}")
+    rng = np.random.default_rng(seed + 1)
+    perm = rng.permutation(nb).astype(np.int32)
+    max_pages = max(max(pages_per_seq), 1)
+    bt = np.zeros((cfg.batch, max_pages), dtype=np.int32)
+    pos = 0
+    for b, n in enumerate(pages_per_seq):
+        bt[b, :n] = perm[pos : pos + n]
+        pos += n
+    gen = torch.Generator(device=device).manual_seed(seed)
+    hkv, d = cfg.num_kv_heads, cfg.head_size
+    rows = cfg.batch * cfg.query_length
+    if dist == "normal":
+        query = torch.randn(rows, cfg.num_query_heads, d, generator=gen, device=device, dtype=torch.float32)
+    else:
+        query = torch.rand(rows, cfg.num_query_heads, d, generator=gen, device=device) * 2 - 1
+    query = query.to(torch.bfloat16)
+
+    def draw(shape):
+        if dist == "normal":
+            return torch.randn(shape, generator=gen, device=device, dtype=torch.float32)
+        return torch.rand(shape, generator=gen, device=device, dtype=torch.float32) * 2 - 1
+
+    # token-major rows [NB, Hkv, bs, D]; quantise, then lay out.
+    k_rows = draw((nb, hkv, bs, d))
+    v_rows = draw((nb, hkv, bs, d))
+    if cfg.per_token:
+        qk, ks = _quant_rows(k_rows)
+        qv, vs = _quant_rows(v_rows)
+    else:
+        qk, ks = _quant_per_tensor(k_rows)
+        qv, vs = _quant_per_tensor(v_rows)
+    del k_rows, v_rows
+    key_cache = qk.view(torch.uint8).reshape(nb, hkv, bs, d // 16, 16).permute(0, 1, 3, 2, 4).contiguous()
+    # trans V: [NB, Hkv, bs/16, D, 16]
+    value_cache = qv.view(torch.uint8).reshape(nb, hkv, bs // 16, 16, d).permute(0, 1, 2, 4, 3).contiguous()
+    del qk, qv
+    return {
+        "config": cfg,
+        "query": query,
+        "key_cache": key_cache.view(FP8),
+        "value_cache": value_cache.view(FP8),
+        "block_tables": torch.from_numpy(bt).to(device),
+        "context_lengths": torch.tensor(ctx, dtype=torch.int32, device=device),
+        "key_scale": ks.contiguous(),
+        "value_scale": vs.contiguous(),
+        "softmax_scale": 1.0 / math.sqrt(d),
+        "query_length": cfg.query_length,
+        "sliding_window": cfg.sliding_window,
+    }
+
+
+def attended_tokens(ctx: List[int], query_length: int, sliding_window: int) -> List[int]:
+    """Distinct keys read per sequence (union over its queries)."""
+    out = []
+    for c in ctx:
+        hi = c
+        lo = max(c - query_length - sliding_window, 0) if sliding_window > 0 else 0
+        out.append(max(hi - lo, 0))
+    return out
+
+
+def kv_bytes(cfg: DecodeConfig, ctx: List[int], include_scales: bool = False) -> int:
+    """Algorithmic bytes of one decode step: attended K + V (+ scales)."""
+    toks = sum(attended_tokens(ctx, cfg.query_length, cfg.sliding_window))
+    per_tok = cfg.num_kv_heads * cfg.head_size * 2
+    if include_scales and cfg.per_token:
+        per_tok += cfg.num_kv_heads * 8
+    return toks * per_tok

@@ -1,0 +1,178 @@
+/*
+ * pa_fp8.h - C ABI of the MI355X (gfx950) FP8 paged-attention decode library.
+ *
+ * The library (libpa_fp8.so) exports hand-written HIP kernels for the
+ * split-context decode of the reference's `pa_decode_ps_launch` routes and a
+ * few host-side planning helpers.  Every tensor is passed as a raw device
+ * pointer plus element strides; the library never allocates device memory
+ * and keeps no mutable global state, so calls are re-entrant and may be
+ * captured into a HIP graph when the caller preallocates every buffer.
+ *
+ * Return codes: 0 on success, a positive hipError_t value when the HIP
+ * runtime rejects a launch, or one of the negative PA_ERR_* codes below for
+ * arguments the kernels do not support.  pa_fp8_error_string() names them.
+ *
+ * Tensor layouts (element strides; the innermost dimension is contiguous):
+ *   query        [B * ql, Hq, D]            bf16 or f16
+ *   key_cache    [NB, Hkv, D / 16, bs, 16]  fp8 e4m3fn (OCP)
+ *   value_cache  trans [NB, Hkv, bs / 16, D, 16] or plain [NB, Hkv, D, bs]
+ *   block_tables [B, max_blocks]            int32 physical page per logical page
+ *   context_lengths [B]                     int32
+ *   key/value scale  per tensor: [1] float32
+ *                    per token:  [NB, Hkv, bs, 1] float32
+ *   exp_sums, max_logits [B, Hkv, P, ql * gqa] float32
+ *   tmp_out      [B, Hkv, P, ql * gqa, D]   bf16 or float32
+ *   output       [B * ql, Hq, D]            bf16, f16 or float32
+ * where gqa = Hq / Hkv and P is the number of context slots.
+ */
+#ifndef PA_FP8_H
+#define PA_FP8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PA_FP8_ABI_VERSION 1
+
+enum pa_fp8_dtype {
+  PA_DTYPE_BF16 = 0,
+  PA_DTYPE_F16 = 1,
+  PA_DTYPE_F32 = 2,
+};
+
+enum pa_fp8_error {
+  PA_OK = 0,
+  PA_ERR_NULL_ARG = -1,       /* a required pointer is NULL */
+  PA_ERR_HEAD_SIZE = -2,      /* head_size other than 128 */
+  PA_ERR_BLOCK_SIZE = -3,     /* page size not 16 or a multiple of 32 up to 1024 */
+  PA_ERR_GROUP = -4,          /* ql * gqa outside [1, 64] */
+  PA_ERR_DTYPE = -5,          /* unsupported query / output / partial dtype */
+  PA_ERR_SHAPE = -6,          /* non-positive dimension or partition count */
+  PA_ERR_ALIGN = -7,          /* a pointer or stride breaks 16-byte alignment */
+  PA_ERR_ABI = -8,            /* struct abi_version mismatch */
+};
+
+/*
+ * Split-context partition pass.
+ *
+ * Replaces the compiled launchers of the reference:
+ *   compile_pa_decode_ps(...)["launch"]   kernels/pa_decode_fp8.py:2738-2802
+ *     (page size 16 / 64 small-block route, sliding_window == 0), and
+ *   compile_pa_decode_sw(...)["launch"]   kernels/pa_decode_swa.py:1644-1718
+ *     (sliding_window > 0; generalised here to any supported page size).
+ * Grid: one workgroup per (sequence, kv head, slot).  Slot z of a sequence
+ * covers the token range of pa_fp8_plan_slot(); it stores, per query column
+ * e = qi * gqa + g, exp_sums = sum exp(l - m), max_logits = m (the slot's
+ * maximum scaled logit, natural-log units; -inf when empty) and the
+ * normalised partial output tmp_out.  When `output` is non-NULL and
+ * num_partitions == 1 the final output is written instead (the reference's
+ * fused single-partition window kernel, kernels/pa_decode_swa.py:1480-1620).
+ */
+typedef struct pa_fp8_partition_args {
+  int32_t abi_version; /* = PA_FP8_ABI_VERSION */
+  /* outputs */
+  float* exp_sums;
+  float* max_logits;
+  void* tmp_out;
+  void* output; /* NULL unless fused (num_partitions == 1) */
+  /* inputs */
+  const void* query;
+  const void* key_cache;
+  const void* value_cache;
+  const int32_t* block_tables;
+  /* Optional.  When non-NULL the page list of sequence b is the flat
+   * kv_page_indices layout of the reference's persistent route:
+   * block_tables + kv_indptr[b] .. block_tables + kv_indptr[b + 1]
+   * (stride_bt_seq and max_blocks_per_seq are then ignored). */
+  const int32_t* kv_indptr;
+  const int32_t* context_lengths;
+  const float* key_scale;
+  const float* value_scale;
+  /* element strides */
+  int64_t stride_q_tok, stride_q_head;
+  int64_t stride_k_block, stride_k_head;
+  int64_t stride_v_block, stride_v_head;
+  int64_t stride_es_seq, stride_es_head, stride_es_part;
+  int64_t stride_to_seq, stride_to_head, stride_to_part, stride_to_group;
+  int64_t stride_bt_seq;
+  int64_t stride_ks_block, stride_ks_head; /* per-token scales only */
+  int64_t stride_out_tok, stride_out_head; /* fused output only */
+  /* sizes */
+  int32_t num_seqs;
+  int32_t num_kv_heads;
+  int32_t num_partitions;
+  int32_t query_length;
+  int32_t query_group_size;
+  int32_t head_size;
+  int32_t block_size;
+  int32_t num_blocks;          /* pages in the cache: page indices are clamped to it */
+  int32_t max_blocks_per_seq;  /* block_tables row length */
+  int32_t sliding_window;      /* 0 = full causal context */
+  int32_t per_token_kv;        /* 0 = per-tensor scales, 1 = [NB, Hkv, bs, 1] */
+  int32_t trans_v;             /* 1 = trans value layout */
+  int32_t query_dtype;         /* PA_DTYPE_BF16 / PA_DTYPE_F16 */
+  int32_t tmp_dtype;           /* PA_DTYPE_BF16 / PA_DTYPE_F32 */
+  int32_t output_dtype;        /* fused output only */
+  float softmax_scale;
+} pa_fp8_partition_args;
+
+int pa_fp8_decode_partition(const pa_fp8_partition_args* args, void* hip_stream);
+
+/*
+ * Log-sum-exp merge of the P slot partials into the final output.
+ *
+ * Replaces compile_pa_decode_sw_reduce(...)["launch"]
+ * (kernels/pa_decode_swa.py:1132-1177; math at :954-1130), which both
+ * partitioned routes of pa_decode_ps_launch call.  For each (sequence, kv
+ * head, column): M = max_p m_p, w_p = s_p e^{m_p - M} / sum_q s_q e^{m_q - M},
+ * out = sum_p w_p tmp_p (zero when every slot is empty).  The output is
+ * addressed through the 5-D view [B, ql, Hkv, gqa, D].
+ */
+typedef struct pa_fp8_reduce_args {
+  int32_t abi_version;
+  void* output;
+  const float* exp_sums;
+  const float* max_logits;
+  const void* tmp_out;
+  int64_t stride_out_seq, stride_out_ql, stride_out_kv_head, stride_out_group;
+  int64_t stride_es_seq, stride_es_head, stride_es_part;
+  int64_t stride_to_seq, stride_to_head, stride_to_part, stride_to_group;
+  int32_t num_seqs;
+  int32_t num_kv_heads;
+  int32_t num_partitions;
+  int32_t query_length;
+  int32_t query_group_size;
+  int32_t head_size;
+  int32_t output_dtype;
+  int32_t tmp_dtype;
+} pa_fp8_reduce_args;
+
+int pa_fp8_decode_reduce(const pa_fp8_reduce_args* args, void* hip_stream);
+
+/*
+ * Host-only planning helpers (no GPU needed).
+ *
+ * pa_fp8_recommended_splits replaces get_recommended_splits
+ * (kernels/pa_decode_fp8.py:1922-1949) with the CU count passed in;
+ * pa_fp8_plan_slot returns the logical token range [*t0, *t1) that slot
+ * `slot` reads (kernels/pa_decode_fp8.py:2311-2320 and
+ * kernels/pa_decode_swa.py:1356-1368); pa_fp8_plan_visible returns the key
+ * range query qi may attend (kernels/pa_decode_swa.py:1597-1620).
+ */
+int pa_fp8_recommended_splits(int num_seqs, int num_kv_heads, int split_kv_blocks, int sliding_window,
+                              int partition_tokens, int query_length, int num_cu);
+int pa_fp8_plan_slot(int context_length, int num_partitions, int slot, int sliding_window, int query_length,
+                     int* t0, int* t1);
+int pa_fp8_plan_visible(int context_length, int qi, int query_length, int sliding_window, int* lo, int* hi);
+
+/* Library identification and error names. */
+const char* pa_fp8_version(void);
+const char* pa_fp8_error_string(int code);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PA_FP8_H */

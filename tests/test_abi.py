@@ -1,0 +1,65 @@
+"""The C-ABI library loads, exports every declared symbol and its structs
+match the header layout (checked by compiling the header with gcc)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from flydsl_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "pa_fp8.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(pa_fp8_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_bound_symbols():
+    assert declared_functions() == sorted(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True).stdout
+    for name in declared_functions():
+        assert re.search(rf"\bT {name}$", out, re.M), name
+
+
+def test_version_and_error_strings():
+    lib = _lib.load()
+    assert b"gfx950" in lib.pa_fp8_version()
+    assert lib.pa_fp8_error_string(-7) == b"pointer or stride not 16-byte aligned"
+
+
+def test_null_args_rejected_without_gpu():
+    lib = _lib.load()
+    assert lib.pa_fp8_decode_partition(None, None) == -1
+    assert lib.pa_fp8_decode_reduce(None, None) == -1
+    a = _lib.PartitionArgs()
+    a.abi_version = 99
+    assert lib.pa_fp8_decode_partition(ctypes.byref(a), None) == -8
+
+
+@pytest.mark.parametrize("struct,cname", [(_lib.PartitionArgs, "pa_fp8_partition_args"), (_lib.ReduceArgs, "pa_fp8_reduce_args")])
+def test_struct_layout_matches_header(tmp_path, struct, cname):
+    fields = [f for f, _ in struct._fields_]
+    src = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){",
+           f'printf("%zu\\n", sizeof({cname}));']
+    src += [f'printf("%zu\\n", offsetof({cname}, {f}));' for f in fields]
+    src += ["return 0;}"]
+    c = tmp_path / "layout.c"
+    c.write_text("\n".join(src))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", str(c), "-o", str(exe)], check=True)
+    vals = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert vals[0] == ctypes.sizeof(struct)
+    assert vals[1:] == [getattr(struct, f).offset for f in fields]

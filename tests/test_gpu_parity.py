@@ -1,0 +1,262 @@
+"""GPU parity of the HIP decode path against the CPU oracle.
+
+Tolerance (from the target): bf16 outputs within atol 2e-2 / rtol 2e-2 of
+the restated torch reference (torch.isclose semantics, every element, as
+tests/kernels/test_pa.py:603-641 applies its tolerance).  Partition
+intermediates (exp_sums, max_logits, tmp_out) are checked per slot against
+the oracle's direct slot computation, which pins the slot indexing: an
+empty slot must be exactly (0, -inf, 0).
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from flydsl_amd import pa_decode_ps_launch, workloads
+from oracle import plan
+from tests._cases import make_case, slot_partials, torch_oracle
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-2
+RTOL = 2e-2
+DEV = "cuda:0"
+
+
+def to_dev(case, device=DEV):
+    out = dict(case)
+    for k, v in case.items():
+        if isinstance(v, torch.Tensor):
+            out[k] = v.to(device)
+    return out
+
+
+def launch(case, *, P=0, out_dtype=torch.bfloat16, tmp_dtype=torch.bfloat16, flat=False, partials=False):
+    q = case["query"]
+    out = torch.empty(q.shape, dtype=out_dtype, device=q.device)
+    kw = dict(
+        sliding_window=case["sliding_window"],
+        block_tables=None if flat else case["block_tables"],
+        max_context_partition_num=P,
+    )
+    page_idx, indptr = None, None
+    if flat:
+        bt = case["block_tables"].cpu()
+        ctx = case["context_lengths"].cpu().tolist()
+        bs = case["key_cache"].shape[-2]
+        rows = [bt[b, : math.ceil(c / bs)] for b, c in enumerate(ctx)]
+        page_idx = torch.cat(rows).to(torch.int32).to(q.device)
+        indptr = torch.tensor([0] + list(torch.tensor([len(r) for r in rows]).cumsum(0)), dtype=torch.int32,
+                              device=q.device)
+    es = ml = to = None
+    if partials:
+        b = case["context_lengths"].shape[0]
+        hkv = case["key_cache"].shape[1]
+        eq = case["query_length"] * (q.shape[1] // hkv)
+        es = torch.full((b, hkv, P, eq), 7.0, device=q.device)
+        ml = torch.full((b, hkv, P, eq), 7.0, device=q.device)
+        to = torch.full((b, hkv, P, eq, 128), 7.0, device=q.device, dtype=tmp_dtype)
+        kw.update(exp_sums=es, max_logits=ml, temporary_output=to)
+    route = pa_decode_ps_launch(
+        out, q, case["key_cache"], case["value_cache"], case["context_lengths"], page_idx, indptr,
+        case["softmax_scale"], case["key_scale"], case["value_scale"], **kw
+    )
+    torch.cuda.synchronize()
+    return out, route, (es, ml, to)
+
+
+def assert_parity(out, ref, what=""):
+    out = out.float().cpu()
+    ref = ref.float().cpu()
+    bad = ~torch.isclose(out, ref, atol=ATOL, rtol=RTOL)
+    err = (out - ref).abs().max().item()
+    print(f"[parity] {what} max_abs_err={err:.3e} bad={int(bad.sum())}/{out.numel()}", flush=True)
+    assert not torch.isnan(out).any(), what
+    assert int(bad.sum()) == 0, f"{what}: {int(bad.sum())} elements outside atol/rtol {ATOL}; max err {err}"
+
+
+CASES = {
+    "c1_tiny": dict(config="c1_tiny"),
+    "per_token": dict(per_token=True, ctx_range=(1, 700)),
+    "ctx_edges": dict(ctx=[1, 2, 15, 16, 17, 31, 32, 33, 255, 256, 257, 1023]),
+    "mtp_ql4_gqa4": dict(query_length=4, num_query_heads=16, num_kv_heads=4, ctx_range=(4, 600)),
+    "mtp_ql2_gqa8_pt": dict(query_length=2, num_query_heads=16, num_kv_heads=2, per_token=True, ctx_range=(2, 900)),
+    "gqa16_ql4": dict(query_length=4, num_query_heads=16, num_kv_heads=1, ctx_range=(4, 1100)),
+    "gqa8_ql3": dict(query_length=3, num_query_heads=8, num_kv_heads=1, ctx_range=(3, 1100), per_token=True),
+    "page64": dict(block_size=64, ctx_range=(1, 2000)),
+    "page64_mtp_pt": dict(block_size=64, query_length=4, num_query_heads=64, num_kv_heads=4, per_token=True,
+                          ctx_range=(4, 1500)),
+    "window": dict(sliding_window=300, ctx_range=(1, 2000)),
+    "window_mtp_pt": dict(sliding_window=100, query_length=3, num_query_heads=16, num_kv_heads=4, per_token=True,
+                          ctx_range=(3, 1500)),
+    "window_page64": dict(sliding_window=513, block_size=64, ctx_range=(1, 3000)),
+    "uniform_data": dict(dist="uniform", ctx_range=(1, 1500)),
+}
+
+
+def build(name):
+    spec = dict(CASES[name])
+    if "config" in spec:
+        cfg = workloads.CONFIGS[spec["config"]]
+        return workloads.build_inputs(cfg, device="cpu", seed=123)
+    return make_case(batch=6, seed=len(name), **spec)
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_decode_matches_oracle(name):
+    case = build(name)
+    ref = torch_oracle(case, float_out=False)
+    out, route, _ = launch(to_dev(case))
+    exp_route = "ps_sw_partitioned" if case["sliding_window"] else "ps_small_block"
+    assert route == exp_route
+    assert_parity(out, ref, name)
+
+
+@pytest.mark.parametrize("P", [1, 2, 3, 5, 8, 13])
+def test_any_partition_count(P):
+    case = make_case(batch=5, ctx_range=(1, 3000), per_token=True, seed=P)
+    ref = torch_oracle(case, float_out=False)
+    out, _, _ = launch(to_dev(case), P=P)
+    assert_parity(out, ref, f"P={P}")
+
+
+@pytest.mark.parametrize("window", [2, 100, 700])
+def test_window_fused_and_partitioned(window):
+    case = make_case(batch=5, ctx=[1, 60, 255, 900, 2500], sliding_window=window, seed=21 + window)
+    ref = torch_oracle(case, float_out=False)
+    out, route, _ = launch(to_dev(case), P=1)
+    assert route == "ps_sw_fused_partitioned"
+    assert_parity(out, ref, f"fused W={window}")
+    out2, route2, _ = launch(to_dev(case))
+    assert route2 == "ps_sw_partitioned"
+    assert_parity(out2, ref, f"window W={window} P=auto")
+
+
+def test_flat_page_list_route():
+    case = make_case(batch=5, block_size=1024, ctx_range=(1, 5000), per_token=True, seed=31)
+    ref = torch_oracle(case, float_out=False)
+    out, route, _ = launch(to_dev(case), flat=True)
+    assert route == "ps_split_reduce"
+    assert_parity(out, ref, "page1024 flat")
+
+
+def test_plain_value_layout_and_dtypes():
+    case = make_case(batch=4, block_size=64, ctx_range=(1, 1000), seed=41)
+    ref = torch_oracle(case, float_out=True)
+    from oracle.torch_ref import unshuffle_value_cache_layout
+
+    d = to_dev(case)
+    d["value_cache"] = unshuffle_value_cache_layout(case["value_cache"].view(torch.uint8)).view(
+        torch.float8_e4m3fn).to(DEV)
+    out, _, _ = launch(d, out_dtype=torch.float32, tmp_dtype=torch.float32, P=4, partials=True)
+    assert_parity(out, ref, "plain V, f32 out/tmp")
+    d["query"] = d["query"].to(torch.float16)
+    out16, _, _ = launch(d, out_dtype=torch.float16)
+    assert_parity(out16, ref, "f16 query/out")
+
+
+@pytest.mark.parametrize("window,ql", [(0, 1), (0, 3), (200, 1), (150, 2)])
+def test_slot_partials_match_oracle(window, ql):
+    """exp_sums / max_logits / tmp_out per slot: same cells as the oracle."""
+    case = make_case(batch=5, query_length=ql, num_query_heads=8, num_kv_heads=2, ctx=[ql, 100, 256, 700, 1500],
+                     sliding_window=window, per_token=True, seed=51 + ql)
+    P = plan.sw_partition_count(window, query_length=ql) if window else 6
+    es_r, ml_r, to_r = slot_partials(case, P)
+    _, _, (es, ml, to) = launch(to_dev(case), P=P, partials=True, tmp_dtype=torch.float32)
+    es, ml, to = es.cpu().double(), ml.cpu().double(), to.cpu().double()
+    empty = torch.isinf(ml_r)
+    assert torch.equal(torch.isinf(ml), empty), "non-empty slot set differs"
+    assert bool((es[empty] == 0).all()) and bool((to[empty.unsqueeze(-1).expand_as(to)] == 0).all())
+    full = ~empty
+    torch.testing.assert_close(ml[full], ml_r[full], atol=1e-2, rtol=0)
+    # exp_sums are relative to the slot max: compare the product s * e^m
+    torch.testing.assert_close(es[full] * torch.exp(ml[full] - ml_r[full]), es_r[full], rtol=2e-2, atol=1e-3)
+    torch.testing.assert_close(to[full.unsqueeze(-1).expand_as(to)], to_r[full.unsqueeze(-1).expand_as(to_r)],
+                               atol=ATOL, rtol=RTOL)
+
+
+def test_graph_capture_replays_match_eager():
+    case = to_dev(make_case(batch=4, ctx_range=(1, 2000), seed=61))
+    b = case["context_lengths"].shape[0]
+    P = 8
+    es = torch.empty((b, 2, P, 4), device=DEV)
+    ml = torch.empty_like(es)
+    to = torch.empty((b, 2, P, 4, 128), device=DEV, dtype=torch.bfloat16)
+    out = torch.empty(case["query"].shape, dtype=torch.bfloat16, device=DEV)
+
+    def call():
+        pa_decode_ps_launch(out, case["query"], case["key_cache"], case["value_cache"], case["context_lengths"],
+                            None, None, case["softmax_scale"], case["key_scale"], case["value_scale"],
+                            block_tables=case["block_tables"], max_context_partition_num=P, exp_sums=es,
+                            max_logits=ml, temporary_output=to)
+
+    call()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            call()
+    torch.cuda.current_stream().wait_stream(s)
+    for i in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        call()  # eager work between replays
+        torch.cuda.synchronize()
+
+
+def _subcase(case, seqs):
+    """Compact CPU copy of a few sequences (their pages only) for the oracle."""
+    bs = case["key_cache"].shape[-2]
+    ctx = case["context_lengths"].cpu()
+    bt = case["block_tables"].cpu()
+    ql = case["query_length"]
+    pages, rows = [], []
+    for b in seqs:
+        n = math.ceil(int(ctx[b]) / bs)
+        rows.append(list(range(len(pages), len(pages) + n)))
+        pages.extend(bt[b, :n].tolist())
+    idx = torch.tensor(pages, dtype=torch.long, device=case["key_cache"].device)
+    width = max(len(r) for r in rows)
+    sub = dict(case)
+    sub["key_cache"] = case["key_cache"].index_select(0, idx).cpu()
+    sub["value_cache"] = case["value_cache"].index_select(0, idx).cpu()
+    if case["key_scale"].dim() > 1:
+        sub["key_scale"] = case["key_scale"].index_select(0, idx).cpu()
+        sub["value_scale"] = case["value_scale"].index_select(0, idx).cpu()
+    else:
+        sub["key_scale"] = case["key_scale"].cpu()
+        sub["value_scale"] = case["value_scale"].cpu()
+    sub["block_tables"] = torch.tensor([r + [0] * (width - len(r)) for r in rows], dtype=torch.int32)
+    sub["context_lengths"] = ctx[list(seqs)].to(torch.int32)
+    sub["query"] = torch.cat([case["query"][b * ql : (b + 1) * ql].cpu() for b in seqs])
+    return sub
+
+
+@pytest.mark.parametrize("name", ["c2_llama8b", "c3_ragged", "c4_window", "c5_mtp"])
+def test_benchmark_config_full_size(name):
+    """Full BASELINE shapes on the GPU; oracle on a sample of sequences
+    (first, last, longest, shortest and a seeded random few)."""
+    cfg = workloads.CONFIGS[name]
+    print(f"[full-size] {name}: building inputs", flush=True)
+    case = workloads.build_inputs(cfg, device=DEV, seed=7)
+    out, route, _ = launch(case)
+    assert not torch.isnan(out).any()
+    ctx = case["context_lengths"].cpu()
+    g = torch.Generator().manual_seed(0)
+    pick = {0, cfg.batch - 1, int(ctx.argmax()), int(ctx.argmin())}
+    pick |= set(torch.randint(0, cfg.batch, (6,), generator=g).tolist())
+    seqs = sorted(pick)
+    sub = _subcase(case, seqs)
+    ref = torch_oracle(sub, float_out=False)
+    ql = cfg.query_length
+    got = torch.cat([out[b * ql : (b + 1) * ql].cpu() for b in seqs])
+    assert_parity(got, ref, f"{name} seqs={seqs}")
