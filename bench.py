@@ -11,9 +11,11 @@ rotate over several independent KV-cache copies whose total exceeds twice
 the 256 MB Infinity Cache, so no step reads KV that the previous step left
 in the cache.  ``value`` = attended K+V bytes / step time.
 
-``roofline`` is measured live: the partition kernel alone is launched K
-times through the C ABI between HIP events on the stream it runs on; its
-algorithmic bytes per launch / average duration is ``achieved``.
+``roofline`` is measured live: the decode kernel (partition pass with the
+in-kernel log-sum-exp merge, the only kernel of a step) is launched K times
+through the C ABI with pre-marshalled arguments between HIP events on the
+stream it runs on; algorithmic bytes per launch / average duration is
+``achieved``.
 ``traffic`` (HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE,
 scaled by a copy-kernel calibration) is read from profiles/ when present.
 
@@ -51,7 +53,23 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     p.add_argument("--copies", type=int, default=0, help="KV-cache copies to rotate (0 = auto)")
+    p.add_argument("--partitions", type=int, default=0, help="override max_context_partition_num (0 = heuristic)")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="instead of decoding, run a plain device copy of MIB MiB (--steps times): the "
+                        "reference point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
     return p.parse_args()
+
+
+def copy_calibration(mib: int, steps: int) -> None:
+    import torch
+
+    n = mib * 1024 * 1024
+    src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read_per_launch": n, "bytes_written_per_launch": n, "launches": steps}))
 
 
 def cpu_model() -> str:
@@ -134,7 +152,7 @@ def load_traffic(name: str):
 def run_config(name: str, args) -> dict:
     import torch
 
-    from flydsl_amd import _lib, get_recommended_splits, pa_decode_ps_launch, workloads
+    from flydsl_amd import get_recommended_splits, pa_decode_ps_launch, prepare_pa_decode, workloads
 
     cfg = workloads.CONFIGS[name]
     dev = torch.device("cuda:0")
@@ -155,6 +173,8 @@ def run_config(name: str, args) -> dict:
         P = get_recommended_splits(B, hkv, sliding_window=cfg.sliding_window, query_length=ql)
     else:
         P = get_recommended_splits(B, hkv, split_kv_blocks=max(1, 256 // cfg.block_size))
+    if args.partitions:
+        P = args.partitions
     es = torch.empty((B, hkv, P, eq), device=dev)
     ml = torch.empty_like(es)
     tmp = torch.empty((B, hkv, P, eq, 128), device=dev, dtype=torch.bfloat16)
@@ -181,44 +201,26 @@ def run_config(name: str, args) -> dict:
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / args.steps
 
-    # Live per-kernel timing of the partition pass (the dominant kernel),
-    # launched through the C ABI on this same stream.
-    lib = _lib.load()
-    pargs = []
+    # Live per-kernel timing of the decode kernel (the dominant and, with
+    # the in-kernel slot merge, the only kernel of a step), launched through
+    # the C ABI with pre-marshalled arguments on this same stream.
+    calls = []
     for k, v, ks, vs in caches:
-        a = _lib.PartitionArgs()
-        a.abi_version = _lib.ABI_VERSION
-        a.exp_sums, a.max_logits, a.tmp_out = es.data_ptr(), ml.data_ptr(), tmp.data_ptr()
-        a.query, a.key_cache, a.value_cache = case["query"].data_ptr(), k.data_ptr(), v.data_ptr()
-        a.block_tables, a.context_lengths = case["block_tables"].data_ptr(), case["context_lengths"].data_ptr()
-        a.key_scale, a.value_scale = ks.data_ptr(), vs.data_ptr()
-        a.stride_q_tok, a.stride_q_head = case["query"].stride(0), case["query"].stride(1)
-        a.stride_k_block, a.stride_k_head = k.stride(0), k.stride(1)
-        a.stride_v_block, a.stride_v_head = v.stride(0), v.stride(1)
-        a.stride_es_seq, a.stride_es_head, a.stride_es_part = es.stride()[:3]
-        a.stride_to_seq, a.stride_to_head, a.stride_to_part, a.stride_to_group = tmp.stride()[:4]
-        a.stride_bt_seq = case["block_tables"].stride(0)
-        if ks.dim() > 1:
-            a.stride_ks_block, a.stride_ks_head = ks.stride(0), ks.stride(1)
-        a.num_seqs, a.num_kv_heads, a.num_partitions = B, hkv, P
-        a.query_length, a.query_group_size, a.head_size = ql, cfg.gqa, 128
-        a.block_size, a.num_blocks = cfg.block_size, k.shape[0]
-        a.max_blocks_per_seq = case["block_tables"].shape[1]
-        a.sliding_window, a.per_token_kv, a.trans_v = cfg.sliding_window, int(ks.dim() > 1), 1
-        a.query_dtype, a.tmp_dtype = _lib.DTYPE_BF16, _lib.DTYPE_BF16
-        a.softmax_scale = case["softmax_scale"]
-        pargs.append(a)
-    sh = ctypes.c_void_p(stream.cuda_stream)
+        calls.append(prepare_pa_decode(out, case["query"], k, v, case["context_lengths"], None, None,
+                                       case["softmax_scale"], ks, vs, sliding_window=cfg.sliding_window,
+                                       block_tables=case["block_tables"], max_context_partition_num=P,
+                                       exp_sums=es, max_logits=ml, temporary_output=tmp))
     for i in range(max(3, args.warmup)):
-        _lib.check(lib.pa_fp8_decode_partition(ctypes.byref(pargs[i % copies]), sh), "partition")
+        calls[i % copies].launch()
     k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     k0.record(stream)
     for i in range(args.steps):
-        lib.pa_fp8_decode_partition(ctypes.byref(pargs[i % copies]), sh)
+        calls[i % copies].launch()
     k1.record(stream)
     torch.cuda.synchronize()
     kern_ms = k0.elapsed_time(k1) / args.steps
+    kernels_per_step = 1 if calls[0]._ra is None else 2
 
     achieved = kv / (kern_ms * 1e-3) / 1e9
     value = kv / (ms * 1e-3) / 1e9
@@ -257,7 +259,8 @@ def run_config(name: str, args) -> dict:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "pa_fp8_partition_kernel",
+            "kernel": "pa_fp8_partition_kernel (slot partials + in-kernel LSE merge)",
+            "kernels_per_step": kernels_per_step,
             "achieved": round(achieved, 2),
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
@@ -281,6 +284,9 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU; --gpus N > 1 is not supported "
                                    "(the decode path shards by sequence / kv head with no communication)"}))
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration, args.steps)
+        return
     names = ["c2_llama8b", "c3_ragged", "c4_window", "c5_mtp"] if args.config == "all" else [args.config]
     for n in names:
         line = run_config(n, args)

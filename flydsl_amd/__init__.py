@@ -8,9 +8,18 @@ kernels of ``libpa_fp8.so`` (C ABI: ``include/pa_fp8.h``).
 
 from .pa_decode import (  # noqa: F401
     KV_COMPUTE_BLOCK,
+    PreparedDecode,
     get_pa_metadata,
     get_recommended_splits,
     pa_decode_ps_launch,
+    prepare_pa_decode,
 )
 
-__all__ = ["pa_decode_ps_launch", "get_recommended_splits", "get_pa_metadata", "KV_COMPUTE_BLOCK"]
+__all__ = [
+    "pa_decode_ps_launch",
+    "get_recommended_splits",
+    "get_pa_metadata",
+    "prepare_pa_decode",
+    "PreparedDecode",
+    "KV_COMPUTE_BLOCK",
+]

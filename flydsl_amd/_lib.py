@@ -54,6 +54,7 @@ class PartitionArgs(ctypes.Structure):
         ("max_logits", _vp),
         ("tmp_out", _vp),
         ("output", _vp),
+        ("counters", _vp),
         ("query", _vp),
         ("key_cache", _vp),
         ("value_cache", _vp),
@@ -142,7 +143,7 @@ def load(path: Optional[str] = None) -> ctypes.CDLL:
     global _LIB
     if _LIB is not None and path is None:
         return _LIB
-    p = path or LIB_PATH
+    p = path or os.environ.get("PA_FP8_LIB") or LIB_PATH
     if not os.path.exists(p):
         raise LibraryNotBuilt(
             f"{p} is missing: build the HIP library first (python -c 'import __graft_entry__ as g; g.build()')"

@@ -45,11 +45,24 @@ typedef int i32x2 __attribute__((ext_vector_type(2)));
 
 #define LDS_AS __attribute__((address_space(3)))
 
-constexpr int kWaves = 4;
+// LDS ring depth per wave (chunks); each stage holds one chunk's K and V.
+#ifndef PA_FP8_STAGES
+#define PA_FP8_STAGES 2
+#endif
+constexpr int kStages = PA_FP8_STAGES;
+// Waves per workgroup (each streams its own chunks of the slot).
+#ifndef PA_FP8_WAVES
+#define PA_FP8_WAVES 4
+#endif
+constexpr int kWaves = PA_FP8_WAVES;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kHead = 128;
 constexpr int kChunk = 32;                  // tokens per wave step
-constexpr int kKBytes = kChunk * kHead;     // fp8 keys of one chunk
+// Key image of one chunk in LDS: two 16-token halves, each [8 dim chunks]
+// [16 tokens][16 B]; the second half sits 64 B past a 2 KiB boundary so the
+// two halves map to different LDS banks.
+constexpr int kKHalf = 2048 + 64;
+constexpr int kKBytes = 2 * kKHalf;         // fp8 keys of one chunk (+ pad)
 constexpr int kVBytes = kChunk * kHead;     // fp8 values of one chunk
 constexpr int kScaleBytes = 2 * kChunk * 4; // per-token K and V scales
 constexpr float kLn2 = 0.69314718055994531f;
@@ -106,8 +119,48 @@ __device__ __forceinline__ f32x4 mfma_fp8(long a, long b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(a, b, c, 0, 0, 0);
 }
 
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+// v_mfma_f32_16x16x128_f8f6f4 with both operands e4m3fn and unit scales:
+// lane l holds 32 k-values of row (A) / column (B) l % 16.
+__device__ __forceinline__ f32x4 mfma_fp8_k128(i32x8 a, i32x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// Reductions over the four lanes l, l^16, l^32, l^48 (one query column
+// across the four 16-lane groups) with gfx950 permlane swaps (VALU only).
+__device__ __forceinline__ float max_over_groups(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_over_groups(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ void lds_dma16(const void* gsrc, LDS_AS void* ldst) {
   __builtin_amdgcn_global_load_lds(gsrc, ldst, 16, 0, 0);
+}
+
+// Device-coherent (agent scope) 32-bit accesses: sc1 stores write through
+// this XCD's L2 and sc1 loads do not hit stale lines, so slot partials can
+// be handed between workgroups on different XCDs within one launch without
+// cache-wide writeback / invalidate fences.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t load_agent(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // s_waitcnt immediate (gfx9 encoding) that waits for vmcnt <= n only:
@@ -115,51 +168,140 @@ __device__ __forceinline__ void lds_dma16(const void* gsrc, LDS_AS void* ldst) {
 // their maxima (7 and 15) so they are not waited on.
 constexpr int vmcnt_only(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | (7 << 4) | (15 << 8); }
 
-// Write one slot's outputs for query column e (8 head dims per thread call).
-__device__ __forceinline__ void store_partial8(const pa_fp8_partition_args& a, bool fused, int b, int h, int slot,
-                                               int e, int d0, const float* v) {
-  if (fused) {
-    const int gqa = a.query_group_size;
-    const int qi = e / gqa, g = e - qi * gqa;
-    const int64_t off = (int64_t)(b * a.query_length + qi) * a.stride_out_tok +
-                        (int64_t)(h * gqa + g) * a.stride_out_head + d0;
-    if (a.output_dtype == PA_DTYPE_F32) {
-      f32x4* p = (f32x4*)((float*)a.output + off);
-      p[0] = f32x4{v[0], v[1], v[2], v[3]};
-      p[1] = f32x4{v[4], v[5], v[6], v[7]};
-    } else {
-      const bool bf = a.output_dtype == PA_DTYPE_BF16;
-      uint32_t w[4];
+// Store 8 head dims of the final output row (sequence b, query column e of
+// kv head h) in the output dtype.
+__device__ __forceinline__ void store_output8(const pa_fp8_partition_args& a, int b, int h, int e, int d0,
+                                              const float* v) {
+  const int gqa = a.query_group_size;
+  const int qi = e / gqa, g = e - qi * gqa;
+  const int64_t off = (int64_t)(b * a.query_length + qi) * a.stride_out_tok + (int64_t)(h * gqa + g) * a.stride_out_head + d0;
+  if (a.output_dtype == PA_DTYPE_F32) {
+    f32x4* p = (f32x4*)((float*)a.output + off);
+    p[0] = f32x4{v[0], v[1], v[2], v[3]};
+    p[1] = f32x4{v[4], v[5], v[6], v[7]};
+  } else {
+    const bool bf = a.output_dtype == PA_DTYPE_BF16;
+    uint32_t w[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t lo16 = bf ? f32_to_bf16_bits(v[2 * i]) : f32_to_f16_bits(v[2 * i]);
-        uint32_t hi16 = bf ? f32_to_bf16_bits(v[2 * i + 1]) : f32_to_f16_bits(v[2 * i + 1]);
-        w[i] = lo16 | (hi16 << 16);
-      }
-      *(i32x4*)((uint16_t*)a.output + off) = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo16 = bf ? f32_to_bf16_bits(v[2 * i]) : f32_to_f16_bits(v[2 * i]);
+      const uint32_t hi16 = bf ? f32_to_bf16_bits(v[2 * i + 1]) : f32_to_f16_bits(v[2 * i + 1]);
+      w[i] = lo16 | (hi16 << 16);
     }
+    *(i32x4*)((uint16_t*)a.output + off) = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+  }
+}
+
+// Write one slot's outputs for query column e (8 head dims per thread call).
+__device__ __forceinline__ void store_partial8(const pa_fp8_partition_args& a, bool fused, bool coherent, int b,
+                                               int h, int slot, int e, int d0, const float* v) {
+  if (fused) {
+    store_output8(a, b, h, e, d0, v);
     return;
   }
   const int64_t off = (int64_t)b * a.stride_to_seq + (int64_t)h * a.stride_to_head +
                       (int64_t)slot * a.stride_to_part + (int64_t)e * a.stride_to_group + d0;
   if (a.tmp_dtype == PA_DTYPE_F32) {
-    f32x4* p = (f32x4*)((float*)a.tmp_out + off);
-    p[0] = f32x4{v[0], v[1], v[2], v[3]};
-    p[1] = f32x4{v[4], v[5], v[6], v[7]};
+    float* p = (float*)a.tmp_out + off;
+    if (coherent) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) store_agent(p + i, v[i]);
+    } else {
+      ((f32x4*)p)[0] = f32x4{v[0], v[1], v[2], v[3]};
+      ((f32x4*)p)[1] = f32x4{v[4], v[5], v[6], v[7]};
+    }
   } else {
     uint32_t w[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) w[i] = f32_to_bf16_bits(v[2 * i]) | (f32_to_bf16_bits(v[2 * i + 1]) << 16);
-    *(i32x4*)((uint16_t*)a.tmp_out + off) = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    uint32_t* p = (uint32_t*)((uint16_t*)a.tmp_out + off);
+    if (coherent) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) store_agent(p + i, w[i]);
+    } else {
+      *(i32x4*)p = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    }
   }
 }
 
-__device__ __forceinline__ void store_stats(const pa_fp8_partition_args& a, int b, int h, int slot, int e,
-                                            float exp_sum, float max_logit) {
+__device__ __forceinline__ void store_stats(const pa_fp8_partition_args& a, bool coherent, int b, int h, int slot,
+                                            int e, float exp_sum, float max_logit) {
   const int64_t off = (int64_t)b * a.stride_es_seq + (int64_t)h * a.stride_es_head +
                       (int64_t)slot * a.stride_es_part + e;
-  a.exp_sums[off] = exp_sum;
-  a.max_logits[off] = max_logit;
+  if (coherent) {
+    store_agent(a.exp_sums + off, exp_sum);
+    store_agent(a.max_logits + off, max_logit);
+  } else {
+    a.exp_sums[off] = exp_sum;
+    a.max_logits[off] = max_logit;
+  }
+}
+
+// Log-sum-exp merge of the P slots of (sequence b, kv head h), run by the
+// workgroup that finished last (same math as pa_fp8_lse_reduce_kernel).
+__device__ void merge_slots(const pa_fp8_partition_args& a, int b, int h, int tid, int nthreads) {
+  const int eq = a.query_length * a.query_group_size;
+  const int P = a.num_partitions;
+  for (int idx = tid; idx < eq * (kHead / 8); idx += nthreads) {
+    const int e = idx / (kHead / 8);
+    const int d0 = (idx % (kHead / 8)) * 8;
+    const int64_t sb = (int64_t)b * a.stride_es_seq + (int64_t)h * a.stride_es_head + e;
+    const int64_t tb0 = (int64_t)b * a.stride_to_seq + (int64_t)h * a.stride_to_head + (int64_t)e * a.stride_to_group + d0;
+    float M = kNegInf;
+    for (int p = 0; p < P; ++p) M = fmaxf(M, load_agent(a.max_logits + sb + p * a.stride_es_part));
+    float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (M != kNegInf) {
+      float tot = 0.0f;
+#pragma unroll 4
+      for (int p = 0; p < P; ++p) {
+        const float m = load_agent(a.max_logits + sb + p * a.stride_es_part);
+        const float w = m == kNegInf ? 0.0f : load_agent(a.exp_sums + sb + p * a.stride_es_part) * __expf(m - M);
+        tot += w;
+        float x[8];
+        if (a.tmp_dtype == PA_DTYPE_F32) {
+          const float* t = (const float*)a.tmp_out + tb0 + p * a.stride_to_part;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) x[i] = load_agent(t + i);
+        } else {
+          const uint32_t* t = (const uint32_t*)((const uint16_t*)a.tmp_out + tb0 + p * a.stride_to_part);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t u = load_agent(t + i);
+            x[2 * i] = bf16_bits_to_f32(u & 0xffffu);
+            x[2 * i + 1] = bf16_bits_to_f32(u >> 16);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] += w * x[i];
+      }
+      const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] *= inv;
+    }
+    store_output8(a, b, h, e, d0, o);
+  }
+}
+
+// Arrival of one slot of (b, h).  Every workgroup publishes its partials
+// (release at agent scope, so they reach memory past this XCD's L2) and
+// bumps the counter; the one that brings it to P acquires, merges all P
+// partials into the output and zeroes the counter for the next launch.
+__device__ __forceinline__ void arrive_and_merge(const pa_fp8_partition_args& a, int b, int h, int tid,
+                                                 int nthreads, int* s_flag) {
+  // The partials were written with device-coherent stores; wait until every
+  // wave's stores have completed before the slot is counted as arrived.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    const int old = __hip_atomic_fetch_add(&a.counters[b * a.num_kv_heads + h], 1, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = old == a.num_partitions - 1;
+  }
+  __syncthreads();
+  if (*s_flag) {
+    merge_slots(a, b, h, tid, nthreads);
+    if (tid == 0) __hip_atomic_store(&a.counters[b * a.num_kv_heads + h], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // Block table, context lengths and scales come in as separate restrict
@@ -197,7 +339,11 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
   const int eq = ql * gqa;
   const int W = a.sliding_window;
   const int ctx = context_lengths[b];
-  const bool fused = a.output != nullptr;
+  // direct: one slot writes the final output itself; merge: slots write
+  // partials and the last one to finish merges them.
+  const bool fused = a.output != nullptr && P == 1;
+  const bool merge = a.output != nullptr && P > 1;
+  __shared__ int s_last;
 
   int t0, t1, lo_all, hi_all, unused;
   pa_plan_slot_tokens(ctx, P, slot, W, ql, &t0, &t1);
@@ -214,74 +360,32 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
     const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int idx = tid; idx < eq * (kHead / 8); idx += kThreads) {
       const int e = idx / (kHead / 8);
-      store_partial8(a, fused, b, h, slot, e, (idx % (kHead / 8)) * 8, z);
+      store_partial8(a, fused, merge, b, h, slot, e, (idx % (kHead / 8)) * 8, z);
     }
     if (!fused)
-      for (int e = tid; e < eq; e += kThreads) store_stats(a, b, h, slot, e, 0.0f, kNegInf);
+      for (int e = tid; e < eq; e += kThreads) store_stats(a, merge, b, h, slot, e, 0.0f, kNegInf);
+    if (merge) arrive_and_merge(a, b, h, tid, kThreads, &s_last);
     return;
   }
 
-  // ---------------- query: load, scale, split into fp8 hi + lo ----------------
-  long qhi[NCG][4], qlo[NCG][4];
-  float qfac[NCG];   // base-2 logit factor per column
-  int vis_lo[NCG], vis_hi[NCG];
-  const float k_tensor_scale = PER_TOKEN ? 1.0f : key_scale[0];
+  // ---------------- query: raw loads (issued before the first KV chunk) ----------------
+  i32x4 qraw[NCG][4];
 #pragma unroll
   for (int cg = 0; cg < NCG; ++cg) {
     const int e = cg * 16 + c16;
-    const bool valid = e < eq;
-    float v[32];
-    int qi = 0;
-    if (valid) {
-      qi = e / gqa;
+    if (e < eq) {
+      const int qi = e / gqa;
       const int g = e - qi * gqa;
       const uint16_t* qp = (const uint16_t*)a.query + (int64_t)(b * ql + qi) * a.stride_q_tok +
                            (int64_t)(h * gqa + g) * a.stride_q_head;
-      i32x4 x[4];
-      x[0] = *(const i32x4*)(qp + 16 * grp);
-      x[1] = *(const i32x4*)(qp + 16 * grp + 8);
-      x[2] = *(const i32x4*)(qp + 16 * (grp + 4));
-      x[3] = *(const i32x4*)(qp + 16 * (grp + 4) + 8);
-      if (a.query_dtype == PA_DTYPE_F16) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const uint32_t w = (uint32_t)x[i >> 2][i & 3];
-          v[2 * i] = f16_bits_to_f32(w & 0xffffu);
-          v[2 * i + 1] = f16_bits_to_f32(w >> 16);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const uint32_t w = (uint32_t)x[i >> 2][i & 3];
-          v[2 * i] = bf16_bits_to_f32(w & 0xffffu);
-          v[2 * i + 1] = bf16_bits_to_f32(w >> 16);
-        }
-      }
+      qraw[cg][0] = *(const i32x4*)(qp + 16 * grp);
+      qraw[cg][1] = *(const i32x4*)(qp + 16 * grp + 8);
+      qraw[cg][2] = *(const i32x4*)(qp + 16 * (grp + 4));
+      qraw[cg][3] = *(const i32x4*)(qp + 16 * (grp + 4) + 8);
     } else {
 #pragma unroll
-      for (int i = 0; i < 32; ++i) v[i] = 0.0f;
+      for (int i = 0; i < 4; ++i) qraw[cg][i] = i32x4{0, 0, 0, 0};
     }
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    amax = fmaxf(amax, shfl_xor(amax, 16));
-    amax = fmaxf(amax, shfl_xor(amax, 32));
-    // Power-of-two scale putting amax into [128, 256): exact in fp32.
-    int sexp = 261 - (int)((__float_as_uint(amax) >> 23) & 0xffu);
-    sexp = sexp < 1 ? 1 : (sexp > 254 ? 254 : sexp);
-    const float sq = amax > 0.0f ? __uint_as_float((uint32_t)sexp << 23) : 1.0f;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      float xs[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) xs[i] = v[8 * s + i] * sq;
-      split8_fp8(xs, qhi[cg][s], qlo[cg][s]);
-    }
-    qfac[cg] = a.softmax_scale * kLog2e * k_tensor_scale / sq;
-    int lo = 0, hi = 0;
-    if (valid) pa_plan_visible(ctx, qi, ql, W, &lo, &hi);
-    vis_lo[cg] = lo;
-    vis_hi[cg] = hi;
   }
 
   // ---------------- stream this wave's chunks ----------------
@@ -317,11 +421,15 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
 
   LDS_AS unsigned char* ring = (LDS_AS unsigned char*)smem + wave * kWaveBytes;
 
-  // Token order inside a chunk's LDS key image: slot r (0..15) of half t
-  // holds chunk token 8*(r/4) + 4*t + r%4, so 16-row tile t of the QK
-  // product reads slots 16t .. 16t+15 contiguously.
-  const int kslot = lane & 31;
-  const int ktok = 8 * ((kslot & 15) >> 2) + 4 * (kslot >> 4) + (kslot & 3);
+  // Per-lane byte offsets of the direct-to-LDS loads.  Every load
+  // instruction reads from a single page, so its address is a wave-uniform
+  // page base plus one of these constants.  Lane l of a 1 KiB load fills
+  // LDS bytes 16l .. 16l+15 of its destination.
+  //   keys   : (16-dim chunk 4q + l/16, token l%16) of a 16-token half
+  //   values : trans layout -> bytes 16l of a [head dim][16 tokens] group;
+  //            plain layout -> head dim 64q + l, 16 tokens
+  const int koff_lane = BS16 ? lane * 16 : (lane >> 4) * (bs * 16) + (lane & 15) * 16;
+  const int voff_plain = lane * bs;
 
   auto issue = [&](int k, int st, int raw0, int raw1) {
     const int p0 = clamp_page(raw0);
@@ -329,44 +437,47 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
     const int tb = cbeg + (wave + k * kWaves) * kChunk;
     LDS_AS unsigned char* sk = ring + st * kStageBytes;
     LDS_AS unsigned char* sv = sk + kKBytes;
-    const int s0 = BS16 ? 0 : (tb & (bs - 1));
-    // keys: 4 x 1 KiB; lane -> (16-dim chunk c, token)
+    if (BS16) {
 #pragma unroll
-    for (int ii = 0; ii < 4; ++ii) {
-      const int c = 2 * ii + (lane >> 5);
-      const uint8_t* src;
-      if (BS16) {
-        const int pg = ktok >= 16 ? p1 : p0;
-        src = kbase + (int64_t)pg * a.stride_k_block + c * 256 + (ktok & 15) * 16;
-      } else {
-        src = kbase + (int64_t)p0 * a.stride_k_block + c * (bs * 16) + (s0 + ktok) * 16;
-      }
-      lds_dma16(src, sk + ii * 1024);
-    }
-    // values: 4 x 1 KiB; LDS image [16-token group][head dim][16 tokens]
+      for (int hh = 0; hh < 2; ++hh) {
+        const uint8_t* kp = kbase + (int64_t)(hh ? p1 : p0) * a.stride_k_block;
+        const uint8_t* vp = vbase + (int64_t)(hh ? p1 : p0) * a.stride_v_block;
 #pragma unroll
-    for (int ii = 0; ii < 4; ++ii) {
-      const int off = ii * 1024 + lane * 16;
-      const int tg = off >> 11;
-      const int hd = (off >> 4) & (kHead - 1);
-      const uint8_t* src;
-      if (BS16) {
-        src = vbase + (int64_t)(tg ? p1 : p0) * a.stride_v_block + hd * 16;
-      } else {
-        const int s = s0 + 16 * tg;
-        src = a.trans_v ? vbase + (int64_t)p0 * a.stride_v_block + (s >> 4) * (kHead * 16) + hd * 16
-                        : vbase + (int64_t)p0 * a.stride_v_block + hd * bs + s;
+        for (int q = 0; q < 2; ++q) lds_dma16(kp + koff_lane + q * 1024, sk + hh * kKHalf + q * 1024);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) lds_dma16(vp + lane * 16 + q * 1024, sv + hh * 2048 + q * 1024);
       }
-      lds_dma16(src, sv + ii * 1024);
+    } else {
+      const int s0 = tb & (bs - 1);
+      const uint8_t* kp = kbase + (int64_t)p0 * a.stride_k_block + s0 * 16;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+          lds_dma16(kp + hh * 256 + q * (4 * bs * 16) + koff_lane, sk + hh * kKHalf + q * 1024);
+      if (a.trans_v) {
+        const uint8_t* vp = vbase + (int64_t)p0 * a.stride_v_block + (s0 >> 4) * (kHead * 16);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int q = 0; q < 2; ++q) lds_dma16(vp + hh * 2048 + q * 1024 + lane * 16, sv + hh * 2048 + q * 1024);
+      } else {
+        const uint8_t* vp = vbase + (int64_t)p0 * a.stride_v_block + s0;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int q = 0; q < 2; ++q)
+            lds_dma16(vp + hh * 16 + q * (64 * bs) + voff_plain, sv + hh * 2048 + q * 1024);
+      }
     }
     if (PER_TOKEN) {
       LDS_AS unsigned char* ss = sv + kVBytes;
       if (lane < 16) {
         const int tt = (lane & 7) * 4;
         const int pg = BS16 ? (tt >= 16 ? p1 : p0) : p0;
-        const int s = BS16 ? (tt & 15) : s0 + tt;
+        const int sidx = BS16 ? (tt & 15) : (tb & (bs - 1)) + tt;
         const float* base = lane < 8 ? ksbase : vsbase;
-        lds_dma16(base + (int64_t)pg * a.stride_ks_block + s, ss);
+        lds_dma16(base + (int64_t)pg * a.stride_ks_block + sidx, ss);
       }
     }
   };
@@ -394,6 +505,75 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
     }
   if (STAGES - 1 < nmine) fetch_pages(STAGES - 1, np0, np1);
 
+  // ---------------- query: scale, split into fp8 hi + lo ----------------
+  // B operand of the 16x16x128 QK product: lane (grp, c) holds the 32 head
+  // dims of 16-dim chunks grp and grp+4 of column c, in the byte order of
+  // the key rows read below.
+  i32x8 qhi8[NCG], qlo8[NCG];
+  float qfac[NCG];   // base-2 logit factor per column
+  int vis_lo[NCG], vis_hi[NCG];
+  const float k_tensor_scale = PER_TOKEN ? 1.0f : key_scale[0];
+#pragma unroll
+  for (int cg = 0; cg < NCG; ++cg) {
+    const int e = cg * 16 + c16;
+    const bool valid = e < eq;
+    const int qi = valid ? e / gqa : 0;
+    float v[32];
+    if (a.query_dtype == PA_DTYPE_F16) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t w = (uint32_t)qraw[cg][i >> 2][i & 3];
+        v[2 * i] = f16_bits_to_f32(w & 0xffffu);
+        v[2 * i + 1] = f16_bits_to_f32(w >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t w = (uint32_t)qraw[cg][i >> 2][i & 3];
+        v[2 * i] = bf16_bits_to_f32(w & 0xffffu);
+        v[2 * i + 1] = bf16_bits_to_f32(w >> 16);
+      }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = max_over_groups(amax);
+    // Power-of-two scale putting amax into [128, 256): exact in fp32.
+    int sexp = 261 - (int)((__float_as_uint(amax) >> 23) & 0xffu);
+    sexp = sexp < 1 ? 1 : (sexp > 254 ? 254 : sexp);
+    const float sq = amax > 0.0f ? __uint_as_float((uint32_t)sexp << 23) : 1.0f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      float xs[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xs[i] = v[8 * s + i] * sq;
+      long hi, lo;
+      split8_fp8(xs, hi, lo);
+      qhi8[cg][2 * s] = (int)(uint32_t)hi;
+      qhi8[cg][2 * s + 1] = (int)(uint32_t)((uint64_t)hi >> 32);
+      qlo8[cg][2 * s] = (int)(uint32_t)lo;
+      qlo8[cg][2 * s + 1] = (int)(uint32_t)((uint64_t)lo >> 32);
+    }
+    qfac[cg] = a.softmax_scale * kLog2e * k_tensor_scale / sq;
+    int lo = 0, hi = 0;
+    if (valid) pa_plan_visible(ctx, qi, ql, W, &lo, &hi);
+    vis_lo[cg] = lo;
+    vis_hi[cg] = hi;
+  }
+  // Chunks inside [lo_max, hi_min) are visible to every query column: no
+  // masking there.  lo grows and hi grows with qi, so the extremes come
+  // from the last and the first query.
+  int lo_max, hi_min;
+  {
+    int t0q, t1q;
+    pa_plan_visible(ctx, ql - 1, ql, W, &lo_max, &t1q);
+    pa_plan_visible(ctx, 0, ql, W, &t0q, &hi_min);
+  }
+
+  // Key row r of QK tile t (0, 1) is chunk token 8*(r/4) + 4t + r%4: that
+  // token's 16-byte pieces for dim chunks grp and grp+4.
+  const int krow = (c16 >> 3) * kKHalf + (8 * ((c16 >> 2) & 1) + (c16 & 3)) * 16;
+
   for (int k = 0; k < nmine; ++k) {
     const int st = k % STAGES;
     if (k + STAGES - 1 < nmine) {
@@ -409,20 +589,12 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
     const LDS_AS unsigned char* sk = ring + st * kStageBytes;
     const LDS_AS unsigned char* sv = sk + kKBytes;
 
-    // key operands: tile 0 rows = slots 0..15, tile 1 rows = slots 16..31
-    i32x4 ka0 = *(const LDS_AS i32x4*)(sk + grp * 512 + c16 * 16);
-    i32x4 ka1 = *(const LDS_AS i32x4*)(sk + (grp + 4) * 512 + c16 * 16);
-    i32x4 kb0 = *(const LDS_AS i32x4*)(sk + grp * 512 + (16 + c16) * 16);
-    i32x4 kb1 = *(const LDS_AS i32x4*)(sk + (grp + 4) * 512 + (16 + c16) * 16);
-    long KA[4], KB[4];
-    KA[0] = (long)((uint64_t)(uint32_t)ka0[0] | ((uint64_t)(uint32_t)ka0[1] << 32));
-    KA[1] = (long)((uint64_t)(uint32_t)ka0[2] | ((uint64_t)(uint32_t)ka0[3] << 32));
-    KA[2] = (long)((uint64_t)(uint32_t)ka1[0] | ((uint64_t)(uint32_t)ka1[1] << 32));
-    KA[3] = (long)((uint64_t)(uint32_t)ka1[2] | ((uint64_t)(uint32_t)ka1[3] << 32));
-    KB[0] = (long)((uint64_t)(uint32_t)kb0[0] | ((uint64_t)(uint32_t)kb0[1] << 32));
-    KB[1] = (long)((uint64_t)(uint32_t)kb0[2] | ((uint64_t)(uint32_t)kb0[3] << 32));
-    KB[2] = (long)((uint64_t)(uint32_t)kb1[0] | ((uint64_t)(uint32_t)kb1[1] << 32));
-    KB[3] = (long)((uint64_t)(uint32_t)kb1[2] | ((uint64_t)(uint32_t)kb1[3] << 32));
+    const i32x4 ka0 = *(const LDS_AS i32x4*)(sk + krow + grp * 256);
+    const i32x4 ka1 = *(const LDS_AS i32x4*)(sk + krow + (grp + 4) * 256);
+    const i32x4 kb0 = *(const LDS_AS i32x4*)(sk + krow + 64 + grp * 256);
+    const i32x4 kb1 = *(const LDS_AS i32x4*)(sk + krow + 64 + (grp + 4) * 256);
+    const i32x8 KA = {ka0[0], ka0[1], ka0[2], ka0[3], ka1[0], ka1[1], ka1[2], ka1[3]};
+    const i32x8 KB = {kb0[0], kb0[1], kb0[2], kb0[3], kb1[0], kb1[1], kb1[2], kb1[3]};
 
     // value operands: head dim 16j + c16, tokens 8*grp .. 8*grp+7
     long V[8];
@@ -432,6 +604,7 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
 
     // This lane's 8 tokens: tb + 8*grp + j.
     const int tok0 = tb + 8 * grp;
+    const bool interior = tb >= lo_max && tb + kChunk <= hi_min;
     const bool edge = tb < lo_all || tb + kChunk > hi_all;
     if (edge) {
       // Zero value bytes of tokens no query sees (stale page tails).
@@ -453,7 +626,6 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
       f32x4 k1 = *(const LDS_AS f32x4*)(ss + 8 * grp + 4);
       f32x4 w0 = *(const LDS_AS f32x4*)(ss + 32 + 8 * grp);
       f32x4 w1 = *(const LDS_AS f32x4*)(ss + 32 + 8 * grp + 4);
-      float cmax = 0.0f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         ksc[j] = k0[j];
@@ -461,14 +633,17 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
         vsc[j] = w0[j];
         vsc[4 + j] = w1[j];
       }
+      if (edge) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int t = tok0 + j;
-        if (!(t >= lo_all && t < hi_all)) vsc[j] = 0.0f;
-        cmax = fmaxf(cmax, vsc[j]);
+        for (int j = 0; j < 8; ++j) {
+          const int t = tok0 + j;
+          if (!(t >= lo_all && t < hi_all)) vsc[j] = 0.0f;
+        }
       }
-      cmax = fmaxf(cmax, shfl_xor(cmax, 16));
-      cmax = fmaxf(cmax, shfl_xor(cmax, 32));
+      float cmax = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) cmax = fmaxf(cmax, vsc[j]);
+      cmax = max_over_groups(cmax);
       const float vnew = fmaxf(vsmax, cmax);
       vratio = vnew > 0.0f ? vsmax / vnew : 1.0f;
       vinv = vnew > 0.0f ? 1.0f / vnew : 0.0f;
@@ -477,42 +652,40 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
 
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg) {
-      f32x4 la = {0.f, 0.f, 0.f, 0.f}, lb = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        la = mfma_fp8(KA[s], qhi[cg][s], la);
-        lb = mfma_fp8(KB[s], qhi[cg][s], lb);
-      }
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        la = mfma_fp8(KA[s], qlo[cg][s], la);
-        lb = mfma_fp8(KB[s], qlo[cg][s], lb);
-      }
+      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+      f32x4 la = mfma_fp8_k128(KA, qhi8[cg], z);
+      f32x4 lb = mfma_fp8_k128(KB, qhi8[cg], z);
+      la = mfma_fp8_k128(KA, qlo8[cg], la);
+      lb = mfma_fp8_k128(KB, qlo8[cg], lb);
       float l[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         l[i] = la[i] * qfac[cg];
         l[4 + i] = lb[i] * qfac[cg];
       }
-      float cmax = kNegInf;
+      if (PER_TOKEN) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (PER_TOKEN) l[j] *= ksc[j];
-        const int t = tok0 + j;
-        l[j] = (t >= vis_lo[cg] && t < vis_hi[cg]) ? l[j] : kNegInf;
-        cmax = fmaxf(cmax, l[j]);
+        for (int j = 0; j < 8; ++j) l[j] *= ksc[j];
       }
-      cmax = fmaxf(cmax, shfl_xor(cmax, 16));
-      cmax = fmaxf(cmax, shfl_xor(cmax, 32));
+      if (!interior) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int t = tok0 + j;
+          l[j] = (t >= vis_lo[cg] && t < vis_hi[cg]) ? l[j] : kNegInf;
+        }
+      }
+      float cmax = fmaxf(fmaxf(fmaxf(l[0], l[1]), fmaxf(l[2], l[3])), fmaxf(fmaxf(l[4], l[5]), fmaxf(l[6], l[7])));
+      cmax = max_over_groups(cmax);
       const float mnew = fmaxf(m2[cg], cmax);
       const float muse = mnew == kNegInf ? 0.0f : mnew;
       const float alpha = __builtin_amdgcn_exp2f(m2[cg] - muse);
       m2[cg] = mnew;
       float p[8];
       float psum = 0.0f;
+      const float bias = 8.0f - muse;  // 256 * exp(l - m)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        p[j] = __builtin_amdgcn_exp2f(l[j] - muse + 8.0f);  // 256 * exp(l - m)
+        p[j] = __builtin_amdgcn_exp2f(l[j] + bias);
         psum += p[j];
       }
       lsum[cg] = lsum[cg] * alpha + psum;
@@ -535,12 +708,9 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
     }
   }
 
-  // ---------------- merge the four waves ----------------
+  // ---------------- merge the waves of the workgroup ----------------
 #pragma unroll
-  for (int cg = 0; cg < NCG; ++cg) {
-    lsum[cg] += shfl_xor(lsum[cg], 16);
-    lsum[cg] += shfl_xor(lsum[cg], 32);
-  }
+  for (int cg = 0; cg < NCG; ++cg) lsum[cg] = sum_over_groups(lsum[cg]);
   const float vfin = PER_TOKEN ? vsmax : value_scale[0];
   float* mbuf = (float*)smem;             // [wave][16]
   float* lbuf = mbuf + kWaves * 16;       // [wave][16]
@@ -563,8 +733,9 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
 #pragma unroll
       for (int i = 0; i < 4; ++i) abuf[(wave * kHead + 16 * j + 4 * grp + i) * 16 + c16] = acc[cg][j][i] * fself;
     __syncthreads();
-    const int col = tid >> 4;
-    const int d0 = (tid & 15) * 8;
+    for (int idx = tid; idx < 256; idx += kThreads) {
+    const int col = idx >> 4;
+    const int d0 = (idx & 15) * 8;
     const int e = cg * 16 + col;
     if (e < eq) {
       float Mc = kNegInf;
@@ -583,13 +754,18 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
         for (int w = 0; w < kWaves; ++w) s += abuf[(w * kHead + d0 + i) * 16 + col];
         o[i] = s * inv;
       }
-      store_partial8(a, fused, b, h, slot, e, d0, o);
-      if (!fused && (tid & 15) == 0) store_stats(a, b, h, slot, e, L * (1.0f / 256.0f), Mc * kLn2);
+      store_partial8(a, fused, merge, b, h, slot, e, d0, o);
+      if (!fused && (idx & 15) == 0) store_stats(a, merge, b, h, slot, e, L * (1.0f / 256.0f), Mc * kLn2);
+    }
     }
   }
+  if (merge) arrive_and_merge(a, b, h, tid, kThreads, &s_last);
 }
 
-// One wave per (sequence, kv head, column); lane covers head dims 2l, 2l+1.
+// One wave per (sequence, kv head, column); lane l covers head dims 2l,
+// 2l+1.  The slot statistics are read once, one slot per lane (up to 64
+// per pass), reduced across the wave, and every partial row is fetched
+// before any is used, so a row costs one round trip to memory per 64 slots.
 __global__ __launch_bounds__(256) void pa_fp8_lse_reduce_kernel(const pa_fp8_reduce_args a) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -601,29 +777,58 @@ __global__ __launch_bounds__(256) void pa_fp8_lse_reduce_kernel(const pa_fp8_red
   const int b = (int)(row / ((int64_t)eq * a.num_kv_heads));
   const int P = a.num_partitions;
   const int64_t sbase = (int64_t)b * a.stride_es_seq + (int64_t)h * a.stride_es_head + e;
+  const int64_t tbase =
+      (int64_t)b * a.stride_to_seq + (int64_t)h * a.stride_to_head + (int64_t)e * a.stride_to_group + 2 * lane;
+  // pass 1: global max over slots
   float M = kNegInf;
-  for (int p = 0; p < P; ++p) M = fmaxf(M, a.max_logits[sbase + p * a.stride_es_part]);
-  const int d = 2 * lane;
-  float o0 = 0.0f, o1 = 0.0f;
+  for (int p0 = 0; p0 < P; p0 += 64) {
+    const int p = p0 + lane;
+    const float m = p < P ? a.max_logits[sbase + p * a.stride_es_part] : kNegInf;
+    M = fmaxf(M, m);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, shfl_xor(M, o));
+  float o0 = 0.0f, o1 = 0.0f, tot = 0.0f;
   if (M != kNegInf) {
-    float tot = 0.0f;
-    const int64_t tbase = (int64_t)b * a.stride_to_seq + (int64_t)h * a.stride_to_head + (int64_t)e * a.stride_to_group + d;
-    for (int p = 0; p < P; ++p) {
-      const float mp = a.max_logits[sbase + p * a.stride_es_part];
-      const float w = mp == kNegInf ? 0.0f : a.exp_sums[sbase + p * a.stride_es_part] * __expf(mp - M);
-      tot += w;
-      float x0, x1;
-      if (a.tmp_dtype == PA_DTYPE_F32) {
-        f32x2 t = *(const f32x2*)((const float*)a.tmp_out + tbase + p * a.stride_to_part);
-        x0 = t[0];
-        x1 = t[1];
-      } else {
-        const uint32_t t = *(const uint32_t*)((const uint16_t*)a.tmp_out + tbase + p * a.stride_to_part);
-        x0 = bf16_bits_to_f32(t & 0xffffu);
-        x1 = bf16_bits_to_f32(t >> 16);
+    for (int p0 = 0; p0 < P; p0 += 64) {
+      const int p = p0 + lane;
+      float w = 0.0f;
+      if (p < P) {
+        const float m = a.max_logits[sbase + p * a.stride_es_part];
+        w = m == kNegInf ? 0.0f : a.exp_sums[sbase + p * a.stride_es_part] * __expf(m - M);
       }
-      o0 += w * x0;
-      o1 += w * x1;
+      float wsum = w;
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) wsum += shfl_xor(wsum, o);
+      tot += wsum;
+      const int n = P - p0 < 64 ? P - p0 : 64;
+      // fetch all partial rows of this pass, then combine
+      constexpr int kBatch = 16;
+      for (int q0 = 0; q0 < n; q0 += kBatch) {
+        float x0[kBatch], x1[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+          const int q = q0 + i < n ? q0 + i : n - 1;
+          const int64_t off = tbase + (int64_t)(p0 + q) * a.stride_to_part;
+          if (a.tmp_dtype == PA_DTYPE_F32) {
+            const f32x2 t = *(const f32x2*)((const float*)a.tmp_out + off);
+            x0[i] = t[0];
+            x1[i] = t[1];
+          } else {
+            const uint32_t t = *(const uint32_t*)((const uint16_t*)a.tmp_out + off);
+            x0[i] = bf16_bits_to_f32(t & 0xffffu);
+            x1[i] = bf16_bits_to_f32(t >> 16);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+          const float wi = __shfl(w, q0 + i, 64);
+          if (q0 + i < n) {
+            o0 += wi * x0[i];
+            o1 += wi * x1[i];
+          }
+        }
+      }
     }
     const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
     o0 *= inv;
@@ -632,7 +837,7 @@ __global__ __launch_bounds__(256) void pa_fp8_lse_reduce_kernel(const pa_fp8_red
   const int gqa = a.query_group_size;
   const int qi = e / gqa, g = e - qi * gqa;
   const int64_t off = (int64_t)b * a.stride_out_seq + (int64_t)qi * a.stride_out_ql +
-                      (int64_t)h * a.stride_out_kv_head + (int64_t)g * a.stride_out_group + d;
+                      (int64_t)h * a.stride_out_kv_head + (int64_t)g * a.stride_out_group + 2 * lane;
   if (a.output_dtype == PA_DTYPE_F32) {
     *(f32x2*)((float*)a.output + off) = f32x2{o0, o1};
   } else if (a.output_dtype == PA_DTYPE_F16) {
@@ -644,7 +849,7 @@ __global__ __launch_bounds__(256) void pa_fp8_lse_reduce_kernel(const pa_fp8_red
 
 template <int NCG, bool PT, bool BS16>
 hipError_t launch_partition(const pa_fp8_partition_args& a, unsigned grid, hipStream_t s) {
-  hipLaunchKernelGGL((pa_fp8_partition_kernel<NCG, PT, BS16, 2>), dim3(grid), dim3(kThreads), 0, s, a,
+  hipLaunchKernelGGL((pa_fp8_partition_kernel<NCG, PT, BS16, kStages>), dim3(grid), dim3(kThreads), 0, s, a,
                      a.block_tables, a.kv_indptr, a.context_lengths, a.key_scale, a.value_scale);
   return hipGetLastError();
 }
@@ -669,8 +874,9 @@ int pa_fp8_decode_partition(const pa_fp8_partition_args* a, void* stream) {
   if (!a->query || !a->key_cache || !a->value_cache || !a->block_tables || !a->context_lengths || !a->key_scale ||
       !a->value_scale)
     return PA_ERR_NULL_ARG;
-  const bool fused = a->output != nullptr;
-  if (fused ? a->num_partitions != 1 : (!a->exp_sums || !a->max_logits || !a->tmp_out)) return PA_ERR_NULL_ARG;
+  const bool fused = a->output != nullptr && a->num_partitions == 1;
+  if (!fused && (!a->exp_sums || !a->max_logits || !a->tmp_out)) return PA_ERR_NULL_ARG;
+  if (a->output != nullptr && a->num_partitions > 1 && !a->counters) return PA_ERR_NULL_ARG;
   if (a->head_size != kHead) return PA_ERR_HEAD_SIZE;
   const int bs = a->block_size;
   if (!(bs == 16 || (bs >= 32 && bs <= 1024 && (bs & (bs - 1)) == 0))) return PA_ERR_BLOCK_SIZE;
@@ -681,7 +887,7 @@ int pa_fp8_decode_partition(const pa_fp8_partition_args* a, void* stream) {
   if (eq > 64) return PA_ERR_GROUP;
   if (a->query_dtype != PA_DTYPE_BF16 && a->query_dtype != PA_DTYPE_F16) return PA_ERR_DTYPE;
   if (!fused && a->tmp_dtype != PA_DTYPE_BF16 && a->tmp_dtype != PA_DTYPE_F32) return PA_ERR_DTYPE;
-  if (fused && a->output_dtype != PA_DTYPE_BF16 && a->output_dtype != PA_DTYPE_F16 && a->output_dtype != PA_DTYPE_F32)
+  if (a->output && a->output_dtype != PA_DTYPE_BF16 && a->output_dtype != PA_DTYPE_F16 && a->output_dtype != PA_DTYPE_F32)
     return PA_ERR_DTYPE;
   // 16-byte vector accesses: query rows, cache pages, scale rows, partials.
   if (!aligned16(a->query) || (a->stride_q_tok % 8) || (a->stride_q_head % 8)) return PA_ERR_ALIGN;
@@ -691,9 +897,10 @@ int pa_fp8_decode_partition(const pa_fp8_partition_args* a, void* stream) {
   if (a->per_token_kv &&
       (!aligned16(a->key_scale) || !aligned16(a->value_scale) || (a->stride_ks_block % 4) || (a->stride_ks_head % 4)))
     return PA_ERR_ALIGN;
-  if (fused) {
+  if (a->output != nullptr) {
     if (!aligned16(a->output) || (a->stride_out_tok % 8) || (a->stride_out_head % 8)) return PA_ERR_ALIGN;
-  } else {
+  }
+  if (!fused) {
     if (!aligned16(a->tmp_out) || (a->stride_to_group % 8) || (a->stride_to_part % 8) || (a->stride_to_head % 8) ||
         (a->stride_to_seq % 8))
       return PA_ERR_ALIGN;

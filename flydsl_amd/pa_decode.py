@@ -6,6 +6,11 @@ Drop-in for the reference's Python API in kernels/pa_decode_fp8.py:
 defaults, tensor layouts, validation errors and route strings; the device
 work is done by the HIP kernels of ``libpa_fp8.so`` through its C ABI.
 
+Each call is one kernel launch: the partition pass writes the slot
+partials and the last slot of every (sequence, kv head) merges them
+(log-sum-exp) into the output.  The separate reduce kernel is used only when
+a graph capture starts before this stream has its merge counters.
+
 Routes (same dispatch order as the reference, :2883 / :3010 / :3123):
   * ``sliding_window > 0``    -> window partition pass + LSE reduce
                                  ("ps_sw_partitioned"), or the fused
@@ -153,8 +158,21 @@ def _tmp_dtype_code(t: torch.Tensor) -> int:
     raise ValueError(f"temporary_output must be bfloat16 or float32, got {t.dtype}")
 
 
-def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
-    return None if t is None else t.data_ptr()
+# Arrival counters of the in-kernel slot merge, one zeroed int32 buffer per
+# (device, stream); the kernel leaves them zero, so they are reused as is.
+_COUNTERS: dict = {}
+
+
+def _merge_counters(device: torch.device, stream, n: int, capturing: bool) -> Optional[torch.Tensor]:
+    key = (device.index, int(stream.cuda_stream))
+    buf = _COUNTERS.get(key)
+    if buf is not None and buf.numel() >= n:
+        return buf
+    if capturing:
+        return None  # no allocation inside a capture: use the separate reduce launch
+    buf = torch.zeros(max(n, 1024), dtype=torch.int32, device=device)
+    _COUNTERS[key] = buf
+    return buf
 
 
 def _check_int32(name: str, t: torch.Tensor, device: torch.device) -> None:
@@ -175,6 +193,30 @@ def _check_partials(exp_sums, max_logits, tmp, shape, head_size):
         raise ValueError("exp_sums and max_logits must share strides with a contiguous last dimension")
     if tmp.stride(-1) != 1:
         raise ValueError("temporary_output must be contiguous in its last dimension")
+
+
+class PreparedDecode:
+    """A validated decode call whose C-ABI arguments are already marshalled.
+
+    ``launch()`` issues exactly the device work ``pa_decode_ps_launch`` would
+    (one partition launch with the in-kernel merge, or partition + reduce)
+    without re-validating or rebuilding arguments; the tensors captured at
+    preparation must stay alive and unchanged in shape.
+    """
+
+    def __init__(self, route: str, partition_args, reduce_args, stream, keepalive):
+        self.route = route
+        self._pa = partition_args
+        self._ra = reduce_args
+        self._stream = ctypes.c_void_p(stream.cuda_stream)
+        self._keep = keepalive
+        self._lib = _lib.load()
+
+    def launch(self) -> str:
+        _lib.check(self._lib.pa_fp8_decode_partition(ctypes.byref(self._pa), self._stream), "pa_fp8_decode_partition")
+        if self._ra is not None:
+            _lib.check(self._lib.pa_fp8_decode_reduce(ctypes.byref(self._ra), self._stream), "pa_fp8_decode_reduce")
+        return self.route
 
 
 def pa_decode_ps_launch(
@@ -208,6 +250,38 @@ def pa_decode_ps_launch(
     key/value_scale: float, [1] tensor (per tensor) or [NB, Hkv, bs, 1]
     (per token per head).  Returns the route name.
     """
+    call = prepare_pa_decode(
+        output, query, key_cache, value_cache, context_lengths, kv_page_indices, kv_indptr, softmax_scale,
+        key_scale, value_scale, sliding_window=sliding_window, metadata=metadata, block_tables=block_tables,
+        max_context_partition_num=max_context_partition_num, exp_sums=exp_sums, max_logits=max_logits,
+        temporary_output=temporary_output, stream=stream,
+    )
+    return call.launch()
+
+
+def prepare_pa_decode(
+    output: torch.Tensor,
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    context_lengths: torch.Tensor,
+    kv_page_indices: torch.Tensor,
+    kv_indptr: torch.Tensor,
+    softmax_scale: float,
+    key_scale: torch.Tensor = None,
+    value_scale: torch.Tensor = None,
+    *,
+    sliding_window: int = 0,
+    metadata: dict = None,
+    block_tables: torch.Tensor = None,
+    max_context_partition_num: int = 0,
+    exp_sums: torch.Tensor = None,
+    max_logits: torch.Tensor = None,
+    temporary_output: torch.Tensor = None,
+    stream=None,
+) -> PreparedDecode:
+    """Validate and marshal one decode call (same arguments and errors as
+    :func:`pa_decode_ps_launch`); returns a :class:`PreparedDecode`."""
     num_query_heads = query.shape[1]
     num_kv_heads = key_cache.shape[1]
     trans_v = value_cache.dim() == 5
@@ -265,7 +339,6 @@ def pa_decode_ps_launch(
     _check_int32("context_lengths", context_lengths, dev)
 
     s = stream or torch.cuda.current_stream(dev)
-    stream_handle = ctypes.c_void_p(s.cuda_stream)
 
     kv_ind = None
     if sliding_window > 0:
@@ -323,6 +396,7 @@ def pa_decode_ps_launch(
     P = int(max_context_partition_num)
 
     fused = route == "sw" and P <= 1
+    counters = None
     shape = (batch_size, num_kv_heads, P, eqgs)
     if not fused:
         if is_graph_capturing and (exp_sums is None or max_logits is None or temporary_output is None):
@@ -377,10 +451,12 @@ def pa_decode_ps_launch(
     pa.trans_v = int(trans_v)
     pa.query_dtype = DTYPE_BF16 if query_input_dtype == "bf16" else DTYPE_F16
     pa.softmax_scale = float(softmax_scale)
-    if fused:
+    if fused or counters is not None:
         pa.output = output.data_ptr()
         pa.output_dtype = output_dtype
         pa.stride_out_tok, pa.stride_out_head = output.stride(0), output.stride(1)
+        pa.counters = None if counters is None else counters.data_ptr()
+    if fused:
         pa.tmp_dtype = DTYPE_BF16
     else:
         pa.exp_sums = exp_sums.data_ptr()
@@ -389,10 +465,13 @@ def pa_decode_ps_launch(
         pa.stride_es_seq, pa.stride_es_head, pa.stride_es_part = exp_sums.stride()[:3]
         (pa.stride_to_seq, pa.stride_to_head, pa.stride_to_part, pa.stride_to_group) = temporary_output.stride()[:4]
         pa.tmp_dtype = _tmp_dtype_code(temporary_output)
-    lib = _lib.load()
-    _lib.check(lib.pa_fp8_decode_partition(ctypes.byref(pa), stream_handle), "pa_fp8_decode_partition")
+    keep = (output, query, key_cache, value_cache, context_lengths, block_tables, kv_page_indices, kv_indptr,
+            key_scale, value_scale, exp_sums, max_logits, temporary_output, counters)
+    route_name = {"sw": "ps_sw_partitioned", "small": "ps_small_block", "flat": "ps_split_reduce"}[route]
     if fused:
-        return "ps_sw_fused_partitioned"
+        return PreparedDecode("ps_sw_fused_partitioned", pa, None, s, keep)
+    if counters is not None:
+        return PreparedDecode(route_name, pa, None, s, keep)
 
     ra = _lib.ReduceArgs()
     ra.abi_version = _lib.ABI_VERSION
@@ -414,8 +493,7 @@ def pa_decode_ps_launch(
     ra.head_size = head_size
     ra.output_dtype = output_dtype
     ra.tmp_dtype = _tmp_dtype_code(temporary_output)
-    _lib.check(lib.pa_fp8_decode_reduce(ctypes.byref(ra), stream_handle), "pa_fp8_decode_reduce")
-    return {"sw": "ps_sw_partitioned", "small": "ps_small_block", "flat": "ps_split_reduce"}[route]
+    return PreparedDecode(route_name, pa, ra, s, keep)
 
 
 def get_pa_metadata(

@@ -66,9 +66,12 @@ enum pa_fp8_error {
  * covers the token range of pa_fp8_plan_slot(); it stores, per query column
  * e = qi * gqa + g, exp_sums = sum exp(l - m), max_logits = m (the slot's
  * maximum scaled logit, natural-log units; -inf when empty) and the
- * normalised partial output tmp_out.  When `output` is non-NULL and
- * num_partitions == 1 the final output is written instead (the reference's
- * fused single-partition window kernel, kernels/pa_decode_swa.py:1480-1620).
+ * normalised partial output tmp_out.  With `output` set, the same launch
+ * also produces the final output: directly when there is one slot (the
+ * reference's fused single-partition window kernel,
+ * kernels/pa_decode_swa.py:1480-1620), otherwise by an in-kernel
+ * log-sum-exp merge (the math of pa_fp8_decode_reduce) done by the last
+ * slot of each (sequence, kv head) to finish, so no second launch is needed.
  */
 typedef struct pa_fp8_partition_args {
   int32_t abi_version; /* = PA_FP8_ABI_VERSION */
@@ -76,7 +79,17 @@ typedef struct pa_fp8_partition_args {
   float* exp_sums;
   float* max_logits;
   void* tmp_out;
-  void* output; /* NULL unless fused (num_partitions == 1) */
+  /* Final output [B * ql, Hq, D].  NULL: only the slot partials are
+   * written (merge them with pa_fp8_decode_reduce).  Non-NULL with
+   * num_partitions == 1: the output is written directly and the partial
+   * buffers may be NULL.  Non-NULL with num_partitions > 1: the partials
+   * are written and the last slot of each (sequence, kv head) to finish
+   * merges them into the output, which needs `counters`. */
+  void* output;
+  /* num_seqs * num_kv_heads int32 arrival counters, all zero on entry; the
+   * kernel leaves them zero.  Required for the in-kernel merge only.
+   * Launches that overlap in time must not share counters. */
+  int32_t* counters;
   /* inputs */
   const void* query;
   const void* key_cache;

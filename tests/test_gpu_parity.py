@@ -15,7 +15,9 @@ import math
 import pytest
 import torch
 
-from flydsl_amd import pa_decode_ps_launch, workloads
+import ctypes
+
+from flydsl_amd import _lib, pa_decode_ps_launch, prepare_pa_decode, workloads
 from oracle import plan
 from tests._cases import make_case, slot_partials, torch_oracle
 
@@ -260,3 +262,79 @@ def test_benchmark_config_full_size(name):
     ql = cfg.query_length
     got = torch.cat([out[b * ql : (b + 1) * ql].cpu() for b in seqs])
     assert_parity(got, ref, f"{name} seqs={seqs}")
+
+
+def test_two_pass_reduce_matches_single_launch():
+    """Partition pass without output + pa_fp8_decode_reduce == the single
+    launch with the in-kernel merge (both through the C ABI)."""
+    case = to_dev(make_case(batch=6, ctx_range=(1, 3000), per_token=True, query_length=2, num_query_heads=16,
+                            num_kv_heads=4, seed=71))
+    ref = torch_oracle({k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in case.items()},
+                       float_out=False)
+    out1, route, (es, ml, to) = launch(case, P=6, partials=True)
+    call = prepare_pa_decode(out1, case["query"], case["key_cache"], case["value_cache"], case["context_lengths"],
+                             None, None, case["softmax_scale"], case["key_scale"], case["value_scale"],
+                             block_tables=case["block_tables"], max_context_partition_num=6, exp_sums=es,
+                             max_logits=ml, temporary_output=to)
+    assert call._ra is None  # single launch
+    # second pass: partials only, then the reduce kernel
+    out2 = torch.zeros_like(out1)
+    pa = _lib.PartitionArgs.from_buffer_copy(call._pa)
+    pa.output = None
+    pa.counters = None
+    lib = _lib.load()
+    sh = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _lib.check(lib.pa_fp8_decode_partition(ctypes.byref(pa), sh), "partition")
+    ra = _lib.ReduceArgs()
+    ra.abi_version = _lib.ABI_VERSION
+    ra.output, ra.exp_sums, ra.max_logits, ra.tmp_out = out2.data_ptr(), es.data_ptr(), ml.data_ptr(), to.data_ptr()
+    ql, gqa = 2, 4
+    ra.stride_out_seq, ra.stride_out_ql = ql * out2.stride(0), out2.stride(0)
+    ra.stride_out_kv_head, ra.stride_out_group = gqa * out2.stride(1), out2.stride(1)
+    ra.stride_es_seq, ra.stride_es_head, ra.stride_es_part = es.stride()[:3]
+    ra.stride_to_seq, ra.stride_to_head, ra.stride_to_part, ra.stride_to_group = to.stride()[:4]
+    ra.num_seqs, ra.num_kv_heads, ra.num_partitions = 6, 4, 6
+    ra.query_length, ra.query_group_size, ra.head_size = ql, gqa, 128
+    ra.output_dtype, ra.tmp_dtype = _lib.DTYPE_BF16, _lib.DTYPE_BF16
+    _lib.check(lib.pa_fp8_decode_reduce(ctypes.byref(ra), sh), "reduce")
+    torch.cuda.synchronize()
+    assert_parity(out2, ref, "two-pass")
+    diff = (out1.float() - out2.float()).abs().max().item()
+    assert diff <= 1e-2, diff
+
+
+def test_graph_capture_with_in_kernel_merge():
+    case = to_dev(make_case(batch=5, ctx_range=(1, 2500), seed=81, per_token=True))
+    P = 8
+    b = 5
+    es = torch.empty((b, 2, P, 4), device=DEV)
+    ml = torch.empty_like(es)
+    to = torch.empty((b, 2, P, 4, 128), device=DEV, dtype=torch.bfloat16)
+    out = torch.empty(case["query"].shape, dtype=torch.bfloat16, device=DEV)
+    s = torch.cuda.Stream()
+
+    def call():
+        return pa_decode_ps_launch(out, case["query"], case["key_cache"], case["value_cache"],
+                                   case["context_lengths"], None, None, case["softmax_scale"], case["key_scale"],
+                                   case["value_scale"], block_tables=case["block_tables"],
+                                   max_context_partition_num=P, exp_sums=es, max_logits=ml, temporary_output=to)
+
+    with torch.cuda.stream(s):
+        call()  # eager call on the capture stream sets up its merge counters
+    torch.cuda.synchronize()
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            call()
+    torch.cuda.synchronize()
+    for i in range(4):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        with torch.cuda.stream(s):
+            call()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"eager after replay {i}"
