@@ -54,7 +54,6 @@ class PartitionArgs(ctypes.Structure):
         ("max_logits", _vp),
         ("tmp_out", _vp),
         ("output", _vp),
-        ("counters", _vp),
         ("query", _vp),
         ("key_cache", _vp),
         ("value_cache", _vp),
@@ -84,6 +83,7 @@ class PartitionArgs(ctypes.Structure):
         ("num_seqs", _i32),
         ("num_kv_heads", _i32),
         ("num_partitions", _i32),
+        ("slots_per_workgroup", _i32),
         ("query_length", _i32),
         ("query_group_size", _i32),
         ("head_size", _i32),

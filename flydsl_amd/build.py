@@ -44,6 +44,10 @@ def build_library(output: str = OUTPUT, verbose: bool = False) -> str:
         "-target-feature",
         "-Xclang",
         "-packed-fp32-ops",
+        # MFMA accumulators in VGPRs: the online-softmax rescale and the
+        # slot merges are VALU work on them (no AGPR round trips).
+        "-mllvm",
+        "-amdgpu-mfma-vgpr-form",
         *SOURCES,
         "-o",
         tmp,

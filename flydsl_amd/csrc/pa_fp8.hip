@@ -146,23 +146,6 @@ __device__ __forceinline__ void lds_dma16(const void* gsrc, LDS_AS void* ldst) {
   __builtin_amdgcn_global_load_lds(gsrc, ldst, 16, 0, 0);
 }
 
-// Device-coherent (agent scope) 32-bit accesses: sc1 stores write through
-// this XCD's L2 and sc1 loads do not hit stale lines, so slot partials can
-// be handed between workgroups on different XCDs within one launch without
-// cache-wide writeback / invalidate fences.
-__device__ __forceinline__ void store_agent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void store_agent(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_agent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t load_agent(const uint32_t* p) {
-  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // s_waitcnt immediate (gfx9 encoding) that waits for vmcnt <= n only:
 // vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14, expcnt and lgkmcnt at
 // their maxima (7 and 15) so they are not waited on.
@@ -193,122 +176,61 @@ __device__ __forceinline__ void store_output8(const pa_fp8_partition_args& a, in
 }
 
 // Write one slot's outputs for query column e (8 head dims per thread call).
-__device__ __forceinline__ void store_partial8(const pa_fp8_partition_args& a, bool fused, bool coherent, int b,
-                                               int h, int slot, int e, int d0, const float* v) {
-  if (fused) {
-    store_output8(a, b, h, e, d0, v);
-    return;
-  }
+__device__ __forceinline__ void store_partial8(const pa_fp8_partition_args& a, int b, int h, int slot, int e,
+                                               int d0, const float* v) {
   const int64_t off = (int64_t)b * a.stride_to_seq + (int64_t)h * a.stride_to_head +
                       (int64_t)slot * a.stride_to_part + (int64_t)e * a.stride_to_group + d0;
   if (a.tmp_dtype == PA_DTYPE_F32) {
     float* p = (float*)a.tmp_out + off;
-    if (coherent) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) store_agent(p + i, v[i]);
-    } else {
-      ((f32x4*)p)[0] = f32x4{v[0], v[1], v[2], v[3]};
-      ((f32x4*)p)[1] = f32x4{v[4], v[5], v[6], v[7]};
-    }
+    ((f32x4*)p)[0] = f32x4{v[0], v[1], v[2], v[3]};
+    ((f32x4*)p)[1] = f32x4{v[4], v[5], v[6], v[7]};
   } else {
     uint32_t w[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) w[i] = f32_to_bf16_bits(v[2 * i]) | (f32_to_bf16_bits(v[2 * i + 1]) << 16);
-    uint32_t* p = (uint32_t*)((uint16_t*)a.tmp_out + off);
-    if (coherent) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) store_agent(p + i, w[i]);
-    } else {
-      *(i32x4*)p = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
-    }
+    *(i32x4*)((uint16_t*)a.tmp_out + off) = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
   }
 }
 
-__device__ __forceinline__ void store_stats(const pa_fp8_partition_args& a, bool coherent, int b, int h, int slot,
-                                            int e, float exp_sum, float max_logit) {
+// 4 consecutive head dims (d0 multiple of 4) of a slot partial row.
+__device__ __forceinline__ void store_partial4(const pa_fp8_partition_args& a, int b, int h, int slot, int e,
+                                               int d0, f32x4 v) {
+  const int64_t off = (int64_t)b * a.stride_to_seq + (int64_t)h * a.stride_to_head +
+                      (int64_t)slot * a.stride_to_part + (int64_t)e * a.stride_to_group + d0;
+  if (a.tmp_dtype == PA_DTYPE_F32) {
+    *(f32x4*)((float*)a.tmp_out + off) = v;
+  } else {
+    const uint32_t w0 = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
+    const uint32_t w1 = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
+    *(i32x2*)((uint16_t*)a.tmp_out + off) = i32x2{(int)w0, (int)w1};
+  }
+}
+
+__device__ __forceinline__ void store_stats(const pa_fp8_partition_args& a, int b, int h, int slot, int e,
+                                            float exp_sum, float max_logit) {
   const int64_t off = (int64_t)b * a.stride_es_seq + (int64_t)h * a.stride_es_head +
                       (int64_t)slot * a.stride_es_part + e;
-  if (coherent) {
-    store_agent(a.exp_sums + off, exp_sum);
-    store_agent(a.max_logits + off, max_logit);
-  } else {
-    a.exp_sums[off] = exp_sum;
-    a.max_logits[off] = max_logit;
-  }
+  a.exp_sums[off] = exp_sum;
+  a.max_logits[off] = max_logit;
 }
 
-// Log-sum-exp merge of the P slots of (sequence b, kv head h), run by the
-// workgroup that finished last (same math as pa_fp8_lse_reduce_kernel).
-__device__ void merge_slots(const pa_fp8_partition_args& a, int b, int h, int tid, int nthreads) {
-  const int eq = a.query_length * a.query_group_size;
-  const int P = a.num_partitions;
-  for (int idx = tid; idx < eq * (kHead / 8); idx += nthreads) {
-    const int e = idx / (kHead / 8);
-    const int d0 = (idx % (kHead / 8)) * 8;
-    const int64_t sb = (int64_t)b * a.stride_es_seq + (int64_t)h * a.stride_es_head + e;
-    const int64_t tb0 = (int64_t)b * a.stride_to_seq + (int64_t)h * a.stride_to_head + (int64_t)e * a.stride_to_group + d0;
-    float M = kNegInf;
-    for (int p = 0; p < P; ++p) M = fmaxf(M, load_agent(a.max_logits + sb + p * a.stride_es_part));
-    float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (M != kNegInf) {
-      float tot = 0.0f;
-#pragma unroll 4
-      for (int p = 0; p < P; ++p) {
-        const float m = load_agent(a.max_logits + sb + p * a.stride_es_part);
-        const float w = m == kNegInf ? 0.0f : load_agent(a.exp_sums + sb + p * a.stride_es_part) * __expf(m - M);
-        tot += w;
-        float x[8];
-        if (a.tmp_dtype == PA_DTYPE_F32) {
-          const float* t = (const float*)a.tmp_out + tb0 + p * a.stride_to_part;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) x[i] = load_agent(t + i);
-        } else {
-          const uint32_t* t = (const uint32_t*)((const uint16_t*)a.tmp_out + tb0 + p * a.stride_to_part);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint32_t u = load_agent(t + i);
-            x[2 * i] = bf16_bits_to_f32(u & 0xffffu);
-            x[2 * i + 1] = bf16_bits_to_f32(u >> 16);
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] += w * x[i];
-      }
-      const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] *= inv;
-    }
-    store_output8(a, b, h, e, d0, o);
-  }
-}
-
-// Arrival of one slot of (b, h).  Every workgroup publishes its partials
-// (release at agent scope, so they reach memory past this XCD's L2) and
-// bumps the counter; the one that brings it to P acquires, merges all P
-// partials into the output and zeroes the counter for the next launch.
-__device__ __forceinline__ void arrive_and_merge(const pa_fp8_partition_args& a, int b, int h, int tid,
-                                                 int nthreads, int* s_flag) {
-  // The partials were written with device-coherent stores; wait until every
-  // wave's stores have completed before the slot is counted as arrived.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (tid == 0) {
-    const int old = __hip_atomic_fetch_add(&a.counters[b * a.num_kv_heads + h], 1, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-    *s_flag = old == a.num_partitions - 1;
-  }
-  __syncthreads();
-  if (*s_flag) {
-    merge_slots(a, b, h, tid, nthreads);
-    if (tid == 0) __hip_atomic_store(&a.counters[b * a.num_kv_heads + h], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
-
+// Workgroup geometry.  A workgroup covers `slots_per_workgroup`
+// consecutive slots of one (sequence, kv head).  Its waves form `groups`
+// groups of `wslot` waves; group g owns local slots g, g + groups, ... and
+// the waves of a group deal that slot's 32-token chunks round robin.  Each
+// wave streams the chunks of all its slots back to back through its LDS
+// ring, so the pipeline runs across slot boundaries.  When a wave owns
+// several slots (MULTI) it finalises each slot's partial as soon as the
+// slot ends and folds it into a running combination; otherwise the slot
+// partials are produced by the workgroup merge at the end.  A workgroup
+// that covers every slot of its (sequence, kv head) also merges them into
+// the final output.
+//
 // Block table, context lengths and scales come in as separate restrict
 // pointers so that their wave-uniform loads become scalar (SMEM) loads:
 // page lookups then count on lgkmcnt and never force a wait on the vmcnt
 // of the direct-to-LDS data loads in flight.
-template <int NCG, bool PER_TOKEN, bool BS16, int STAGES>
+template <int NCG, bool PER_TOKEN, bool BS16, int STAGES, bool MULTI>
 __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8_partition_args a,
                                                                     const int32_t* __restrict__ block_tables,
                                                                     const int32_t* __restrict__ kv_indptr,
@@ -328,44 +250,74 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
   const int c16 = lane & 15;
 
   const int P = a.num_partitions;
+  const int SPW = a.slots_per_workgroup;
+  const int PG = pa_cdiv(P, SPW);
   int bid = blockIdx.x;
-  const int slot = bid % P;
-  bid /= P;
+  const int pg = bid % PG;
+  bid /= PG;
   const int h = bid % a.num_kv_heads;
   const int b = bid / a.num_kv_heads;
+  const int zs = pg * SPW;
+  const int nslots = pa_min(P - zs, SPW);
+  const bool owner = PG == 1;
+  const bool direct_out = owner && a.output != nullptr;
+  const bool want_partials = a.exp_sums != nullptr;
+  const int wslot = nslots >= kWaves ? 1 : kWaves / nslots;
+  const int groups = kWaves / wslot;
+  const int gid = wave / wslot;
+  const int rank = wave - gid * wslot;
 
   const int ql = a.query_length;
   const int gqa = a.query_group_size;
   const int eq = ql * gqa;
   const int W = a.sliding_window;
   const int ctx = context_lengths[b];
-  // direct: one slot writes the final output itself; merge: slots write
-  // partials and the last one to finish merges them.
-  const bool fused = a.output != nullptr && P == 1;
-  const bool merge = a.output != nullptr && P > 1;
-  __shared__ int s_last;
 
-  int t0, t1, lo_all, hi_all, unused;
-  pa_plan_slot_tokens(ctx, P, slot, W, ql, &t0, &t1);
+  int lo_all, hi_all, unused;
   pa_plan_visible(ctx, 0, ql, W, &lo_all, &unused);
   pa_plan_visible(ctx, ql - 1, ql, W, &unused, &hi_all);
-  const int a0 = pa_max(t0, lo_all);
-  const int a1 = pa_min(t1, hi_all);
 
-  // A sequence without pages in its block-table row reads nothing.
-  const int bs_rows = kv_indptr ? kv_indptr[b + 1] - kv_indptr[b] : a.max_blocks_per_seq;
-  if (a1 <= a0 || bs_rows <= 0) {
-    // Empty slot: zero partial, zero sum, -inf max (reference empty-slot
-    // semantics, kernels/pa_decode_swa.py:1493-1504).
-    const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int idx = tid; idx < eq * (kHead / 8); idx += kThreads) {
-      const int e = idx / (kHead / 8);
-      store_partial8(a, fused, merge, b, h, slot, e, (idx % (kHead / 8)) * 8, z);
+  const int bs = a.block_size;
+  const int bs_shift = BS16 ? 4 : __builtin_ctz((unsigned)bs);
+  const int64_t row_off = kv_indptr ? (int64_t)kv_indptr[b] : (int64_t)b * a.stride_bt_seq;
+  const int row_len = kv_indptr ? kv_indptr[b + 1] - kv_indptr[b] : a.max_blocks_per_seq;
+  const int32_t* bt_row = block_tables + row_off;
+  const int last_page = pa_min(pa_cdiv(ctx, bs) - 1, row_len - 1);
+  const bool has_pages = row_len > 0;
+  const int nblocks = a.num_blocks;
+
+  // Chunks of slot z: first chunk token (32-aligned) and how many of the
+  // slot's chunks wave-rank `rank` takes.  Wave-uniform.
+  auto slot_range = [&](int z, int& cbeg, int& nmine) {
+    int t0, t1;
+    pa_plan_slot_tokens(ctx, P, z, W, ql, &t0, &t1);
+    const int a0 = pa_max(t0, lo_all);
+    const int a1 = pa_min(t1, hi_all);
+    cbeg = a0 & ~(kChunk - 1);
+    nmine = 0;
+    if (a1 > a0 && has_pages) {
+      const int n = pa_cdiv(a1 - cbeg, kChunk);
+      nmine = n > rank ? (n - rank + wslot - 1) / wslot : 0;
     }
-    if (!fused)
-      for (int e = tid; e < eq; e += kThreads) store_stats(a, merge, b, h, slot, e, 0.0f, kNegInf);
-    if (merge) arrive_and_merge(a, b, h, tid, kThreads, &s_last);
-    return;
+  };
+
+  if (nslots == 1) {
+    // One slot per workgroup: an empty slot writes (0, -inf, 0) and stops
+    // (reference empty-slot semantics, kernels/pa_decode_swa.py:1493-1504).
+    int t0, t1;
+    pa_plan_slot_tokens(ctx, P, zs, W, ql, &t0, &t1);
+    if (!(pa_min(t1, hi_all) > pa_max(t0, lo_all) && has_pages)) {
+      const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      for (int idx = tid; idx < eq * (kHead / 8); idx += kThreads) {
+        const int e = idx / (kHead / 8);
+        const int d0 = (idx % (kHead / 8)) * 8;
+        if (want_partials) store_partial8(a, b, h, zs, e, d0, z);
+        if (direct_out) store_output8(a, b, h, e, d0, z);
+      }
+      if (want_partials)
+        for (int e = tid; e < eq; e += kThreads) store_stats(a, b, h, zs, e, 0.0f, kNegInf);
+      return;
+    }
   }
 
   // ---------------- query: raw loads (issued before the first KV chunk) ----------------
@@ -388,32 +340,6 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
     }
   }
 
-  // ---------------- stream this wave's chunks ----------------
-  const int cbeg = a0 & ~(kChunk - 1);
-  const int nchunks = pa_cdiv(a1 - cbeg, kChunk);
-  const int nmine = nchunks > wave ? (nchunks - wave + kWaves - 1) / kWaves : 0;
-
-  const int bs = a.block_size;
-  const int bs_shift = BS16 ? 4 : __builtin_ctz((unsigned)bs);
-  const int64_t row_off = kv_indptr ? (int64_t)kv_indptr[b] : (int64_t)b * a.stride_bt_seq;
-  const int row_len = kv_indptr ? kv_indptr[b + 1] - kv_indptr[b] : a.max_blocks_per_seq;
-  const int32_t* bt_row = block_tables + row_off;
-  const int last_page = pa_min(pa_cdiv(ctx, bs) - 1, row_len - 1);
-  const int nblocks = a.num_blocks;
-  // Block-table entries of the (one or two) pages of chunk k.  Reads past
-  // the context reuse the last page (its tokens are masked).  The raw
-  // entries are clamped into the cache only when used, one step later, so
-  // the scalar loads overlap the current chunk's compute.
-  auto fetch_pages = [&](int k, int& q0, int& q1) {
-    const int lp0 = (cbeg + (wave + k * kWaves) * kChunk) >> bs_shift;
-    q0 = bt_row[pa_min(lp0, last_page)];
-    q1 = BS16 ? bt_row[pa_min(lp0 + 1, last_page)] : q0;
-  };
-  auto clamp_page = [&](int p) -> int {
-    p = p < 0 ? 0 : p;
-    return p < nblocks ? p : nblocks - 1;
-  };
-
   const uint8_t* kbase = (const uint8_t*)a.key_cache + (int64_t)h * a.stride_k_head;
   const uint8_t* vbase = (const uint8_t*)a.value_cache + (int64_t)h * a.stride_v_head;
   const float* ksbase = PER_TOKEN ? key_scale + (int64_t)h * a.stride_ks_head : nullptr;
@@ -431,10 +357,23 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
   const int koff_lane = BS16 ? lane * 16 : (lane >> 4) * (bs * 16) + (lane & 15) * 16;
   const int voff_plain = lane * bs;
 
-  auto issue = [&](int k, int st, int raw0, int raw1) {
+  auto clamp_page = [&](int p) -> int {
+    p = p < 0 ? 0 : p;
+    return p < nblocks ? p : nblocks - 1;
+  };
+  // Block-table entries of the (one or two) pages of the chunk starting at
+  // token tb.  Reads past the context reuse the last page (its tokens are
+  // masked).  Clamped into the cache only when used, one step later, so the
+  // scalar loads overlap the current chunk's compute.
+  auto fetch_pages = [&](int tb, int& q0, int& q1) {
+    const int lp0 = tb >> bs_shift;
+    q0 = bt_row[pa_min(lp0, last_page)];
+    q1 = BS16 ? bt_row[pa_min(lp0 + 1, last_page)] : q0;
+  };
+
+  auto issue = [&](int tb, int st, int raw0, int raw1) {
     const int p0 = clamp_page(raw0);
     const int p1 = BS16 ? clamp_page(raw1) : p0;
-    const int tb = cbeg + (wave + k * kWaves) * kChunk;
     LDS_AS unsigned char* sk = ring + st * kStageBytes;
     LDS_AS unsigned char* sv = sk + kKBytes;
     if (BS16) {
@@ -474,13 +413,28 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
       LDS_AS unsigned char* ss = sv + kVBytes;
       if (lane < 16) {
         const int tt = (lane & 7) * 4;
-        const int pg = BS16 ? (tt >= 16 ? p1 : p0) : p0;
+        const int pg2 = BS16 ? (tt >= 16 ? p1 : p0) : p0;
         const int sidx = BS16 ? (tt & 15) : (tb & (bs - 1)) + tt;
         const float* base = lane < 8 ? ksbase : vsbase;
-        lds_dma16(base + (int64_t)pg * a.stride_ks_block + sidx, ss);
+        lds_dma16(base + (int64_t)pg2 * a.stride_ks_block + sidx, ss);
       }
     }
   };
+
+  // ---------------- issue cursor: the next chunk of this wave to load ----------------
+  int ic_l = gid;  // local slot index
+  int ic_j = 0;    // chunk index within this wave's share of the slot
+  int ic_cbeg = 0, ic_n = 0;
+  if (ic_l < nslots) slot_range(zs + ic_l, ic_cbeg, ic_n);
+  auto ic_skip_empty = [&]() {
+    while (ic_l < nslots && ic_j >= ic_n) {
+      ic_l += groups;
+      ic_j = 0;
+      if (ic_l < nslots) slot_range(zs + ic_l, ic_cbeg, ic_n);
+    }
+  };
+  ic_skip_empty();
+  auto ic_tb = [&]() { return ic_cbeg + (rank + ic_j * wslot) * kChunk; };
 
   float m2[NCG], lsum[NCG];
   f32x4 acc[NCG][8];
@@ -491,19 +445,35 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[cg][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  float vsmax = 0.0f;  // running max of per-token value scales (per wave)
-
-  // Pipeline: chunks k+1 .. k+STAGES-1 are in flight while chunk k is
-  // computed; the page indices of the next chunk to issue are fetched one
-  // step ahead so their scalar-load latency is hidden as well.
-  int np0 = 0, np1 = 0;
+  float vsmax = 0.0f;  // running max of per-token value scales (per wave, per slot)
+  // Combination of the finished slots of this wave (MULTI only; in value
+  // units: per-tensor / per-token value scales already applied).
+  float mC[MULTI ? NCG : 1], lC[MULTI ? NCG : 1];
+  f32x4 accC[MULTI ? NCG : 1][8];
+  if (MULTI) {
 #pragma unroll
-  for (int k = 0; k < STAGES - 1; ++k)
-    if (k < nmine) {
-      fetch_pages(k, np0, np1);
-      issue(k, k, np0, np1);
+    for (int cg = 0; cg < NCG; ++cg) {
+      mC[cg] = kNegInf;
+      lC[cg] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) accC[cg][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-  if (STAGES - 1 < nmine) fetch_pages(STAGES - 1, np0, np1);
+  }
+
+  // Pipeline: chunks g+1 .. g+STAGES-1 (in this wave's global order) are in
+  // flight while chunk g is computed; the page indices of the next chunk to
+  // issue are fetched one step ahead so their scalar-load latency is hidden.
+  int np0 = 0, np1 = 0;
+  if (ic_l < nslots) fetch_pages(ic_tb(), np0, np1);
+#pragma unroll
+  for (int k = 0; k < STAGES - 1; ++k) {
+    if (ic_l < nslots) {
+      issue(ic_tb(), k, np0, np1);
+      ++ic_j;
+      ic_skip_empty();
+      if (ic_l < nslots) fetch_pages(ic_tb(), np0, np1);
+    }
+  }
 
   // ---------------- query: scale, split into fp8 hi + lo ----------------
   // B operand of the 16x16x128 QK product: lane (grp, c) holds the 32 head
@@ -513,6 +483,7 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
   float qfac[NCG];   // base-2 logit factor per column
   int vis_lo[NCG], vis_hi[NCG];
   const float k_tensor_scale = PER_TOKEN ? 1.0f : key_scale[0];
+  const float v_tensor_scale = PER_TOKEN ? 1.0f : value_scale[0];
 #pragma unroll
   for (int cg = 0; cg < NCG; ++cg) {
     const int e = cg * 16 + c16;
@@ -543,16 +514,16 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
     sexp = sexp < 1 ? 1 : (sexp > 254 ? 254 : sexp);
     const float sq = amax > 0.0f ? __uint_as_float((uint32_t)sexp << 23) : 1.0f;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int sI = 0; sI < 4; ++sI) {
       float xs[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) xs[i] = v[8 * s + i] * sq;
+      for (int i = 0; i < 8; ++i) xs[i] = v[8 * sI + i] * sq;
       long hi, lo;
       split8_fp8(xs, hi, lo);
-      qhi8[cg][2 * s] = (int)(uint32_t)hi;
-      qhi8[cg][2 * s + 1] = (int)(uint32_t)((uint64_t)hi >> 32);
-      qlo8[cg][2 * s] = (int)(uint32_t)lo;
-      qlo8[cg][2 * s + 1] = (int)(uint32_t)((uint64_t)lo >> 32);
+      qhi8[cg][2 * sI] = (int)(uint32_t)hi;
+      qhi8[cg][2 * sI + 1] = (int)(uint32_t)((uint64_t)hi >> 32);
+      qlo8[cg][2 * sI] = (int)(uint32_t)lo;
+      qlo8[cg][2 * sI + 1] = (int)(uint32_t)((uint64_t)lo >> 32);
     }
     qfac[cg] = a.softmax_scale * kLog2e * k_tensor_scale / sq;
     int lo = 0, hi = 0;
@@ -561,8 +532,8 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
     vis_hi[cg] = hi;
   }
   // Chunks inside [lo_max, hi_min) are visible to every query column: no
-  // masking there.  lo grows and hi grows with qi, so the extremes come
-  // from the last and the first query.
+  // masking there.  lo and hi grow with qi, so the extremes come from the
+  // last and the first query.
   int lo_max, hi_min;
   {
     int t0q, t1q;
@@ -574,192 +545,245 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
   // token's 16-byte pieces for dim chunks grp and grp+4.
   const int krow = (c16 >> 3) * kKHalf + (8 * ((c16 >> 2) & 1) + (c16 & 3)) * 16;
 
-  for (int k = 0; k < nmine; ++k) {
-    const int st = k % STAGES;
-    if (k + STAGES - 1 < nmine) {
-      issue(k + STAGES - 1, (k + STAGES - 1) % STAGES, np0, np1);
-      if (k + STAGES < nmine) fetch_pages(k + STAGES, np0, np1);
-      // Loads retire in order: leave the newest chunks' loads in flight.
-      constexpr int kLoadsPerChunk = 8 + (PER_TOKEN ? 1 : 0);
-      __builtin_amdgcn_s_waitcnt(vmcnt_only(kLoadsPerChunk * (STAGES - 1)));
-    } else {
-      __builtin_amdgcn_s_waitcnt(0);
-    }
-    const int tb = cbeg + (wave + k * kWaves) * kChunk;
-    const LDS_AS unsigned char* sk = ring + st * kStageBytes;
-    const LDS_AS unsigned char* sv = sk + kKBytes;
-
-    const i32x4 ka0 = *(const LDS_AS i32x4*)(sk + krow + grp * 256);
-    const i32x4 ka1 = *(const LDS_AS i32x4*)(sk + krow + (grp + 4) * 256);
-    const i32x4 kb0 = *(const LDS_AS i32x4*)(sk + krow + 64 + grp * 256);
-    const i32x4 kb1 = *(const LDS_AS i32x4*)(sk + krow + 64 + (grp + 4) * 256);
-    const i32x8 KA = {ka0[0], ka0[1], ka0[2], ka0[3], ka1[0], ka1[1], ka1[2], ka1[3]};
-    const i32x8 KB = {kb0[0], kb0[1], kb0[2], kb0[3], kb1[0], kb1[1], kb1[2], kb1[3]};
-
-    // value operands: head dim 16j + c16, tokens 8*grp .. 8*grp+7
-    long V[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      V[j] = *(const LDS_AS long*)(sv + (grp >> 1) * 2048 + (16 * j + c16) * 16 + 8 * (grp & 1));
-
-    // This lane's 8 tokens: tb + 8*grp + j.
-    const int tok0 = tb + 8 * grp;
-    const bool interior = tb >= lo_max && tb + kChunk <= hi_min;
-    const bool edge = tb < lo_all || tb + kChunk > hi_all;
-    if (edge) {
-      // Zero value bytes of tokens no query sees (stale page tails).
-      uint64_t keep = 0;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int t = tok0 + j;
-        if (t >= lo_all && t < hi_all) keep |= (uint64_t)0xff << (8 * j);
+  int gc = 0;  // chunks of this wave computed so far
+  for (int l = gid; l < nslots; l += groups) {
+    const int z = zs + l;
+    int cbeg, nmine;
+    slot_range(z, cbeg, nmine);
+    for (int k = 0; k < nmine; ++k) {
+      const int st = gc % STAGES;
+      if (ic_l < nslots) {
+        issue(ic_tb(), (gc + STAGES - 1) % STAGES, np0, np1);
+        ++ic_j;
+        ic_skip_empty();
+        if (ic_l < nslots) fetch_pages(ic_tb(), np0, np1);
+        // Loads retire in order: leave the newest chunks' loads in flight.
+        constexpr int kLoadsPerChunk = 8 + (PER_TOKEN ? 1 : 0);
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(kLoadsPerChunk * (STAGES - 1)));
+      } else {
+        __builtin_amdgcn_s_waitcnt(0);
       }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) V[j] = (long)((uint64_t)V[j] & keep);
-    }
+      ++gc;
+      const int tb = cbeg + (rank + k * wslot) * kChunk;
+      const LDS_AS unsigned char* sk = ring + st * kStageBytes;
+      const LDS_AS unsigned char* sv = sk + kKBytes;
 
-    float ksc[8], vsc[8];
-    float vratio = 1.0f, vinv = 1.0f;
-    if (PER_TOKEN) {
-      const LDS_AS float* ss = (const LDS_AS float*)(sv + kVBytes);
-      f32x4 k0 = *(const LDS_AS f32x4*)(ss + 8 * grp);
-      f32x4 k1 = *(const LDS_AS f32x4*)(ss + 8 * grp + 4);
-      f32x4 w0 = *(const LDS_AS f32x4*)(ss + 32 + 8 * grp);
-      f32x4 w1 = *(const LDS_AS f32x4*)(ss + 32 + 8 * grp + 4);
+      const i32x4 ka0 = *(const LDS_AS i32x4*)(sk + krow + grp * 256);
+      const i32x4 ka1 = *(const LDS_AS i32x4*)(sk + krow + (grp + 4) * 256);
+      const i32x4 kb0 = *(const LDS_AS i32x4*)(sk + krow + 64 + grp * 256);
+      const i32x4 kb1 = *(const LDS_AS i32x4*)(sk + krow + 64 + (grp + 4) * 256);
+      const i32x8 KA = {ka0[0], ka0[1], ka0[2], ka0[3], ka1[0], ka1[1], ka1[2], ka1[3]};
+      const i32x8 KB = {kb0[0], kb0[1], kb0[2], kb0[3], kb1[0], kb1[1], kb1[2], kb1[3]};
+
+      // value operands: head dim 16j + c16, tokens 8*grp .. 8*grp+7
+      long V[8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        ksc[j] = k0[j];
-        ksc[4 + j] = k1[j];
-        vsc[j] = w0[j];
-        vsc[4 + j] = w1[j];
-      }
+      for (int j = 0; j < 8; ++j)
+        V[j] = *(const LDS_AS long*)(sv + (grp >> 1) * 2048 + (16 * j + c16) * 16 + 8 * (grp & 1));
+
+      // This lane's 8 tokens: tb + 8*grp + j.
+      const int tok0 = tb + 8 * grp;
+      const bool interior = tb >= lo_max && tb + kChunk <= hi_min;
+      const bool edge = tb < lo_all || tb + kChunk > hi_all;
       if (edge) {
+        // Zero value bytes of tokens no query sees (stale page tails).
+        uint64_t keep = 0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int t = tok0 + j;
-          if (!(t >= lo_all && t < hi_all)) vsc[j] = 0.0f;
+          if (t >= lo_all && t < hi_all) keep |= (uint64_t)0xff << (8 * j);
         }
-      }
-      float cmax = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) cmax = fmaxf(cmax, vsc[j]);
-      cmax = max_over_groups(cmax);
-      const float vnew = fmaxf(vsmax, cmax);
-      vratio = vnew > 0.0f ? vsmax / vnew : 1.0f;
-      vinv = vnew > 0.0f ? 1.0f / vnew : 0.0f;
-      vsmax = vnew;
-    }
+        for (int j = 0; j < 8; ++j) V[j] = (long)((uint64_t)V[j] & keep);
+      }
+
+      float ksc[8], vsc[8];
+      float vratio = 1.0f, vinv = 1.0f;
+      if (PER_TOKEN) {
+        const LDS_AS float* ss = (const LDS_AS float*)(sv + kVBytes);
+        f32x4 k0 = *(const LDS_AS f32x4*)(ss + 8 * grp);
+        f32x4 k1 = *(const LDS_AS f32x4*)(ss + 8 * grp + 4);
+        f32x4 w0 = *(const LDS_AS f32x4*)(ss + 32 + 8 * grp);
+        f32x4 w1 = *(const LDS_AS f32x4*)(ss + 32 + 8 * grp + 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          ksc[j] = k0[j];
+          ksc[4 + j] = k1[j];
+          vsc[j] = w0[j];
+          vsc[4 + j] = w1[j];
+        }
+        if (edge) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int t = tok0 + j;
+            if (!(t >= lo_all && t < hi_all)) vsc[j] = 0.0f;
+          }
+        }
+        float cmax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) cmax = fmaxf(cmax, vsc[j]);
+        cmax = max_over_groups(cmax);
+        const float vnew = fmaxf(vsmax, cmax);
+        vratio = vnew > 0.0f ? vsmax / vnew : 1.0f;
+        vinv = vnew > 0.0f ? 1.0f / vnew : 0.0f;
+        vsmax = vnew;
+      }
 
 #pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) {
-      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-      f32x4 la = mfma_fp8_k128(KA, qhi8[cg], z);
-      f32x4 lb = mfma_fp8_k128(KB, qhi8[cg], z);
-      la = mfma_fp8_k128(KA, qlo8[cg], la);
-      lb = mfma_fp8_k128(KB, qlo8[cg], lb);
-      float l[8];
+      for (int cg = 0; cg < NCG; ++cg) {
+        const f32x4 zz = {0.f, 0.f, 0.f, 0.f};
+        f32x4 la = mfma_fp8_k128(KA, qhi8[cg], zz);
+        f32x4 lb = mfma_fp8_k128(KB, qhi8[cg], zz);
+        la = mfma_fp8_k128(KA, qlo8[cg], la);
+        lb = mfma_fp8_k128(KB, qlo8[cg], lb);
+        float lg[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        l[i] = la[i] * qfac[cg];
-        l[4 + i] = lb[i] * qfac[cg];
-      }
-      if (PER_TOKEN) {
+        for (int i = 0; i < 4; ++i) {
+          lg[i] = la[i] * qfac[cg];
+          lg[4 + i] = lb[i] * qfac[cg];
+        }
+        if (PER_TOKEN) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) l[j] *= ksc[j];
-      }
-      if (!interior) {
+          for (int j = 0; j < 8; ++j) lg[j] *= ksc[j];
+        }
+        if (!interior) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int t = tok0 + j;
+            lg[j] = (t >= vis_lo[cg] && t < vis_hi[cg]) ? lg[j] : kNegInf;
+          }
+        }
+        float cmax = fmaxf(fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3])), fmaxf(fmaxf(lg[4], lg[5]), fmaxf(lg[6], lg[7])));
+        cmax = max_over_groups(cmax);
+        const float mnew = fmaxf(m2[cg], cmax);
+        const float muse = mnew == kNegInf ? 0.0f : mnew;
+        const float alpha = __builtin_amdgcn_exp2f(m2[cg] - muse);
+        m2[cg] = mnew;
+        float pr[8];
+        float psum = 0.0f;
+        const float bias = 8.0f - muse;  // 256 * exp(l - m)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const int t = tok0 + j;
-          l[j] = (t >= vis_lo[cg] && t < vis_hi[cg]) ? l[j] : kNegInf;
+          pr[j] = __builtin_amdgcn_exp2f(lg[j] + bias);
+          psum += pr[j];
+        }
+        lsum[cg] = lsum[cg] * alpha + psum;
+        if (PER_TOKEN) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) pr[j] *= vsc[j] * vinv;
+        }
+        long phi, plo;
+        split8_fp8(pr, phi, plo);
+        const float f = alpha * vratio;
+        if (__ballot(f != 1.0f)) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[cg][j] *= f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          acc[cg][j] = mfma_fp8(V[j], phi, acc[cg][j]);
+          acc[cg][j] = mfma_fp8(V[j], plo, acc[cg][j]);
         }
       }
-      float cmax = fmaxf(fmaxf(fmaxf(l[0], l[1]), fmaxf(l[2], l[3])), fmaxf(fmaxf(l[4], l[5]), fmaxf(l[6], l[7])));
-      cmax = max_over_groups(cmax);
-      const float mnew = fmaxf(m2[cg], cmax);
-      const float muse = mnew == kNegInf ? 0.0f : mnew;
-      const float alpha = __builtin_amdgcn_exp2f(m2[cg] - muse);
-      m2[cg] = mnew;
-      float p[8];
-      float psum = 0.0f;
-      const float bias = 8.0f - muse;  // 256 * exp(l - m)
+    }
+    if (MULTI) {
+      // Slot z is complete (this wave owns it alone): write its partial and
+      // fold it into the wave's running combination.
+      const float vfin = PER_TOKEN ? vsmax : v_tensor_scale;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        p[j] = __builtin_amdgcn_exp2f(l[j] + bias);
-        psum += p[j];
-      }
-      lsum[cg] = lsum[cg] * alpha + psum;
-      if (PER_TOKEN) {
+      for (int cg = 0; cg < NCG; ++cg) {
+        const float L = sum_over_groups(lsum[cg]);
+        const float m = m2[cg];
+        const int e = cg * 16 + c16;
+        if (want_partials && e < eq) {
+          const float sc = L > 0.0f ? vfin / L : 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) p[j] *= vsc[j] * vinv;
-      }
-      long phi, plo;
-      split8_fp8(p, phi, plo);
-      const float f = alpha * vratio;
-      if (__ballot(f != 1.0f)) {
+          for (int j = 0; j < 8; ++j) store_partial4(a, b, h, z, e, 16 * j + 4 * grp, acc[cg][j] * sc);
+          if (grp == 0) store_stats(a, b, h, z, e, L * (1.0f / 256.0f), m * kLn2);
+        }
+        const float Mn = fmaxf(mC[cg], m);
+        const float Mu = Mn == kNegInf ? 0.0f : Mn;
+        const float fc = __builtin_amdgcn_exp2f(mC[cg] - Mu);
+        const float fs = __builtin_amdgcn_exp2f(m - Mu);
+        const float fsv = fs * vfin;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[cg][j] *= f;
-      }
+        for (int j = 0; j < 8; ++j) accC[cg][j] = accC[cg][j] * fc + acc[cg][j] * fsv;
+        lC[cg] = lC[cg] * fc + L * fs;
+        mC[cg] = Mn;
+        m2[cg] = kNegInf;
+        lsum[cg] = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        acc[cg][j] = mfma_fp8(V[j], phi, acc[cg][j]);
-        acc[cg][j] = mfma_fp8(V[j], plo, acc[cg][j]);
+        for (int j = 0; j < 8; ++j) acc[cg][j] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
+      vsmax = 0.0f;
     }
   }
 
-  // ---------------- merge the waves of the workgroup ----------------
-#pragma unroll
-  for (int cg = 0; cg < NCG; ++cg) lsum[cg] = sum_over_groups(lsum[cg]);
-  const float vfin = PER_TOKEN ? vsmax : value_scale[0];
+  // ---------------- workgroup merge ----------------
+  // Each wave publishes (max, sum, value-unit accumulator) per column; sets
+  // of waves are then combined by log-sum-exp: each group of `wslot` waves
+  // into its slot's partial (unless MULTI waves already wrote them), and,
+  // for a workgroup that covers every slot, all waves into the output.
+  const float vfin_end = PER_TOKEN ? vsmax : v_tensor_scale;
   float* mbuf = (float*)smem;             // [wave][16]
   float* lbuf = mbuf + kWaves * 16;       // [wave][16]
   float* abuf = lbuf + kWaves * 16;       // [wave][head dim][16]
+  const int ngp = (!MULTI && want_partials) ? pa_min(groups, nslots) : 0;
+  const int nsets = ngp + (direct_out ? 1 : 0);
 #pragma unroll
   for (int cg = 0; cg < NCG; ++cg) {
-    __syncthreads();
-    if (grp == 0) {
-      mbuf[wave * 16 + c16] = m2[cg];
-      lbuf[wave * 16 + c16] = lsum[cg];
+    float Mst, Lst, sc;
+    if (MULTI) {
+      Mst = mC[cg];
+      Lst = lC[cg];
+      sc = 1.0f;
+    } else {
+      Mst = m2[cg];
+      Lst = sum_over_groups(lsum[cg]);
+      sc = vfin_end;
     }
     __syncthreads();
-    float M = kNegInf;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mbuf[w * 16 + c16]);
-    const float Mu = M == kNegInf ? 0.0f : M;
-    const float fself = __builtin_amdgcn_exp2f(m2[cg] - Mu) * vfin;
+    if (grp == 0) {
+      mbuf[wave * 16 + c16] = Mst;
+      lbuf[wave * 16 + c16] = Lst;
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) abuf[(wave * kHead + 16 * j + 4 * grp + i) * 16 + c16] = acc[cg][j][i] * fself;
+      for (int i = 0; i < 4; ++i)
+        abuf[(wave * kHead + 16 * j + 4 * grp + i) * 16 + c16] = (MULTI ? accC[cg][j][i] : acc[cg][j][i]) * sc;
     __syncthreads();
-    for (int idx = tid; idx < 256; idx += kThreads) {
-    const int col = idx >> 4;
-    const int d0 = (idx & 15) * 8;
-    const int e = cg * 16 + col;
-    if (e < eq) {
+    for (int idx = tid; idx < nsets * 256; idx += kThreads) {
+      const int set = idx >> 8;
+      const int col = (idx >> 4) & 15;
+      const int d0 = (idx & 15) * 8;
+      const int e = cg * 16 + col;
+      if (e >= eq) continue;
+      const int w0 = set < ngp ? set * wslot : 0;
+      const int w1 = set < ngp ? w0 + wslot : kWaves;
       float Mc = kNegInf;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) Mc = fmaxf(Mc, mbuf[w * 16 + col]);
+      for (int w = w0; w < w1; ++w) Mc = fmaxf(Mc, mbuf[w * 16 + col]);
       const float Mcu = Mc == kNegInf ? 0.0f : Mc;
       float L = 0.0f;
+      float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      for (int w = w0; w < w1; ++w) {
+        const float f = __builtin_amdgcn_exp2f(mbuf[w * 16 + col] - Mcu);
+        L += lbuf[w * 16 + col] * f;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) L += lbuf[w * 16 + col] * __builtin_amdgcn_exp2f(mbuf[w * 16 + col] - Mcu);
-      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-      float o[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float s = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) s += abuf[(w * kHead + d0 + i) * 16 + col];
-        o[i] = s * inv;
+        for (int i = 0; i < 8; ++i) o[i] += abuf[(w * kHead + d0 + i) * 16 + col] * f;
       }
-      store_partial8(a, fused, merge, b, h, slot, e, d0, o);
-      if (!fused && (idx & 15) == 0) store_stats(a, merge, b, h, slot, e, L * (1.0f / 256.0f), Mc * kLn2);
-    }
+      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] *= inv;
+      if (set < ngp) {
+        const int z = zs + set;
+        store_partial8(a, b, h, z, e, d0, o);
+        if (d0 == 0) store_stats(a, b, h, z, e, L * (1.0f / 256.0f), Mc * kLn2);
+      } else {
+        store_output8(a, b, h, e, d0, o);
+      }
     }
   }
-  if (merge) arrive_and_merge(a, b, h, tid, kThreads, &s_last);
 }
 
 // One wave per (sequence, kv head, column); lane l covers head dims 2l,
@@ -847,19 +871,22 @@ __global__ __launch_bounds__(256) void pa_fp8_lse_reduce_kernel(const pa_fp8_red
   }
 }
 
-template <int NCG, bool PT, bool BS16>
+template <int NCG, bool PT, bool BS16, bool MULTI>
 hipError_t launch_partition(const pa_fp8_partition_args& a, unsigned grid, hipStream_t s) {
-  hipLaunchKernelGGL((pa_fp8_partition_kernel<NCG, PT, BS16, kStages>), dim3(grid), dim3(kThreads), 0, s, a,
+  hipLaunchKernelGGL((pa_fp8_partition_kernel<NCG, PT, BS16, kStages, MULTI>), dim3(grid), dim3(kThreads), 0, s, a,
                      a.block_tables, a.kv_indptr, a.context_lengths, a.key_scale, a.value_scale);
   return hipGetLastError();
 }
 
-template <int NCG>
+template <int NCG, bool MULTI>
 hipError_t dispatch_ncg(const pa_fp8_partition_args& a, unsigned grid, hipStream_t s) {
   const bool pt = a.per_token_kv != 0;
   const bool bs16 = a.block_size == 16;
-  if (pt) return bs16 ? launch_partition<NCG, true, true>(a, grid, s) : launch_partition<NCG, true, false>(a, grid, s);
-  return bs16 ? launch_partition<NCG, false, true>(a, grid, s) : launch_partition<NCG, false, false>(a, grid, s);
+  if (pt)
+    return bs16 ? launch_partition<NCG, true, true, MULTI>(a, grid, s)
+                : launch_partition<NCG, true, false, MULTI>(a, grid, s);
+  return bs16 ? launch_partition<NCG, false, true, MULTI>(a, grid, s)
+              : launch_partition<NCG, false, false, MULTI>(a, grid, s);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -874,9 +901,15 @@ int pa_fp8_decode_partition(const pa_fp8_partition_args* a, void* stream) {
   if (!a->query || !a->key_cache || !a->value_cache || !a->block_tables || !a->context_lengths || !a->key_scale ||
       !a->value_scale)
     return PA_ERR_NULL_ARG;
-  const bool fused = a->output != nullptr && a->num_partitions == 1;
-  if (!fused && (!a->exp_sums || !a->max_logits || !a->tmp_out)) return PA_ERR_NULL_ARG;
-  if (a->output != nullptr && a->num_partitions > 1 && !a->counters) return PA_ERR_NULL_ARG;
+  const int spw = a->slots_per_workgroup;
+  if (spw <= 0 || a->num_partitions <= 0) return PA_ERR_SHAPE;
+  const bool owner = spw >= a->num_partitions;  // one workgroup covers every slot
+  const bool partials = a->exp_sums || a->max_logits || a->tmp_out;
+  if (partials && (!a->exp_sums || !a->max_logits || !a->tmp_out)) return PA_ERR_NULL_ARG;
+  if (!owner && !partials) return PA_ERR_NULL_ARG;   // slot partials are the only result
+  if (a->output != nullptr && !owner) return PA_ERR_SHAPE;  // output needs every slot
+  if (!partials && a->output == nullptr) return PA_ERR_NULL_ARG;
+  const bool fused = !partials;
   if (a->head_size != kHead) return PA_ERR_HEAD_SIZE;
   const int bs = a->block_size;
   if (!(bs == 16 || (bs >= 32 && bs <= 1024 && (bs & (bs - 1)) == 0))) return PA_ERR_BLOCK_SIZE;
@@ -905,16 +938,26 @@ int pa_fp8_decode_partition(const pa_fp8_partition_args* a, void* stream) {
         (a->stride_to_seq % 8))
       return PA_ERR_ALIGN;
   }
-  const int64_t grid = (int64_t)a->num_seqs * a->num_kv_heads * a->num_partitions;
+  const int64_t grid = (int64_t)a->num_seqs * a->num_kv_heads * pa_cdiv(a->num_partitions, spw);
   if (grid == 0) return PA_OK;
   if (grid > 0x7fffffffLL) return PA_ERR_SHAPE;
+  // A wave owns several slots only when a workgroup covers more slots than
+  // it has waves; that form keeps a second accumulator set, built for one
+  // 16-column group only.
+  const bool multi = pa_min(spw, a->num_partitions) > kWaves;
+  const int ncg = (eq + 15) / 16;
+  if (multi && ncg > 1) return PA_ERR_GROUP;
   hipStream_t s = (hipStream_t)stream;
   hipError_t err;
-  switch ((eq + 15) / 16) {
-    case 1: err = dispatch_ncg<1>(*a, (unsigned)grid, s); break;
-    case 2: err = dispatch_ncg<2>(*a, (unsigned)grid, s); break;
-    case 3: err = dispatch_ncg<3>(*a, (unsigned)grid, s); break;
-    default: err = dispatch_ncg<4>(*a, (unsigned)grid, s); break;
+  if (multi) {
+    err = dispatch_ncg<1, true>(*a, (unsigned)grid, s);
+  } else {
+    switch (ncg) {
+      case 1: err = dispatch_ncg<1, false>(*a, (unsigned)grid, s); break;
+      case 2: err = dispatch_ncg<2, false>(*a, (unsigned)grid, s); break;
+      case 3: err = dispatch_ncg<3, false>(*a, (unsigned)grid, s); break;
+      default: err = dispatch_ncg<4, false>(*a, (unsigned)grid, s); break;
+    }
   }
   return err == hipSuccess ? PA_OK : (int)err;
 }

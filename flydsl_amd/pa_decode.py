@@ -6,10 +6,12 @@ Drop-in for the reference's Python API in kernels/pa_decode_fp8.py:
 defaults, tensor layouts, validation errors and route strings; the device
 work is done by the HIP kernels of ``libpa_fp8.so`` through its C ABI.
 
-Each call is one kernel launch: the partition pass writes the slot
-partials and the last slot of every (sequence, kv head) merges them
-(log-sum-exp) into the output.  The separate reduce kernel is used only when
-a graph capture starts before this stream has its merge counters.
+Scheduling (see ``_schedule``): when the batch has enough (sequence, kv
+head) pairs and bounded contexts, one workgroup per pair walks all of its
+slots and merges them itself (one launch); otherwise workgroups take one or
+a few slots each and the reduce kernel merges them (two launches).  Either
+way the slot partials the reference defines are written whenever the caller
+passes the buffers for them.
 
 Routes (same dispatch order as the reference, :2883 / :3010 / :3123):
   * ``sliding_window > 0``    -> window partition pass + LSE reduce
@@ -158,23 +160,6 @@ def _tmp_dtype_code(t: torch.Tensor) -> int:
     raise ValueError(f"temporary_output must be bfloat16 or float32, got {t.dtype}")
 
 
-# Arrival counters of the in-kernel slot merge, one zeroed int32 buffer per
-# (device, stream); the kernel leaves them zero, so they are reused as is.
-_COUNTERS: dict = {}
-
-
-def _merge_counters(device: torch.device, stream, n: int, capturing: bool) -> Optional[torch.Tensor]:
-    key = (device.index, int(stream.cuda_stream))
-    buf = _COUNTERS.get(key)
-    if buf is not None and buf.numel() >= n:
-        return buf
-    if capturing:
-        return None  # no allocation inside a capture: use the separate reduce launch
-    buf = torch.zeros(max(n, 1024), dtype=torch.int32, device=device)
-    _COUNTERS[key] = buf
-    return buf
-
-
 def _check_int32(name: str, t: torch.Tensor, device: torch.device) -> None:
     if t.dtype != torch.int32:
         raise ValueError(f"`{name}` must be int32, got {t.dtype}")
@@ -193,6 +178,39 @@ def _check_partials(exp_sums, max_logits, tmp, shape, head_size):
         raise ValueError("exp_sums and max_logits must share strides with a contiguous last dimension")
     if tmp.stride(-1) != 1:
         raise ValueError("temporary_output must be contiguous in its last dimension")
+
+
+# A workgroup that owns a whole (sequence, kv head) streams at most this many
+# tokens; beyond it the slots are spread over workgroups (slot mode).
+OWNER_MAX_CONTEXT = 8192
+WAVES_PER_WORKGROUP = 4
+
+
+def _schedule(route: str, batch: int, kv_heads: int, P: int, eqgs: int, capacity: Optional[int], num_cu: int):
+    """Slots per workgroup for one call.
+
+    Owner mode (slots_per_workgroup = P): one workgroup per (sequence, kv
+    head) streams every slot and merges them in LDS, so one launch finishes
+    the decode; used when there are enough (sequence, kv head) pairs to fill
+    the GPU and no sequence can be long (its workgroup would set the
+    kernel's duration).  Slot mode otherwise: one slot per wave when slots
+    are short, else the four waves share a slot; a reduce launch merges.
+    """
+    ncg = -(-eqgs // 16)
+    if P == 1:
+        return 1
+    if (route != "flat" and capacity is not None and capacity <= OWNER_MAX_CONTEXT
+            and batch * kv_heads >= 2 * num_cu and (ncg == 1 or P <= WAVES_PER_WORKGROUP)):
+        return P
+    if route == "sw":
+        slot_tokens = KV_COMPUTE_BLOCK
+    elif capacity is None:
+        return 1
+    else:
+        slot_tokens = -(-(-(-capacity // KV_COMPUTE_BLOCK)) // P) * KV_COMPUTE_BLOCK
+    if slot_tokens <= 16 * 32 and P >= WAVES_PER_WORKGROUP:
+        return WAVES_PER_WORKGROUP
+    return 1
 
 
 class PreparedDecode:
@@ -395,11 +413,14 @@ def prepare_pa_decode(
             raise ValueError("block_tables must be a 2-D int32 tensor with a contiguous last dimension")
     P = int(max_context_partition_num)
 
-    fused = route == "sw" and P <= 1
-    counters = None
+    capacity = None if route == "flat" else int(block_tables.shape[1]) * block_size
+    spw = _schedule(route, batch_size, num_kv_heads, P, eqgs, capacity, _cu_count(dev) if P > 1 else 1)
+    owner = spw >= P
+    user_partials = exp_sums is not None or max_logits is not None or temporary_output is not None
+    fused = owner and not user_partials
     shape = (batch_size, num_kv_heads, P, eqgs)
     if not fused:
-        if is_graph_capturing and (exp_sums is None or max_logits is None or temporary_output is None):
+        if not owner and is_graph_capturing and (exp_sums is None or max_logits is None or temporary_output is None):
             which = "sliding-window" if route == "sw" else "small-block PS"
             raise ValueError(
                 "CUDA graph capture requires preallocated `exp_sums`, `max_logits`, "
@@ -451,11 +472,11 @@ def prepare_pa_decode(
     pa.trans_v = int(trans_v)
     pa.query_dtype = DTYPE_BF16 if query_input_dtype == "bf16" else DTYPE_F16
     pa.softmax_scale = float(softmax_scale)
-    if fused or counters is not None:
+    pa.slots_per_workgroup = spw
+    if owner:
         pa.output = output.data_ptr()
         pa.output_dtype = output_dtype
         pa.stride_out_tok, pa.stride_out_head = output.stride(0), output.stride(1)
-        pa.counters = None if counters is None else counters.data_ptr()
     if fused:
         pa.tmp_dtype = DTYPE_BF16
     else:
@@ -466,11 +487,11 @@ def prepare_pa_decode(
         (pa.stride_to_seq, pa.stride_to_head, pa.stride_to_part, pa.stride_to_group) = temporary_output.stride()[:4]
         pa.tmp_dtype = _tmp_dtype_code(temporary_output)
     keep = (output, query, key_cache, value_cache, context_lengths, block_tables, kv_page_indices, kv_indptr,
-            key_scale, value_scale, exp_sums, max_logits, temporary_output, counters)
+            key_scale, value_scale, exp_sums, max_logits, temporary_output)
     route_name = {"sw": "ps_sw_partitioned", "small": "ps_small_block", "flat": "ps_split_reduce"}[route]
-    if fused:
-        return PreparedDecode("ps_sw_fused_partitioned", pa, None, s, keep)
-    if counters is not None:
+    if route == "sw" and P <= 1:
+        route_name = "ps_sw_fused_partitioned"
+    if owner:
         return PreparedDecode(route_name, pa, None, s, keep)
 
     ra = _lib.ReduceArgs()

@@ -66,12 +66,12 @@ enum pa_fp8_error {
  * covers the token range of pa_fp8_plan_slot(); it stores, per query column
  * e = qi * gqa + g, exp_sums = sum exp(l - m), max_logits = m (the slot's
  * maximum scaled logit, natural-log units; -inf when empty) and the
- * normalised partial output tmp_out.  With `output` set, the same launch
- * also produces the final output: directly when there is one slot (the
- * reference's fused single-partition window kernel,
- * kernels/pa_decode_swa.py:1480-1620), otherwise by an in-kernel
- * log-sum-exp merge (the math of pa_fp8_decode_reduce) done by the last
- * slot of each (sequence, kv head) to finish, so no second launch is needed.
+ * normalised partial output tmp_out.  When one workgroup covers all slots
+ * of its (sequence, kv head) (slots_per_workgroup >= num_partitions) it
+ * also merges them by log-sum-exp (the math of pa_fp8_decode_reduce) and
+ * writes the final output, so one launch completes the decode; with one
+ * slot this is the reference's fused single-partition window kernel
+ * (kernels/pa_decode_swa.py:1480-1620).
  */
 typedef struct pa_fp8_partition_args {
   int32_t abi_version; /* = PA_FP8_ABI_VERSION */
@@ -79,17 +79,10 @@ typedef struct pa_fp8_partition_args {
   float* exp_sums;
   float* max_logits;
   void* tmp_out;
-  /* Final output [B * ql, Hq, D].  NULL: only the slot partials are
-   * written (merge them with pa_fp8_decode_reduce).  Non-NULL with
-   * num_partitions == 1: the output is written directly and the partial
-   * buffers may be NULL.  Non-NULL with num_partitions > 1: the partials
-   * are written and the last slot of each (sequence, kv head) to finish
-   * merges them into the output, which needs `counters`. */
+  /* Final output [B * ql, Hq, D], or NULL.  Written only by a launch whose
+   * workgroups each cover every slot (slots_per_workgroup >=
+   * num_partitions); the partial buffers may then be NULL as well. */
   void* output;
-  /* num_seqs * num_kv_heads int32 arrival counters, all zero on entry; the
-   * kernel leaves them zero.  Required for the in-kernel merge only.
-   * Launches that overlap in time must not share counters. */
-  int32_t* counters;
   /* inputs */
   const void* query;
   const void* key_cache;
@@ -116,6 +109,12 @@ typedef struct pa_fp8_partition_args {
   int32_t num_seqs;
   int32_t num_kv_heads;
   int32_t num_partitions;
+  /* Slots one workgroup walks (its waves stream them back to back):
+   * 1 = one workgroup per slot (grid B * Hkv * P, merge with
+   * pa_fp8_decode_reduce); >= num_partitions = one workgroup per
+   * (sequence, kv head) that also merges the slots into `output`.  More
+   * slots than waves per workgroup (4) needs query_length * gqa <= 16. */
+  int32_t slots_per_workgroup;
   int32_t query_length;
   int32_t query_group_size;
   int32_t head_size;

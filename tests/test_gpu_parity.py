@@ -10,6 +10,7 @@ empty slot must be exactly (0, -inf, 0).
 
 from __future__ import annotations
 
+import contextlib
 import math
 
 import pytest
@@ -17,6 +18,7 @@ import torch
 
 import ctypes
 
+import flydsl_amd.pa_decode as pd
 from flydsl_amd import _lib, pa_decode_ps_launch, prepare_pa_decode, workloads
 from oracle import plan
 from tests._cases import make_case, slot_partials, torch_oracle
@@ -36,7 +38,33 @@ def to_dev(case, device=DEV):
     return out
 
 
-def launch(case, *, P=0, out_dtype=torch.bfloat16, tmp_dtype=torch.bfloat16, flat=False, partials=False):
+SCHEDULES = {
+    "auto": None,
+    "owner": lambda route, batch, kv_heads, P, eqgs, capacity, num_cu: P if (-(-eqgs // 16) == 1 or P <= 4) else 1,
+    "slot": lambda *args: 1,
+    "wave_slot": lambda route, batch, kv_heads, P, eqgs, capacity, num_cu: 4 if P >= 4 else 1,
+}
+
+
+@contextlib.contextmanager
+def schedule(name):
+    """Force the launcher's slots-per-workgroup choice."""
+    saved = pd._schedule
+    if SCHEDULES[name] is not None:
+        pd._schedule = SCHEDULES[name]
+    try:
+        yield
+    finally:
+        pd._schedule = saved
+
+
+def launch(case, *, P=0, out_dtype=torch.bfloat16, tmp_dtype=torch.bfloat16, flat=False, partials=False,
+           sched="auto"):
+    with schedule(sched):
+        return _launch(case, P=P, out_dtype=out_dtype, tmp_dtype=tmp_dtype, flat=flat, partials=partials)
+
+
+def _launch(case, *, P, out_dtype, tmp_dtype, flat, partials):
     q = case["query"]
     out = torch.empty(q.shape, dtype=out_dtype, device=q.device)
     kw = dict(
@@ -107,22 +135,24 @@ def build(name):
     return make_case(batch=6, seed=len(name), **spec)
 
 
+@pytest.mark.parametrize("sched", ["auto", "owner", "slot", "wave_slot"])
 @pytest.mark.parametrize("name", sorted(CASES))
-def test_decode_matches_oracle(name):
+def test_decode_matches_oracle(name, sched):
     case = build(name)
     ref = torch_oracle(case, float_out=False)
-    out, route, _ = launch(to_dev(case))
+    out, route, _ = launch(to_dev(case), sched=sched)
     exp_route = "ps_sw_partitioned" if case["sliding_window"] else "ps_small_block"
     assert route == exp_route
-    assert_parity(out, ref, name)
+    assert_parity(out, ref, f"{name}/{sched}")
 
 
+@pytest.mark.parametrize("sched", ["owner", "slot", "wave_slot"])
 @pytest.mark.parametrize("P", [1, 2, 3, 5, 8, 13])
-def test_any_partition_count(P):
+def test_any_partition_count(P, sched):
     case = make_case(batch=5, ctx_range=(1, 3000), per_token=True, seed=P)
     ref = torch_oracle(case, float_out=False)
-    out, _, _ = launch(to_dev(case), P=P)
-    assert_parity(out, ref, f"P={P}")
+    out, _, _ = launch(to_dev(case), P=P, sched=sched)
+    assert_parity(out, ref, f"P={P}/{sched}")
 
 
 @pytest.mark.parametrize("window", [2, 100, 700])
@@ -160,14 +190,16 @@ def test_plain_value_layout_and_dtypes():
     assert_parity(out16, ref, "f16 query/out")
 
 
+@pytest.mark.parametrize("sched", ["owner", "slot", "wave_slot"])
 @pytest.mark.parametrize("window,ql", [(0, 1), (0, 3), (200, 1), (150, 2)])
-def test_slot_partials_match_oracle(window, ql):
-    """exp_sums / max_logits / tmp_out per slot: same cells as the oracle."""
+def test_slot_partials_match_oracle(window, ql, sched):
+    """exp_sums / max_logits / tmp_out per slot: same cells as the oracle,
+    whichever way the slots are spread over workgroups and waves."""
     case = make_case(batch=5, query_length=ql, num_query_heads=8, num_kv_heads=2, ctx=[ql, 100, 256, 700, 1500],
                      sliding_window=window, per_token=True, seed=51 + ql)
     P = plan.sw_partition_count(window, query_length=ql) if window else 6
     es_r, ml_r, to_r = slot_partials(case, P)
-    _, _, (es, ml, to) = launch(to_dev(case), P=P, partials=True, tmp_dtype=torch.float32)
+    _, _, (es, ml, to) = launch(to_dev(case), P=P, partials=True, tmp_dtype=torch.float32, sched=sched)
     es, ml, to = es.cpu().double(), ml.cpu().double(), to.cpu().double()
     empty = torch.isinf(ml_r)
     assert torch.equal(torch.isinf(ml), empty), "non-empty slot set differs"
@@ -264,46 +296,42 @@ def test_benchmark_config_full_size(name):
     assert_parity(got, ref, f"{name} seqs={seqs}")
 
 
-def test_two_pass_reduce_matches_single_launch():
-    """Partition pass without output + pa_fp8_decode_reduce == the single
-    launch with the in-kernel merge (both through the C ABI)."""
-    case = to_dev(make_case(batch=6, ctx_range=(1, 3000), per_token=True, query_length=2, num_query_heads=16,
-                            num_kv_heads=4, seed=71))
+@pytest.mark.parametrize("P", [4, 6, 9])
+def test_owner_launch_matches_two_pass_reduce(P):
+    """One launch that merges in LDS (owner workgroups) == partition pass
+    with one slot per workgroup + pa_fp8_decode_reduce; same partials."""
+    case = to_dev(make_case(batch=6, ctx_range=(1, 3000), per_token=P != 9, query_length=2 if P != 9 else 1,
+                            num_query_heads=16 if P != 9 else 8, num_kv_heads=4 if P != 9 else 2, seed=71 + P))
     ref = torch_oracle({k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in case.items()},
                        float_out=False)
-    out1, route, (es, ml, to) = launch(case, P=6, partials=True)
-    call = prepare_pa_decode(out1, case["query"], case["key_cache"], case["value_cache"], case["context_lengths"],
-                             None, None, case["softmax_scale"], case["key_scale"], case["value_scale"],
-                             block_tables=case["block_tables"], max_context_partition_num=6, exp_sums=es,
-                             max_logits=ml, temporary_output=to)
-    assert call._ra is None  # single launch
-    # second pass: partials only, then the reduce kernel
-    out2 = torch.zeros_like(out1)
-    pa = _lib.PartitionArgs.from_buffer_copy(call._pa)
-    pa.output = None
-    pa.counters = None
-    lib = _lib.load()
-    sh = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    _lib.check(lib.pa_fp8_decode_partition(ctypes.byref(pa), sh), "partition")
-    ra = _lib.ReduceArgs()
-    ra.abi_version = _lib.ABI_VERSION
-    ra.output, ra.exp_sums, ra.max_logits, ra.tmp_out = out2.data_ptr(), es.data_ptr(), ml.data_ptr(), to.data_ptr()
-    ql, gqa = 2, 4
-    ra.stride_out_seq, ra.stride_out_ql = ql * out2.stride(0), out2.stride(0)
-    ra.stride_out_kv_head, ra.stride_out_group = gqa * out2.stride(1), out2.stride(1)
-    ra.stride_es_seq, ra.stride_es_head, ra.stride_es_part = es.stride()[:3]
-    ra.stride_to_seq, ra.stride_to_head, ra.stride_to_part, ra.stride_to_group = to.stride()[:4]
-    ra.num_seqs, ra.num_kv_heads, ra.num_partitions = 6, 4, 6
-    ra.query_length, ra.query_group_size, ra.head_size = ql, gqa, 128
-    ra.output_dtype, ra.tmp_dtype = _lib.DTYPE_BF16, _lib.DTYPE_BF16
-    _lib.check(lib.pa_fp8_decode_reduce(ctypes.byref(ra), sh), "reduce")
+    out1, _, (es1, ml1, to1) = launch(case, P=P, partials=True, sched="owner", tmp_dtype=torch.float32)
+    out2, _, (es2, ml2, to2) = launch(case, P=P, partials=True, sched="slot", tmp_dtype=torch.float32)
+    assert_parity(out1, ref, f"owner P={P}")
+    assert_parity(out2, ref, f"slot+reduce P={P}")
+    assert torch.equal(torch.isinf(ml1), torch.isinf(ml2))
+    fin = ~torch.isinf(ml1)
+    torch.testing.assert_close(ml1[fin], ml2[fin], atol=1e-4, rtol=1e-5)
+    torch.testing.assert_close(es1[fin], es2[fin], atol=1e-3, rtol=1e-3)
+    torch.testing.assert_close(to1, to2, atol=2e-3, rtol=2e-3)
+
+
+def test_owner_launch_without_partials_writes_only_output():
+    case = to_dev(make_case(batch=4, ctx_range=(1, 2000), seed=77))
+    ref = torch_oracle({k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in case.items()},
+                       float_out=False)
+    with schedule("owner"):
+        call = prepare_pa_decode(torch.empty(case["query"].shape, dtype=torch.bfloat16, device=DEV), case["query"],
+                                 case["key_cache"], case["value_cache"], case["context_lengths"], None, None,
+                                 case["softmax_scale"], case["key_scale"], case["value_scale"],
+                                 block_tables=case["block_tables"], max_context_partition_num=8)
+    assert call._ra is None and call._pa.exp_sums is None
+    call.launch()
     torch.cuda.synchronize()
-    assert_parity(out2, ref, "two-pass")
-    diff = (out1.float() - out2.float()).abs().max().item()
-    assert diff <= 1e-2, diff
+    assert_parity(call._keep[0], ref, "owner, output only")
 
 
-def test_graph_capture_with_in_kernel_merge():
+@pytest.mark.parametrize("sched", ["owner", "slot"])
+def test_graph_capture_every_schedule(sched):
     case = to_dev(make_case(batch=5, ctx_range=(1, 2500), seed=81, per_token=True))
     P = 8
     b = 5
@@ -319,14 +347,15 @@ def test_graph_capture_with_in_kernel_merge():
                                    case["value_scale"], block_tables=case["block_tables"],
                                    max_context_partition_num=P, exp_sums=es, max_logits=ml, temporary_output=to)
 
-    with torch.cuda.stream(s):
-        call()  # eager call on the capture stream sets up its merge counters
-    torch.cuda.synchronize()
-    eager = out.clone()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(s):
-        with torch.cuda.graph(g, stream=s):
+    with schedule(sched):
+        with torch.cuda.stream(s):
             call()
+        torch.cuda.synchronize()
+        eager = out.clone()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                call()
     torch.cuda.synchronize()
     for i in range(4):
         out.zero_()
@@ -334,7 +363,8 @@ def test_graph_capture_with_in_kernel_merge():
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i}"
-        with torch.cuda.stream(s):
-            call()
+        with schedule(sched):
+            with torch.cuda.stream(s):
+                call()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"eager after replay {i}"

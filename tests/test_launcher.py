@@ -1,0 +1,134 @@
+"""Host-side launcher logic without a GPU: validation errors mirror the
+reference launcher (kernels/pa_decode_fp8.py:1862-1919, 2859-2863,
+3014-3018, 3030-3034), the schedule choice, and the C-ABI arguments it
+marshals (checked field by field on a stub stream; nothing is launched)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import flydsl_amd.pa_decode as pd
+from flydsl_amd import prepare_pa_decode, workloads
+from tests._cases import make_case
+
+
+class StubStream:
+    cuda_stream = 0
+
+
+@pytest.fixture(autouse=True)
+def no_device(monkeypatch):
+    monkeypatch.setattr(pd, "_cu_count", lambda device=None: 256)
+
+
+def prep(case, **kw):
+    out = kw.pop("output", None)
+    if out is None:
+        out = torch.empty(case["query"].shape, dtype=torch.bfloat16)
+    return prepare_pa_decode(out, case["query"], case["key_cache"], case["value_cache"], case["context_lengths"],
+                             kw.pop("kv_page_indices", None), kw.pop("kv_indptr", None), case["softmax_scale"],
+                             case["key_scale"], case["value_scale"], stream=StubStream(),
+                             block_tables=kw.pop("block_tables", case["block_tables"]), **kw)
+
+
+def test_small_block_slot_mode_marshalling():
+    case = make_case(batch=3, ctx=[10, 300, 1000], per_token=True, seed=1)
+    call = prep(case)
+    a = call._pa
+    assert call.route == "ps_small_block"
+    assert a.num_partitions == 8 and a.slots_per_workgroup in (1, 4)
+    assert call._ra is not None  # partials + reduce launch
+    assert a.per_token_kv == 1 and a.trans_v == 1 and a.block_size == 16
+    assert a.num_seqs == 3 and a.num_kv_heads == 2 and a.query_group_size == 4 and a.query_length == 1
+    assert a.stride_k_block == case["key_cache"].stride(0)
+    assert a.stride_ks_block == case["key_scale"].stride(0) and a.stride_ks_head == case["key_scale"].stride(1)
+    assert a.output is None  # slot mode: the reduce writes the output
+    assert call._ra.num_partitions == 8
+
+
+def test_owner_mode_for_large_uniform_batch():
+    cfg = workloads.DecodeConfig("x", 64, 1, 32, 8, 16, "fixed:64", False)
+    case = workloads.build_inputs(cfg, device="cpu", seed=0, context_lengths=[4096] * 64)
+    call = prep(case)
+    assert call._pa.slots_per_workgroup == call._pa.num_partitions == 8
+    assert call._ra is None and call._pa.output is not None
+    assert call._pa.exp_sums is None  # caller passed no partial buffers
+
+
+def test_owner_mode_still_writes_requested_partials():
+    cfg = workloads.DecodeConfig("x", 64, 1, 32, 8, 16, "fixed:64", False)
+    case = workloads.build_inputs(cfg, device="cpu", seed=0, context_lengths=[4096] * 64)
+    es = torch.empty(64, 8, 8, 4)
+    call = prep(case, max_context_partition_num=8, exp_sums=es, max_logits=torch.empty_like(es),
+                temporary_output=torch.empty(64, 8, 8, 4, 128, dtype=torch.bfloat16))
+    assert call._ra is None and call._pa.exp_sums == es.data_ptr()
+
+
+def test_schedule_policy():
+    # long contexts or few (sequence, kv head) pairs: slot mode
+    assert pd._schedule("small", 128, 8, 8, 4, 27000, 256) == 1
+    assert pd._schedule("small", 8, 8, 8, 4, 4096, 256) == 4
+    assert pd._schedule("small", 64, 8, 8, 4, 4096, 256) == 8
+    assert pd._schedule("sw", 32, 8, 17, 4, 32768, 256) == 4
+    assert pd._schedule("small", 256, 4, 4, 64, 8192, 256) == 4
+    assert pd._schedule("small", 256, 4, 8, 64, 8192, 256) == 1  # 4 column groups: no multi-slot waves
+    assert pd._schedule("flat", 64, 8, 8, 4, None, 256) == 1
+    assert pd._schedule("small", 4, 2, 1, 4, 512, 256) == 1
+
+
+def test_window_route_and_fused_single_slot():
+    case = make_case(batch=2, ctx=[500, 900], sliding_window=100, seed=2)
+    call = prep(case, sliding_window=100)
+    assert call.route == "ps_sw_partitioned" and call._pa.sliding_window == 100
+    assert call._pa.num_partitions == 2  # cdiv(100 + 1 - 1, 256) + 1
+    call1 = prep(case, sliding_window=100, max_context_partition_num=1)
+    assert call1.route == "ps_sw_fused_partitioned" and call1._ra is None and call1._pa.exp_sums is None
+
+
+def test_flat_route_uses_page_list():
+    case = make_case(batch=2, block_size=1024, ctx=[100, 3000], seed=3)
+    pages = torch.tensor([0, 1, 2, 3], dtype=torch.int32)
+    indptr = torch.tensor([0, 1, 4], dtype=torch.int32)
+    call = prep(case, block_tables=None, kv_page_indices=pages, kv_indptr=indptr)
+    assert call.route == "ps_split_reduce"
+    assert call._pa.kv_indptr == indptr.data_ptr() and call._pa.block_tables == pages.data_ptr()
+
+
+def test_rejects_packed_fp8_query():
+    case = make_case(batch=1, ctx=[10], seed=4)
+    case["query"] = case["query"].to(torch.float8_e4m3fn)
+    with pytest.raises(ValueError, match="no longer accepts host query_scale"):
+        prep(case)
+
+
+def test_rejects_bad_dtypes_and_shapes():
+    case = make_case(batch=1, ctx=[10], seed=5)
+    with pytest.raises(ValueError, match="Unsupported query dtype"):
+        c = dict(case)
+        c["query"] = case["query"].float()
+        prep(c)
+    with pytest.raises(ValueError, match="Unsupported output dtype"):
+        prep(case, output=torch.empty(case["query"].shape, dtype=torch.int32))
+    with pytest.raises(ValueError, match="requires `block_tables`"):
+        prep(case, block_tables=None)
+    with pytest.raises(ValueError, match="must be int32"):
+        prep(case, block_tables=case["block_tables"].long())
+    c = dict(case)
+    c["query"] = torch.zeros(1, 8, 64, dtype=torch.bfloat16)
+    with pytest.raises((ValueError, NotImplementedError)):
+        prep(c, output=torch.empty(1, 8, 64, dtype=torch.bfloat16))
+
+
+def test_rejects_too_few_window_slots():
+    case = make_case(batch=1, ctx=[5000], sliding_window=1000, seed=6)
+    with pytest.raises(ValueError, match="cannot cover a window"):
+        prep(case, sliding_window=1000, max_context_partition_num=2)
+
+
+def test_partial_buffer_shape_checked():
+    case = make_case(batch=2, ctx=[10, 20], seed=7)
+    es = torch.empty(2, 2, 3, 4)
+    with pytest.raises(ValueError, match="exp_sums/max_logits must have shape"):
+        prep(case, max_context_partition_num=8, exp_sums=es, max_logits=torch.empty_like(es),
+             temporary_output=torch.empty(2, 2, 3, 4, 128, dtype=torch.bfloat16))
