@@ -5,8 +5,10 @@ decode step, on the Llama-3-8B-shaped configuration (batch 64, 32 query / 8
 KV heads, head 128, 16-token pages, every context 4096, per-tensor fp8
 scales) unless ``--config`` names another.
 
-A step is one ``pa_decode_ps_launch`` call (partition pass + LSE reduce)
-with scratch preallocated.  Inputs are resident in HBM; the timed steps
+A step is one ``pa_decode_ps_launch`` call as the reference harness makes
+it (recommended split count; the window route with preallocated partials):
+one launch when workgroups own whole (sequence, kv head) pairs, else the
+partition pass plus the LSE reduce.  Inputs are resident in HBM; the timed steps
 rotate over several independent KV-cache copies whose total exceeds twice
 the 256 MB Infinity Cache, so no step reads KV that the previous step left
 in the cache.  ``value`` = attended K+V bytes / step time.
@@ -180,12 +182,16 @@ def run_config(name: str, args) -> dict:
     tmp = torch.empty((B, hkv, P, eq, 128), device=dev, dtype=torch.bfloat16)
     out = torch.empty(case["query"].shape, device=dev, dtype=torch.bfloat16)
 
+    # The call the reference's own harness makes for this route
+    # (tests/kernels/test_pa.py:849-900): recommended split count, no
+    # caller-side scratch (the window route preallocates its partials).
+    sw_scratch = dict(exp_sums=es, max_logits=ml, temporary_output=tmp) if cfg.sliding_window else {}
+
     def step(i):
         k, v, ks, vs = caches[i % copies]
         return pa_decode_ps_launch(out, case["query"], k, v, case["context_lengths"], None, None,
                                    case["softmax_scale"], ks, vs, sliding_window=cfg.sliding_window,
-                                   block_tables=case["block_tables"], max_context_partition_num=P,
-                                   exp_sums=es, max_logits=ml, temporary_output=tmp)
+                                   block_tables=case["block_tables"], max_context_partition_num=P, **sw_scratch)
 
     route = None
     for i in range(args.warmup):
@@ -209,7 +215,7 @@ def run_config(name: str, args) -> dict:
         calls.append(prepare_pa_decode(out, case["query"], k, v, case["context_lengths"], None, None,
                                        case["softmax_scale"], ks, vs, sliding_window=cfg.sliding_window,
                                        block_tables=case["block_tables"], max_context_partition_num=P,
-                                       exp_sums=es, max_logits=ml, temporary_output=tmp))
+                                       **sw_scratch))
     for i in range(max(3, args.warmup)):
         calls[i % copies].launch()
     k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

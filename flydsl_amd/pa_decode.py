@@ -199,8 +199,11 @@ def _schedule(route: str, batch: int, kv_heads: int, P: int, eqgs: int, capacity
     ncg = -(-eqgs // 16)
     if P == 1:
         return 1
+    multi_ok = ncg == 1 or P <= WAVES_PER_WORKGROUP
+    if route == "sw" and batch * kv_heads >= num_cu and multi_ok:
+        return P  # a window bounds every (sequence, kv head)'s work
     if (route != "flat" and capacity is not None and capacity <= OWNER_MAX_CONTEXT
-            and batch * kv_heads >= 2 * num_cu and (ncg == 1 or P <= WAVES_PER_WORKGROUP)):
+            and batch * kv_heads >= 2 * num_cu and multi_ok):
         return P
     if route == "sw":
         slot_tokens = KV_COMPUTE_BLOCK
@@ -418,6 +421,11 @@ def prepare_pa_decode(
     owner = spw >= P
     user_partials = exp_sums is not None or max_logits is not None or temporary_output is not None
     fused = owner and not user_partials
+    if fused and route != "sw":
+        # Nobody observes the slot partials: let each of the workgroup's
+        # waves stream one contiguous quarter of the context.  (The window
+        # route keeps its 256-token tiles, whose layout its slots define.)
+        P = spw = min(P, WAVES_PER_WORKGROUP)
     shape = (batch_size, num_kv_heads, P, eqgs)
     if not fused:
         if not owner and is_graph_capturing and (exp_sums is None or max_logits is None or temporary_output is None):
