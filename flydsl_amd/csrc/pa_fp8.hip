@@ -787,10 +787,12 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
 }
 
 // One wave per (sequence, kv head, column); lane l covers head dims 2l,
-// 2l+1.  The slot statistics are read once, one slot per lane (up to 64
-// per pass), reduced across the wave, and every partial row is fetched
-// before any is used, so a row costs one round trip to memory per 64 slots.
+// 2l+1.  For each batch of up to 32 slots every load -- the slot's max and
+// sum (one slot per lane) and the lane's two values of every slot's partial
+// row -- is issued before any is used, so a row costs one memory round trip
+// per 32 slots; max and sum are then reduced across the wave.
 __global__ __launch_bounds__(256) void pa_fp8_lse_reduce_kernel(const pa_fp8_reduce_args a) {
+  constexpr int kBatch = 32;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int eq = a.query_length * a.query_group_size;
@@ -803,61 +805,55 @@ __global__ __launch_bounds__(256) void pa_fp8_lse_reduce_kernel(const pa_fp8_red
   const int64_t sbase = (int64_t)b * a.stride_es_seq + (int64_t)h * a.stride_es_head + e;
   const int64_t tbase =
       (int64_t)b * a.stride_to_seq + (int64_t)h * a.stride_to_head + (int64_t)e * a.stride_to_group + 2 * lane;
-  // pass 1: global max over slots
-  float M = kNegInf;
-  for (int p0 = 0; p0 < P; p0 += 64) {
+  // Running log-sum-exp state over the batches.
+  float M = kNegInf, tot = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  for (int p0 = 0; p0 < P; p0 += kBatch) {
+    const int n = P - p0 < kBatch ? P - p0 : kBatch;
     const int p = p0 + lane;
-    const float m = p < P ? a.max_logits[sbase + p * a.stride_es_part] : kNegInf;
-    M = fmaxf(M, m);
-  }
+    const bool mine = lane < n;
+    const float m = mine ? a.max_logits[sbase + p * a.stride_es_part] : kNegInf;
+    const float es = mine ? a.exp_sums[sbase + p * a.stride_es_part] : 0.0f;
+    float x0[kBatch], x1[kBatch];
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, shfl_xor(M, o));
-  float o0 = 0.0f, o1 = 0.0f, tot = 0.0f;
-  if (M != kNegInf) {
-    for (int p0 = 0; p0 < P; p0 += 64) {
-      const int p = p0 + lane;
-      float w = 0.0f;
-      if (p < P) {
-        const float m = a.max_logits[sbase + p * a.stride_es_part];
-        w = m == kNegInf ? 0.0f : a.exp_sums[sbase + p * a.stride_es_part] * __expf(m - M);
-      }
-      float wsum = w;
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) wsum += shfl_xor(wsum, o);
-      tot += wsum;
-      const int n = P - p0 < 64 ? P - p0 : 64;
-      // fetch all partial rows of this pass, then combine
-      constexpr int kBatch = 16;
-      for (int q0 = 0; q0 < n; q0 += kBatch) {
-        float x0[kBatch], x1[kBatch];
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i) {
-          const int q = q0 + i < n ? q0 + i : n - 1;
-          const int64_t off = tbase + (int64_t)(p0 + q) * a.stride_to_part;
-          if (a.tmp_dtype == PA_DTYPE_F32) {
-            const f32x2 t = *(const f32x2*)((const float*)a.tmp_out + off);
-            x0[i] = t[0];
-            x1[i] = t[1];
-          } else {
-            const uint32_t t = *(const uint32_t*)((const uint16_t*)a.tmp_out + off);
-            x0[i] = bf16_bits_to_f32(t & 0xffffu);
-            x1[i] = bf16_bits_to_f32(t >> 16);
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i) {
-          const float wi = __shfl(w, q0 + i, 64);
-          if (q0 + i < n) {
-            o0 += wi * x0[i];
-            o1 += wi * x1[i];
-          }
-        }
+    for (int i = 0; i < kBatch; ++i) {
+      const int q = i < n ? i : n - 1;
+      const int64_t off = tbase + (int64_t)(p0 + q) * a.stride_to_part;
+      if (a.tmp_dtype == PA_DTYPE_F32) {
+        const f32x2 t = *(const f32x2*)((const float*)a.tmp_out + off);
+        x0[i] = t[0];
+        x1[i] = t[1];
+      } else {
+        const uint32_t t = *(const uint32_t*)((const uint16_t*)a.tmp_out + off);
+        x0[i] = bf16_bits_to_f32(t & 0xffffu);
+        x1[i] = bf16_bits_to_f32(t >> 16);
       }
     }
-    const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
-    o0 *= inv;
-    o1 *= inv;
+    float mb = m;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mb = fmaxf(mb, shfl_xor(mb, o));
+    const float Mn = fmaxf(M, mb);
+    if (Mn == kNegInf) continue;  // every slot so far empty
+    const float w = m == kNegInf ? 0.0f : es * __expf(m - Mn);
+    float ws = w;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ws += shfl_xor(ws, o);
+    const float fold = M == kNegInf ? 0.0f : __expf(M - Mn);
+    tot = tot * fold + ws;
+    o0 *= fold;
+    o1 *= fold;
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const float wi = __shfl(w, i, 64);
+      if (i < n) {
+        o0 += wi * x0[i];
+        o1 += wi * x1[i];
+      }
+    }
+    M = Mn;
   }
+  const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
+  o0 *= inv;
+  o1 *= inv;
   const int gqa = a.query_group_size;
   const int qi = e / gqa, g = e - qi * gqa;
   const int64_t off = (int64_t)b * a.stride_out_seq + (int64_t)qi * a.stride_out_ql +
