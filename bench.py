@@ -151,6 +151,13 @@ def load_traffic(name: str):
         return None
 
 
+KERNEL_OF_ENTRY = {
+    "pa_fp8_decode_partition": "pa_fp8_partition_kernel",
+    "pa_fp8_decode_balanced": "pa_fp8_stream_kernel (balanced split)",
+    "pa_fp8_decode_worklist": "pa_fp8_stream_kernel (work list)",
+}
+
+
 def run_config(name: str, args) -> dict:
     import torch
 
@@ -207,26 +214,30 @@ def run_config(name: str, args) -> dict:
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / args.steps
 
-    # Live per-kernel timing of the decode kernel (the dominant and, with
-    # the in-kernel slot merge, the only kernel of a step), launched through
-    # the C ABI with pre-marshalled arguments on this same stream.
+    # Live timing of the step's decode kernel (the dominant one; with the
+    # in-kernel slot merge the only one), launched alone through its C-ABI
+    # entry point with pre-marshalled arguments on this same stream.
     calls = []
     for k, v, ks, vs in caches:
         calls.append(prepare_pa_decode(out, case["query"], k, v, case["context_lengths"], None, None,
                                        case["softmax_scale"], ks, vs, sliding_window=cfg.sliding_window,
                                        block_tables=case["block_tables"], max_context_partition_num=P,
                                        **sw_scratch))
+    kernel_name, _ = calls[0].kernels()[0]
+    decode = [c.kernels()[0][1] for c in calls]
     for i in range(max(3, args.warmup)):
         calls[i % copies].launch()
     k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     k0.record(stream)
     for i in range(args.steps):
-        calls[i % copies].launch()
+        rc = decode[i % copies]()
+        if rc != 0:
+            raise RuntimeError(f"{kernel_name} failed: {rc}")
     k1.record(stream)
     torch.cuda.synchronize()
     kern_ms = k0.elapsed_time(k1) / args.steps
-    kernels_per_step = 1 if calls[0]._ra is None else 2
+    kernels_per_step = len(calls[0].kernels())
 
     achieved = kv / (kern_ms * 1e-3) / 1e9
     value = kv / (ms * 1e-3) / 1e9
@@ -265,7 +276,7 @@ def run_config(name: str, args) -> dict:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "pa_fp8_partition_kernel (slot partials + in-kernel LSE merge)",
+            "kernel": KERNEL_OF_ENTRY[kernel_name],
             "kernels_per_step": kernels_per_step,
             "achieved": round(achieved, 2),
             "peak": PEAK_HBM_GBPS,

@@ -38,6 +38,14 @@ EXPORTED_SYMBOLS = (
     "pa_fp8_plan_visible",
     "pa_fp8_version",
     "pa_fp8_error_string",
+    "pa_fp8_decode_worklist",
+    "pa_fp8_decode_balanced",
+    "pa_fp8_merge_balanced",
+    "pa_fp8_balanced_workspace_bytes",
+    "pa_fp8_stream_workers",
+    "pa_fp8_reduce_worklist",
+    "pa_fp8_worklist_sizes",
+    "pa_fp8_plan_worklist",
 )
 
 _i32 = ctypes.c_int32
@@ -131,6 +139,79 @@ class ReduceArgs(ctypes.Structure):
     ]
 
 
+class StreamArgs(ctypes.Structure):
+    """Mirror of ``pa_fp8_stream_args``."""
+
+    _fields_ = [
+        ("abi_version", _i32),
+        ("output", _vp),
+        ("query", _vp),
+        ("key_cache", _vp),
+        ("value_cache", _vp),
+        ("block_tables", _vp),
+        ("kv_indptr", _vp),
+        ("context_lengths", _vp),
+        ("key_scale", _vp),
+        ("value_scale", _vp),
+        ("work_indptr", _vp),
+        ("work_info", _vp),
+        ("partition_indptr", _vp),
+        ("partial_output", _vp),
+        ("partial_lse", _vp),
+        ("stride_q_tok", _i64),
+        ("stride_q_head", _i64),
+        ("stride_k_block", _i64),
+        ("stride_k_head", _i64),
+        ("stride_v_block", _i64),
+        ("stride_v_head", _i64),
+        ("stride_bt_seq", _i64),
+        ("stride_ks_block", _i64),
+        ("stride_ks_head", _i64),
+        ("stride_out_tok", _i64),
+        ("stride_out_head", _i64),
+        ("stride_po_row", _i64),
+        ("stride_pl_row", _i64),
+        ("num_seqs", _i32),
+        ("num_kv_heads", _i32),
+        ("query_length", _i32),
+        ("query_group_size", _i32),
+        ("head_size", _i32),
+        ("block_size", _i32),
+        ("num_blocks", _i32),
+        ("max_blocks_per_seq", _i32),
+        ("sliding_window", _i32),
+        ("per_token_kv", _i32),
+        ("trans_v", _i32),
+        ("query_dtype", _i32),
+        ("output_dtype", _i32),
+        ("num_workers", _i32),
+        ("softmax_scale", ctypes.c_float),
+    ]
+
+
+class WorklistReduceArgs(ctypes.Structure):
+    """Mirror of ``pa_fp8_worklist_reduce_args``."""
+
+    _fields_ = [
+        ("abi_version", _i32),
+        ("output", _vp),
+        ("partial_output", _vp),
+        ("partial_lse", _vp),
+        ("reduce_indptr", _vp),
+        ("reduce_final_map", _vp),
+        ("reduce_partial_map", _vp),
+        ("stride_out_tok", _i64),
+        ("stride_out_head", _i64),
+        ("stride_po_row", _i64),
+        ("stride_pl_row", _i64),
+        ("num_groups", _i32),
+        ("num_query_heads", _i32),
+        ("head_size", _i32),
+        ("max_query_length", _i32),
+        ("output_dtype", _i32),
+    ]
+
+
 _LIB: Optional[ctypes.CDLL] = None
 
 
@@ -163,6 +244,22 @@ def load(path: Optional[str] = None) -> ctypes.CDLL:
     lib.pa_fp8_version.restype = ctypes.c_char_p
     lib.pa_fp8_error_string.argtypes = [ctypes.c_int]
     lib.pa_fp8_error_string.restype = ctypes.c_char_p
+    lib.pa_fp8_decode_worklist.argtypes = [ctypes.POINTER(StreamArgs), _vp]
+    lib.pa_fp8_decode_worklist.restype = ctypes.c_int
+    lib.pa_fp8_decode_balanced.argtypes = [ctypes.POINTER(StreamArgs), _vp, _i64, _vp]
+    lib.pa_fp8_decode_balanced.restype = ctypes.c_int
+    lib.pa_fp8_merge_balanced.argtypes = [ctypes.POINTER(StreamArgs), _vp, _i64, _vp]
+    lib.pa_fp8_merge_balanced.restype = ctypes.c_int
+    lib.pa_fp8_balanced_workspace_bytes.argtypes = [ctypes.c_int] * 5
+    lib.pa_fp8_balanced_workspace_bytes.restype = _i64
+    lib.pa_fp8_stream_workers.argtypes = [ctypes.c_int] * 4
+    lib.pa_fp8_stream_workers.restype = ctypes.c_int
+    lib.pa_fp8_reduce_worklist.argtypes = [ctypes.POINTER(WorklistReduceArgs), _vp]
+    lib.pa_fp8_reduce_worklist.restype = ctypes.c_int
+    lib.pa_fp8_worklist_sizes.argtypes = [ctypes.c_int] * 3 + [ctypes.POINTER(ctypes.c_int)] * 2
+    lib.pa_fp8_worklist_sizes.restype = ctypes.c_int
+    lib.pa_fp8_plan_worklist.argtypes = [_vp] + [ctypes.c_int] * 6 + [_vp] * 5
+    lib.pa_fp8_plan_worklist.restype = ctypes.c_int
     if path is None:
         _LIB = lib
     return lib
@@ -195,3 +292,50 @@ def recommended_splits(num_seqs, num_kv_heads, split_kv_blocks, sliding_window, 
             num_seqs, num_kv_heads, split_kv_blocks, sliding_window, partition_tokens, query_length, num_cu
         )
     )
+
+
+def stream_workers(num_cu: int, query_length: int, query_group_size: int, per_token_kv: bool) -> int:
+    n = int(load().pa_fp8_stream_workers(num_cu, query_length, query_group_size, int(per_token_kv)))
+    if n < 0:
+        check(n, "pa_fp8_stream_workers")
+    return n
+
+
+def balanced_workspace_bytes(num_seqs: int, num_kv_heads: int, query_length: int, query_group_size: int,
+                             num_workers: int) -> int:
+    n = int(load().pa_fp8_balanced_workspace_bytes(num_seqs, num_kv_heads, query_length, query_group_size,
+                                                   num_workers))
+    if n < 0:
+        check(n, "pa_fp8_balanced_workspace_bytes")
+    return n
+
+
+def worklist_sizes(num_seqs: int, num_kv_heads: int, num_cu: int):
+    mw, ms = ctypes.c_int(), ctypes.c_int()
+    check(load().pa_fp8_worklist_sizes(num_seqs, num_kv_heads, num_cu, mw, ms), "pa_fp8_worklist_sizes")
+    return mw.value, ms.value
+
+
+def plan_worklist(context_lengths, num_kv_heads: int, query_group_size: int, query_length: int, num_cu: int,
+                  kv_granularity: int = 256):
+    """Host work list (numpy int32 arrays); returns (num_works, dict)."""
+    import numpy as np
+
+    ctx = np.ascontiguousarray(np.asarray(context_lengths, dtype=np.int32))
+    B = int(ctx.shape[0])
+    max_works, max_split = worklist_sizes(B, num_kv_heads, num_cu)
+    out = {
+        "work_indptr": np.zeros(num_cu + 1, np.int32),
+        "work_info": np.zeros((max(max_works, 0), 8), np.int32),
+        "reduce_indptr": np.zeros(B + 1, np.int32),
+        "reduce_final_map": np.zeros((B, 2), np.int32),
+        "reduce_partial_map": np.zeros(max(max_split, 1), np.int32),
+    }
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    n = int(load().pa_fp8_plan_worklist(ptr(ctx), B, num_kv_heads, query_group_size, query_length, num_cu,
+                                        kv_granularity, ptr(out["work_indptr"]), ptr(out["work_info"]),
+                                        ptr(out["reduce_indptr"]), ptr(out["reduce_final_map"]),
+                                        ptr(out["reduce_partial_map"])))
+    if n < 0:
+        check(n, "pa_fp8_plan_worklist")
+    return n, out

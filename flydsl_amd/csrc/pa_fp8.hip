@@ -33,8 +33,11 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "pa_fp8.h"
 #include "pa_plan.h"
+#include "pa_worklist.h"
 
 namespace {
 
@@ -212,6 +215,225 @@ __device__ __forceinline__ void store_stats(const pa_fp8_partition_args& a, int 
                       (int64_t)slot * a.stride_es_part + e;
   a.exp_sums[off] = exp_sum;
   a.max_logits[off] = max_logit;
+}
+
+// Online-softmax state of one wave over NCG 16-column query blocks: base-2
+// running maximum m2, lane-partial sum lsum of 256 * 2^(l - m2), and the PV
+// accumulator (acc[cg][j][i] = head dim 16j + 4*grp + i of column c16);
+// vsmax is the running maximum of the per-token value scales.
+template <int NCG>
+struct WaveState {
+  float m2[NCG];
+  float lsum[NCG];
+  f32x4 acc[NCG][8];
+  float vsmax;
+  __device__ __forceinline__ void reset() {
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) {
+      m2[cg] = kNegInf;
+      lsum[cg] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[cg][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    vsmax = 0.0f;
+  }
+};
+
+// Query columns of one (sequence, kv head) as MFMA B operands, with the
+// keys each column may see.  lo_all/hi_all bound the union of the columns'
+// visible ranges, lo_max/hi_min their intersection (no masking needed).
+template <int NCG>
+struct QueryTile {
+  i32x8 hi[NCG], lo[NCG];
+  float fac[NCG];  // base-2 logit factor per column
+  int vis_lo[NCG], vis_hi[NCG];
+  int lo_all, hi_all, lo_max, hi_min;
+};
+
+// Raw query rows (bf16 or f16 bits) -> fp8 hi + lo B operands.  Lane
+// (grp, c16) holds, for column cg * 16 + c16, the 32 head dims of 16-dim
+// chunks grp and grp + 4 in qraw[cg][0..3] (8 dims each).  The column is
+// scaled by a power of two putting its amax into [128, 256), which is exact.
+template <int NCG>
+__device__ __forceinline__ void prepare_query(QueryTile<NCG>& q, const i32x4 (&qraw)[NCG][4], int query_dtype,
+                                              float logit_scale, int ctx, int ql, int gqa, int W, int c16) {
+  const int eq = ql * gqa;
+#pragma unroll
+  for (int cg = 0; cg < NCG; ++cg) {
+    const int e = cg * 16 + c16;
+    const bool valid = e < eq;
+    const int qi = valid ? e / gqa : 0;
+    float v[32];
+    if (query_dtype == PA_DTYPE_F16) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t w = (uint32_t)qraw[cg][i >> 2][i & 3];
+        v[2 * i] = f16_bits_to_f32(w & 0xffffu);
+        v[2 * i + 1] = f16_bits_to_f32(w >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t w = (uint32_t)qraw[cg][i >> 2][i & 3];
+        v[2 * i] = bf16_bits_to_f32(w & 0xffffu);
+        v[2 * i + 1] = bf16_bits_to_f32(w >> 16);
+      }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = max_over_groups(amax);
+    int sexp = 261 - (int)((__float_as_uint(amax) >> 23) & 0xffu);
+    sexp = sexp < 1 ? 1 : (sexp > 254 ? 254 : sexp);
+    const float sq = amax > 0.0f ? __uint_as_float((uint32_t)sexp << 23) : 1.0f;
+#pragma unroll
+    for (int sI = 0; sI < 4; ++sI) {
+      float xs[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xs[i] = v[8 * sI + i] * sq;
+      long hi, lo;
+      split8_fp8(xs, hi, lo);
+      q.hi[cg][2 * sI] = (int)(uint32_t)hi;
+      q.hi[cg][2 * sI + 1] = (int)(uint32_t)((uint64_t)hi >> 32);
+      q.lo[cg][2 * sI] = (int)(uint32_t)lo;
+      q.lo[cg][2 * sI + 1] = (int)(uint32_t)((uint64_t)lo >> 32);
+    }
+    q.fac[cg] = logit_scale / sq;
+    int lo = 0, hi = 0;
+    if (valid) pa_plan_visible(ctx, qi, ql, W, &lo, &hi);
+    q.vis_lo[cg] = lo;
+    q.vis_hi[cg] = hi;
+  }
+  // lo and hi grow with qi: the extremes come from the first and last query.
+  pa_plan_visible(ctx, 0, ql, W, &q.lo_all, &q.hi_min);
+  pa_plan_visible(ctx, ql - 1, ql, W, &q.lo_max, &q.hi_all);
+}
+
+// One 32-token chunk of keys and values, staged in LDS at sk (keys: two
+// 16-token halves [8 dim chunks][16 tokens][16 B], kKHalf apart; values:
+// [2 halves][128 head dims][16 tokens]; per-token K then V scales), folded
+// into the wave's online softmax.  tb is the chunk's first token.
+template <int NCG, bool PER_TOKEN>
+__device__ __forceinline__ void compute_chunk(WaveState<NCG>& s, const QueryTile<NCG>& q,
+                                              const LDS_AS unsigned char* sk, int krow, int grp, int c16, int tb) {
+  const LDS_AS unsigned char* sv = sk + kKBytes;
+  const i32x4 ka0 = *(const LDS_AS i32x4*)(sk + krow + grp * 256);
+  const i32x4 ka1 = *(const LDS_AS i32x4*)(sk + krow + (grp + 4) * 256);
+  const i32x4 kb0 = *(const LDS_AS i32x4*)(sk + krow + 64 + grp * 256);
+  const i32x4 kb1 = *(const LDS_AS i32x4*)(sk + krow + 64 + (grp + 4) * 256);
+  const i32x8 KA = {ka0[0], ka0[1], ka0[2], ka0[3], ka1[0], ka1[1], ka1[2], ka1[3]};
+  const i32x8 KB = {kb0[0], kb0[1], kb0[2], kb0[3], kb1[0], kb1[1], kb1[2], kb1[3]};
+
+  // value operands: head dim 16j + c16, tokens 8*grp .. 8*grp+7
+  long V[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) V[j] = *(const LDS_AS long*)(sv + (grp >> 1) * 2048 + (16 * j + c16) * 16 + 8 * (grp & 1));
+
+  // This lane's 8 tokens: tb + 8*grp + j.
+  const int tok0 = tb + 8 * grp;
+  const bool interior = tb >= q.lo_max && tb + kChunk <= q.hi_min;
+  const bool edge = tb < q.lo_all || tb + kChunk > q.hi_all;
+  if (edge) {
+    // Zero value bytes of tokens no query sees (stale page tails).
+    uint64_t keep = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int t = tok0 + j;
+      if (t >= q.lo_all && t < q.hi_all) keep |= (uint64_t)0xff << (8 * j);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) V[j] = (long)((uint64_t)V[j] & keep);
+  }
+
+  float ksc[8], vsc[8];
+  float vratio = 1.0f, vinv = 1.0f;
+  if (PER_TOKEN) {
+    const LDS_AS float* ss = (const LDS_AS float*)(sv + kVBytes);
+    f32x4 k0 = *(const LDS_AS f32x4*)(ss + 8 * grp);
+    f32x4 k1 = *(const LDS_AS f32x4*)(ss + 8 * grp + 4);
+    f32x4 w0 = *(const LDS_AS f32x4*)(ss + 32 + 8 * grp);
+    f32x4 w1 = *(const LDS_AS f32x4*)(ss + 32 + 8 * grp + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      ksc[j] = k0[j];
+      ksc[4 + j] = k1[j];
+      vsc[j] = w0[j];
+      vsc[4 + j] = w1[j];
+    }
+    if (edge) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int t = tok0 + j;
+        if (!(t >= q.lo_all && t < q.hi_all)) vsc[j] = 0.0f;
+      }
+    }
+    float cmax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) cmax = fmaxf(cmax, vsc[j]);
+    cmax = max_over_groups(cmax);
+    const float vnew = fmaxf(s.vsmax, cmax);
+    vratio = vnew > 0.0f ? s.vsmax / vnew : 1.0f;
+    vinv = vnew > 0.0f ? 1.0f / vnew : 0.0f;
+    s.vsmax = vnew;
+  }
+
+#pragma unroll
+  for (int cg = 0; cg < NCG; ++cg) {
+    const f32x4 zz = {0.f, 0.f, 0.f, 0.f};
+    f32x4 la = mfma_fp8_k128(KA, q.hi[cg], zz);
+    f32x4 lb = mfma_fp8_k128(KB, q.hi[cg], zz);
+    la = mfma_fp8_k128(KA, q.lo[cg], la);
+    lb = mfma_fp8_k128(KB, q.lo[cg], lb);
+    float lg[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lg[i] = la[i] * q.fac[cg];
+      lg[4 + i] = lb[i] * q.fac[cg];
+    }
+    if (PER_TOKEN) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) lg[j] *= ksc[j];
+    }
+    if (!interior) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int t = tok0 + j;
+        lg[j] = (t >= q.vis_lo[cg] && t < q.vis_hi[cg]) ? lg[j] : kNegInf;
+      }
+    }
+    float cmax =
+        fmaxf(fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3])), fmaxf(fmaxf(lg[4], lg[5]), fmaxf(lg[6], lg[7])));
+    cmax = max_over_groups(cmax);
+    const float mnew = fmaxf(s.m2[cg], cmax);
+    const float muse = mnew == kNegInf ? 0.0f : mnew;
+    const float alpha = __builtin_amdgcn_exp2f(s.m2[cg] - muse);
+    s.m2[cg] = mnew;
+    float pr[8];
+    float psum = 0.0f;
+    const float bias = 8.0f - muse;  // 256 * exp(l - m)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pr[j] = __builtin_amdgcn_exp2f(lg[j] + bias);
+      psum += pr[j];
+    }
+    s.lsum[cg] = s.lsum[cg] * alpha + psum;
+    if (PER_TOKEN) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pr[j] *= vsc[j] * vinv;
+    }
+    long phi, plo;
+    split8_fp8(pr, phi, plo);
+    const float f = alpha * vratio;
+    if (__ballot(f != 1.0f)) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s.acc[cg][j] *= f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      s.acc[cg][j] = mfma_fp8(V[j], phi, s.acc[cg][j]);
+      s.acc[cg][j] = mfma_fp8(V[j], plo, s.acc[cg][j]);
+    }
+  }
 }
 
 // Workgroup geometry.  A workgroup covers `slots_per_workgroup`
@@ -436,16 +658,8 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
   ic_skip_empty();
   auto ic_tb = [&]() { return ic_cbeg + (rank + ic_j * wslot) * kChunk; };
 
-  float m2[NCG], lsum[NCG];
-  f32x4 acc[NCG][8];
-#pragma unroll
-  for (int cg = 0; cg < NCG; ++cg) {
-    m2[cg] = kNegInf;
-    lsum[cg] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[cg][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  float vsmax = 0.0f;  // running max of per-token value scales (per wave, per slot)
+  WaveState<NCG> st;
+  st.reset();
   // Combination of the finished slots of this wave (MULTI only; in value
   // units: per-tensor / per-token value scales already applied).
   float mC[MULTI ? NCG : 1], lC[MULTI ? NCG : 1];
@@ -476,71 +690,10 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
   }
 
   // ---------------- query: scale, split into fp8 hi + lo ----------------
-  // B operand of the 16x16x128 QK product: lane (grp, c) holds the 32 head
-  // dims of 16-dim chunks grp and grp+4 of column c, in the byte order of
-  // the key rows read below.
-  i32x8 qhi8[NCG], qlo8[NCG];
-  float qfac[NCG];   // base-2 logit factor per column
-  int vis_lo[NCG], vis_hi[NCG];
+  QueryTile<NCG> qt;
   const float k_tensor_scale = PER_TOKEN ? 1.0f : key_scale[0];
   const float v_tensor_scale = PER_TOKEN ? 1.0f : value_scale[0];
-#pragma unroll
-  for (int cg = 0; cg < NCG; ++cg) {
-    const int e = cg * 16 + c16;
-    const bool valid = e < eq;
-    const int qi = valid ? e / gqa : 0;
-    float v[32];
-    if (a.query_dtype == PA_DTYPE_F16) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const uint32_t w = (uint32_t)qraw[cg][i >> 2][i & 3];
-        v[2 * i] = f16_bits_to_f32(w & 0xffffu);
-        v[2 * i + 1] = f16_bits_to_f32(w >> 16);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const uint32_t w = (uint32_t)qraw[cg][i >> 2][i & 3];
-        v[2 * i] = bf16_bits_to_f32(w & 0xffffu);
-        v[2 * i + 1] = bf16_bits_to_f32(w >> 16);
-      }
-    }
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    amax = max_over_groups(amax);
-    // Power-of-two scale putting amax into [128, 256): exact in fp32.
-    int sexp = 261 - (int)((__float_as_uint(amax) >> 23) & 0xffu);
-    sexp = sexp < 1 ? 1 : (sexp > 254 ? 254 : sexp);
-    const float sq = amax > 0.0f ? __uint_as_float((uint32_t)sexp << 23) : 1.0f;
-#pragma unroll
-    for (int sI = 0; sI < 4; ++sI) {
-      float xs[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) xs[i] = v[8 * sI + i] * sq;
-      long hi, lo;
-      split8_fp8(xs, hi, lo);
-      qhi8[cg][2 * sI] = (int)(uint32_t)hi;
-      qhi8[cg][2 * sI + 1] = (int)(uint32_t)((uint64_t)hi >> 32);
-      qlo8[cg][2 * sI] = (int)(uint32_t)lo;
-      qlo8[cg][2 * sI + 1] = (int)(uint32_t)((uint64_t)lo >> 32);
-    }
-    qfac[cg] = a.softmax_scale * kLog2e * k_tensor_scale / sq;
-    int lo = 0, hi = 0;
-    if (valid) pa_plan_visible(ctx, qi, ql, W, &lo, &hi);
-    vis_lo[cg] = lo;
-    vis_hi[cg] = hi;
-  }
-  // Chunks inside [lo_max, hi_min) are visible to every query column: no
-  // masking there.  lo and hi grow with qi, so the extremes come from the
-  // last and the first query.
-  int lo_max, hi_min;
-  {
-    int t0q, t1q;
-    pa_plan_visible(ctx, ql - 1, ql, W, &lo_max, &t1q);
-    pa_plan_visible(ctx, 0, ql, W, &t0q, &hi_min);
-  }
-
+  prepare_query<NCG>(qt, qraw, a.query_dtype, a.softmax_scale * kLog2e * k_tensor_scale, ctx, ql, gqa, W, c16);
   // Key row r of QK tile t (0, 1) is chunk token 8*(r/4) + 4t + r%4: that
   // token's 16-byte pieces for dim chunks grp and grp+4.
   const int krow = (c16 >> 3) * kKHalf + (8 * ((c16 >> 2) & 1) + (c16 & 3)) * 16;
@@ -551,7 +704,7 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
     int cbeg, nmine;
     slot_range(z, cbeg, nmine);
     for (int k = 0; k < nmine; ++k) {
-      const int st = gc % STAGES;
+      const int stg = gc % STAGES;
       if (ic_l < nslots) {
         issue(ic_tb(), (gc + STAGES - 1) % STAGES, np0, np1);
         ++ic_j;
@@ -565,140 +718,22 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
       }
       ++gc;
       const int tb = cbeg + (rank + k * wslot) * kChunk;
-      const LDS_AS unsigned char* sk = ring + st * kStageBytes;
-      const LDS_AS unsigned char* sv = sk + kKBytes;
-
-      const i32x4 ka0 = *(const LDS_AS i32x4*)(sk + krow + grp * 256);
-      const i32x4 ka1 = *(const LDS_AS i32x4*)(sk + krow + (grp + 4) * 256);
-      const i32x4 kb0 = *(const LDS_AS i32x4*)(sk + krow + 64 + grp * 256);
-      const i32x4 kb1 = *(const LDS_AS i32x4*)(sk + krow + 64 + (grp + 4) * 256);
-      const i32x8 KA = {ka0[0], ka0[1], ka0[2], ka0[3], ka1[0], ka1[1], ka1[2], ka1[3]};
-      const i32x8 KB = {kb0[0], kb0[1], kb0[2], kb0[3], kb1[0], kb1[1], kb1[2], kb1[3]};
-
-      // value operands: head dim 16j + c16, tokens 8*grp .. 8*grp+7
-      long V[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        V[j] = *(const LDS_AS long*)(sv + (grp >> 1) * 2048 + (16 * j + c16) * 16 + 8 * (grp & 1));
-
-      // This lane's 8 tokens: tb + 8*grp + j.
-      const int tok0 = tb + 8 * grp;
-      const bool interior = tb >= lo_max && tb + kChunk <= hi_min;
-      const bool edge = tb < lo_all || tb + kChunk > hi_all;
-      if (edge) {
-        // Zero value bytes of tokens no query sees (stale page tails).
-        uint64_t keep = 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int t = tok0 + j;
-          if (t >= lo_all && t < hi_all) keep |= (uint64_t)0xff << (8 * j);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) V[j] = (long)((uint64_t)V[j] & keep);
-      }
-
-      float ksc[8], vsc[8];
-      float vratio = 1.0f, vinv = 1.0f;
-      if (PER_TOKEN) {
-        const LDS_AS float* ss = (const LDS_AS float*)(sv + kVBytes);
-        f32x4 k0 = *(const LDS_AS f32x4*)(ss + 8 * grp);
-        f32x4 k1 = *(const LDS_AS f32x4*)(ss + 8 * grp + 4);
-        f32x4 w0 = *(const LDS_AS f32x4*)(ss + 32 + 8 * grp);
-        f32x4 w1 = *(const LDS_AS f32x4*)(ss + 32 + 8 * grp + 4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          ksc[j] = k0[j];
-          ksc[4 + j] = k1[j];
-          vsc[j] = w0[j];
-          vsc[4 + j] = w1[j];
-        }
-        if (edge) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const int t = tok0 + j;
-            if (!(t >= lo_all && t < hi_all)) vsc[j] = 0.0f;
-          }
-        }
-        float cmax = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) cmax = fmaxf(cmax, vsc[j]);
-        cmax = max_over_groups(cmax);
-        const float vnew = fmaxf(vsmax, cmax);
-        vratio = vnew > 0.0f ? vsmax / vnew : 1.0f;
-        vinv = vnew > 0.0f ? 1.0f / vnew : 0.0f;
-        vsmax = vnew;
-      }
-
-#pragma unroll
-      for (int cg = 0; cg < NCG; ++cg) {
-        const f32x4 zz = {0.f, 0.f, 0.f, 0.f};
-        f32x4 la = mfma_fp8_k128(KA, qhi8[cg], zz);
-        f32x4 lb = mfma_fp8_k128(KB, qhi8[cg], zz);
-        la = mfma_fp8_k128(KA, qlo8[cg], la);
-        lb = mfma_fp8_k128(KB, qlo8[cg], lb);
-        float lg[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          lg[i] = la[i] * qfac[cg];
-          lg[4 + i] = lb[i] * qfac[cg];
-        }
-        if (PER_TOKEN) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) lg[j] *= ksc[j];
-        }
-        if (!interior) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const int t = tok0 + j;
-            lg[j] = (t >= vis_lo[cg] && t < vis_hi[cg]) ? lg[j] : kNegInf;
-          }
-        }
-        float cmax = fmaxf(fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3])), fmaxf(fmaxf(lg[4], lg[5]), fmaxf(lg[6], lg[7])));
-        cmax = max_over_groups(cmax);
-        const float mnew = fmaxf(m2[cg], cmax);
-        const float muse = mnew == kNegInf ? 0.0f : mnew;
-        const float alpha = __builtin_amdgcn_exp2f(m2[cg] - muse);
-        m2[cg] = mnew;
-        float pr[8];
-        float psum = 0.0f;
-        const float bias = 8.0f - muse;  // 256 * exp(l - m)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          pr[j] = __builtin_amdgcn_exp2f(lg[j] + bias);
-          psum += pr[j];
-        }
-        lsum[cg] = lsum[cg] * alpha + psum;
-        if (PER_TOKEN) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) pr[j] *= vsc[j] * vinv;
-        }
-        long phi, plo;
-        split8_fp8(pr, phi, plo);
-        const float f = alpha * vratio;
-        if (__ballot(f != 1.0f)) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) acc[cg][j] *= f;
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          acc[cg][j] = mfma_fp8(V[j], phi, acc[cg][j]);
-          acc[cg][j] = mfma_fp8(V[j], plo, acc[cg][j]);
-        }
-      }
+      const LDS_AS unsigned char* sk = ring + stg * kStageBytes;
+      compute_chunk<NCG, PER_TOKEN>(st, qt, sk, krow, grp, c16, tb);
     }
     if (MULTI) {
       // Slot z is complete (this wave owns it alone): write its partial and
       // fold it into the wave's running combination.
-      const float vfin = PER_TOKEN ? vsmax : v_tensor_scale;
+      const float vfin = PER_TOKEN ? st.vsmax : v_tensor_scale;
 #pragma unroll
       for (int cg = 0; cg < NCG; ++cg) {
-        const float L = sum_over_groups(lsum[cg]);
-        const float m = m2[cg];
+        const float L = sum_over_groups(st.lsum[cg]);
+        const float m = st.m2[cg];
         const int e = cg * 16 + c16;
         if (want_partials && e < eq) {
           const float sc = L > 0.0f ? vfin / L : 0.0f;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) store_partial4(a, b, h, z, e, 16 * j + 4 * grp, acc[cg][j] * sc);
+          for (int j = 0; j < 8; ++j) store_partial4(a, b, h, z, e, 16 * j + 4 * grp, st.acc[cg][j] * sc);
           if (grp == 0) store_stats(a, b, h, z, e, L * (1.0f / 256.0f), m * kLn2);
         }
         const float Mn = fmaxf(mC[cg], m);
@@ -707,15 +742,11 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
         const float fs = __builtin_amdgcn_exp2f(m - Mu);
         const float fsv = fs * vfin;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) accC[cg][j] = accC[cg][j] * fc + acc[cg][j] * fsv;
+        for (int j = 0; j < 8; ++j) accC[cg][j] = accC[cg][j] * fc + st.acc[cg][j] * fsv;
         lC[cg] = lC[cg] * fc + L * fs;
         mC[cg] = Mn;
-        m2[cg] = kNegInf;
-        lsum[cg] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[cg][j] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-      vsmax = 0.0f;
+      st.reset();
     }
   }
 
@@ -724,7 +755,7 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
   // of waves are then combined by log-sum-exp: each group of `wslot` waves
   // into its slot's partial (unless MULTI waves already wrote them), and,
   // for a workgroup that covers every slot, all waves into the output.
-  const float vfin_end = PER_TOKEN ? vsmax : v_tensor_scale;
+  const float vfin_end = PER_TOKEN ? st.vsmax : v_tensor_scale;
   float* mbuf = (float*)smem;             // [wave][16]
   float* lbuf = mbuf + kWaves * 16;       // [wave][16]
   float* abuf = lbuf + kWaves * 16;       // [wave][head dim][16]
@@ -738,8 +769,8 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
       Lst = lC[cg];
       sc = 1.0f;
     } else {
-      Mst = m2[cg];
-      Lst = sum_over_groups(lsum[cg]);
+      Mst = st.m2[cg];
+      Lst = sum_over_groups(st.lsum[cg]);
       sc = vfin_end;
     }
     __syncthreads();
@@ -751,7 +782,7 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
     for (int j = 0; j < 8; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        abuf[(wave * kHead + 16 * j + 4 * grp + i) * 16 + c16] = (MULTI ? accC[cg][j][i] : acc[cg][j][i]) * sc;
+        abuf[(wave * kHead + 16 * j + 4 * grp + i) * 16 + c16] = (MULTI ? accC[cg][j][i] : st.acc[cg][j][i]) * sc;
     __syncthreads();
     for (int idx = tid; idx < nsets * 256; idx += kThreads) {
       const int set = idx >> 8;
@@ -784,6 +815,563 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
       }
     }
   }
+}
+
+// ============================================================================
+// Per-wave streaming decode (work list or balanced split)
+// ============================================================================
+
+// A balanced launch gives every wave at least this many chunks (it uses
+// fewer waves for small problems).
+constexpr int kMinChunksPerWave = 8;
+
+// One piece of a wave's walk: chunks [tb0, tb0 + 32 n) of (sequence b, kv
+// head h).  target < 0: the piece is the whole (sequence, kv head) and
+// goes to the output; otherwise it is a partial (balanced: partial id;
+// work list: partial row of query 0).
+struct Piece {
+  int b, h, ctx, lo_all, hi_all;
+  int tb0, n;
+  int target;
+  int orow;       // output row of query 0 of the sequence
+  int desc_cnt;   // balanced: pieces of the pair, when this piece starts it
+  int last_page;  // last page index of the sequence's page list
+  int64_t bt_off; // offset of the sequence's page list in block_tables
+};
+
+// Wave-uniform read of read-only kernel input through the constant address
+// space, so it is a scalar (SMEM) load counted on lgkmcnt: it never waits on
+// the vmcnt of the direct-to-LDS loads in flight.
+__device__ __forceinline__ int ld_uniform(const int32_t* p, int64_t i) {
+  return ((const __attribute__((address_space(4))) int32_t*)p)[i];
+}
+
+// Sequence-level fields of a piece: context, visible range, page list.
+__device__ __forceinline__ void piece_sequence(Piece& p, const pa_fp8_stream_args& a, const int32_t* kv_indptr,
+                                               const int32_t* context_lengths, int b) {
+  p.b = b;
+  p.ctx = ld_uniform(context_lengths, b);
+  int u;
+  pa_plan_visible(p.ctx, 0, a.query_length, a.sliding_window, &p.lo_all, &u);
+  pa_plan_visible(p.ctx, a.query_length - 1, a.query_length, a.sliding_window, &u, &p.hi_all);
+  int row_len;
+  if (kv_indptr) {
+    p.bt_off = ld_uniform(kv_indptr, b);
+    row_len = ld_uniform(kv_indptr, b + 1) - (int)p.bt_off;
+  } else {
+    p.bt_off = (int64_t)b * a.stride_bt_seq;
+    row_len = a.max_blocks_per_seq;
+  }
+  p.last_page = pa_min(pa_cdiv(p.ctx, a.block_size) - 1, row_len - 1);
+  if (p.last_page < 0) p.hi_all = p.lo_all;  // no pages: nothing visible
+  p.orow = b * a.query_length;
+}
+
+// Balanced split: chunks of all (sequence, kv head) pairs, sequence-major
+// with kv heads inner, cut into nw equal runs (pa_plan_run_begin).
+struct BalancedWalk {
+  int b, h, nb, c, left, first, wid, nw;
+  long long gseg, T;  // global index of chunk 0 of pair (b, h); total chunks
+  Piece seq;          // sequence-level fields of b
+
+  __device__ __forceinline__ bool next(Piece& p, const pa_fp8_stream_args& a, const int32_t* kv_indptr,
+                                       const int32_t* context_lengths) {
+    if (left <= 0) return false;
+    p = seq;
+    p.h = h;
+    p.tb0 = (seq.lo_all & ~(kChunk - 1)) + c * kChunk;
+    p.n = pa_min(nb - c, left);
+    const bool whole = c == 0 && p.n == nb;
+    p.target = whole ? -1 : 2 * wid + (first ? 0 : 1);
+    p.desc_cnt = c != 0 ? 0 : (whole ? 1 : pa_plan_run_of_chunk(gseg + nb - 1, T, nw) - wid + 1);
+    left -= p.n;
+    first = 0;
+    c += p.n;
+    if (left > 0 && c == nb) {
+      c = 0;
+      gseg += nb;
+      if (++h == a.num_kv_heads) {
+        h = 0;
+        do {
+          if (b + 1 >= a.num_seqs) {  // inconsistent context lengths: stop
+            left = 0;
+            break;
+          }
+          ++b;
+          piece_sequence(seq, a, kv_indptr, context_lengths, b);
+          nb = seq.hi_all > seq.lo_all ? pa_cdiv(seq.hi_all - (seq.lo_all & ~(kChunk - 1)), kChunk) : 0;
+        } while (nb == 0);
+      }
+    }
+    return true;
+  }
+};
+
+// Work-list walk: works [idx, end) of this wave's bin.
+struct WorklistWalk {
+  int idx, end;
+  __device__ __forceinline__ bool next(Piece& p, const pa_fp8_stream_args& a, const int32_t* kv_indptr,
+                                       const int32_t* context_lengths, const int32_t* work_info,
+                                       const int32_t* partition_indptr) {
+    if (idx >= end) return false;
+    const int64_t w = 8 * (int64_t)idx;
+    ++idx;
+    const int b = ld_uniform(work_info, w), ploc = ld_uniform(work_info, w + 1), qo0 = ld_uniform(work_info, w + 2);
+    const int kv0 = ld_uniform(work_info, w + 4), kv1 = ld_uniform(work_info, w + 5);
+    const int qh0 = ld_uniform(work_info, w + 7) & 0xffff;
+    piece_sequence(p, a, kv_indptr, context_lengths, b);
+    p.h = qh0 / a.query_group_size;
+    const int pb = ld_uniform(partition_indptr, b);
+    const int a0 = pa_max((kv0 - pb) * PA_PARTITION_TOKENS, p.lo_all);
+    const int a1 = pa_min(pa_min((kv1 - pb) * PA_PARTITION_TOKENS, p.ctx), p.hi_all);
+    if (a1 > a0) {
+      p.tb0 = a0 & ~(kChunk - 1);
+      p.n = pa_cdiv(a1 - p.tb0, kChunk);
+    } else {
+      p.tb0 = 0;
+      p.n = 0;
+    }
+    p.target = ploc < 0 ? -1 : ploc + a.query_length;
+    p.orow = qo0;
+    p.desc_cnt = 0;
+    return true;
+  }
+};
+
+// 4 consecutive head dims of an output row in the output dtype.
+__device__ __forceinline__ void store_out4(void* out, int dtype, int64_t off, f32x4 v) {
+  if (dtype == PA_DTYPE_F32) {
+    *(f32x4*)((float*)out + off) = v;
+  } else {
+    const bool bf = dtype == PA_DTYPE_BF16;
+    const uint32_t w0 = bf ? (f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16))
+                           : (f32_to_f16_bits(v[0]) | (f32_to_f16_bits(v[1]) << 16));
+    const uint32_t w1 = bf ? (f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16))
+                           : (f32_to_f16_bits(v[2]) | (f32_to_f16_bits(v[3]) << 16));
+    *(i32x2*)((uint16_t*)out + off) = i32x2{(int)w0, (int)w1};
+  }
+}
+
+// Each wave walks its pieces through a private LDS ring (2 stages of one
+// 32-token chunk each) plus two query images (the current piece's and the
+// next one's: a piece's query rows are loaded by direct-to-LDS DMA just
+// before its first chunk, so they ride the same in-order vmcnt pipeline).
+// One 16-column query block (query_length * gqa <= 16).
+template <bool PER_TOKEN, bool BS16, bool WORKLIST, int NQ>
+__global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
+    const pa_fp8_stream_args a, const int32_t* __restrict__ block_tables, const int32_t* __restrict__ kv_indptr,
+    const int32_t* __restrict__ context_lengths, const float* __restrict__ key_scale,
+    const float* __restrict__ value_scale, const int32_t* __restrict__ work_indptr,
+    const int32_t* __restrict__ work_info, const int32_t* __restrict__ partition_indptr,
+    int32_t* __restrict__ segdesc, float* __restrict__ part_out, float* __restrict__ part_lse,
+    void* __restrict__ output) {
+  // Every store goes through a restrict pointer, so the loads of the page
+  // lists, lengths and work list stay scalar (SMEM) loads inside the walk.
+  constexpr int NCG = 1;
+  constexpr int kStageBytes = kKBytes + kVBytes + (PER_TOKEN ? kScaleBytes : 0);
+  constexpr int kQBytes = NQ * 1024;  // NQ * 4 query columns x 128 dims x 2 B
+  constexpr int kWaveBytes = kStages * kStageBytes + 2 * kQBytes;
+  constexpr int kLoadsPerChunk = 8 + (PER_TOKEN ? 1 : 0);
+  static_assert(kStages == 2, "the streaming pipeline keeps one chunk in flight");
+  __shared__ __attribute__((aligned(16))) unsigned char smem[kWaves * kWaveBytes];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = lane >> 4;
+  const int c16 = lane & 15;
+  const int wid = blockIdx.x * kWaves + wave;
+  const int H = a.num_kv_heads;
+  const int ql = a.query_length;
+  const int gqa = a.query_group_size;
+  const int eq = ql * gqa;
+  const int W = a.sliding_window;
+  const int bs = a.block_size;
+  const int bs_shift = BS16 ? 4 : __builtin_ctz((unsigned)bs);
+  const int nblocks = a.num_blocks;
+
+  // ---------------- this wave's walk ----------------
+  using Walk = typename std::conditional<WORKLIST, WorklistWalk, BalancedWalk>::type;
+  Walk iwalk;
+  if constexpr (WORKLIST) {
+    if (wid >= a.num_workers) return;
+    iwalk.idx = ld_uniform(work_indptr, wid);
+    iwalk.end = ld_uniform(work_indptr, wid + 1);
+  } else {
+    // Chunks per sequence: lane l holds sequences l*K .. l*K+K-1.
+    const int B = a.num_seqs;
+    const int K = pa_cdiv(B, 64);
+    // All loads first (indices clamped into the batch), then the counts.
+    int cnt[16], rl[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int bb = pa_min(lane * K + k, B - 1);
+      cnt[k] = context_lengths[bb];
+      const int32_t* rows = kv_indptr ? kv_indptr : context_lengths;
+      const int r0 = rows[bb], r1 = rows[kv_indptr ? bb + 1 : bb];
+      rl[k] = kv_indptr ? r1 - r0 : 1;
+    }
+    int mine = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const bool real = k < K && lane * K + k < B;
+      cnt[k] = real && rl[k] > 0 ? pa_plan_seq_chunks(cnt[k], ql, W) : 0;
+      mine += cnt[k];
+    }
+    int incl = mine;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += t;
+    }
+    const int excl = incl - mine;
+    // Wave-uniform from here on (readlane), so the walk lives in SGPRs and
+    // its page lookups are scalar loads.
+    const long long T = (long long)__builtin_amdgcn_readlane(incl, 63) * H;
+    long long nwl = T / kMinChunksPerWave;
+    nwl = nwl < 1 ? 1 : nwl;
+    const int nw = nwl < a.num_workers ? (int)nwl : a.num_workers;
+    if (wid >= nw) return;
+    const long long g0 = pa_plan_run_begin(wid, T, nw);
+    const long long g1 = pa_plan_run_begin(wid + 1, T, nw);
+    if (g1 <= g0) return;
+    // The lane whose sequences hold chunk g0, then the sequence itself.
+    const uint64_t hit = __ballot(mine > 0 && (long long)excl * H <= g0 && g0 < (long long)incl * H);
+    if (hit == 0) return;  // cannot happen: the lanes' ranges tile [0, T)
+    const int ls = __builtin_amdgcn_readfirstlane((int)__builtin_ctzll(hit));
+    long long S = __builtin_amdgcn_readlane(excl, ls);
+    int b0 = -1, n0 = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int ck = __builtin_amdgcn_readlane(cnt[k], ls);
+      if (b0 < 0 && k < K) {
+        if ((S + ck) * H > g0) {
+          b0 = ls * K + k;
+          n0 = ck;
+        } else {
+          S += ck;
+        }
+      }
+    }
+    if (b0 < 0 || n0 <= 0) return;  // as above
+    const long long off = g0 - S * H;
+    iwalk.b = b0;
+    iwalk.nb = n0;
+    iwalk.h = (int)(off / n0);
+    iwalk.c = (int)(off - (long long)iwalk.h * n0);
+    iwalk.gseg = S * H + (long long)iwalk.h * n0;
+    iwalk.left = (int)(g1 - g0);
+    iwalk.first = 1;
+    iwalk.wid = wid;
+    iwalk.nw = nw;
+    iwalk.T = T;
+    piece_sequence(iwalk.seq, a, kv_indptr, context_lengths, b0);
+  }
+  Walk cwalk = iwalk;  // the compute side replays the issue side's walk
+  auto next_piece = [&](Walk& walk, Piece& p) -> bool {
+    if constexpr (WORKLIST)
+      return walk.next(p, a, kv_indptr, context_lengths, work_info, partition_indptr);
+    else
+      return walk.next(p, a, kv_indptr, context_lengths);
+  };
+
+  LDS_AS unsigned char* ring = (LDS_AS unsigned char*)smem + wave * kWaveBytes;
+  LDS_AS unsigned char* qimg = ring + kStages * kStageBytes;
+  const int koff_lane = BS16 ? lane * 16 : (lane >> 4) * (bs * 16) + (lane & 15) * 16;
+  const int voff_plain = lane * bs;
+
+  // ---------------- issue side ----------------
+  Piece ip;
+  bool iok = next_piece(iwalk, ip);
+  while (iok && ip.n == 0) iok = next_piece(iwalk, ip);
+  int ic = 0;     // next chunk of ip to issue
+  int iq = 0;     // query image the next piece's rows go to
+  int np0 = 0, np1 = 0;
+  auto fetch_pages = [&]() {
+    const int lp0 = (ip.tb0 + ic * kChunk) >> bs_shift;
+    np0 = ld_uniform(block_tables, ip.bt_off + pa_min(lp0, ip.last_page));
+    np1 = BS16 ? ld_uniform(block_tables, ip.bt_off + pa_min(lp0 + 1, ip.last_page)) : np0;
+  };
+  auto clamp_page = [&](int p) -> int {
+    p = p < 0 ? 0 : p;
+    return p < nblocks ? p : nblocks - 1;
+  };
+  if (iok) fetch_pages();
+  // Issues the next chunk (and, first in a piece, the piece's query rows)
+  // into stage st; returns whether query rows were issued.
+  auto issue_next = [&](int st) -> bool {
+    bool q = false;
+    if (ic == 0) {
+      // Query rows of columns 4i + lane/16 (clamped to a real column).
+      LDS_AS unsigned char* qd = qimg + iq * kQBytes;
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) {
+        const int e = pa_min(4 * i + (lane >> 4), eq - 1);
+        const int qi = e / gqa;
+        const int g = e - qi * gqa;
+        const unsigned char* src = (const unsigned char*)a.query +
+                                   2 * ((int64_t)(ip.orow + qi) * a.stride_q_tok +
+                                        (int64_t)(ip.h * gqa + g) * a.stride_q_head) +
+                                   (lane & 15) * 16;
+        lds_dma16(src, qd + i * 1024);
+      }
+      iq ^= 1;
+      q = true;
+    }
+    const int tb = ip.tb0 + ic * kChunk;
+    const int p0 = clamp_page(np0);
+    const int p1 = BS16 ? clamp_page(np1) : p0;
+    const uint8_t* kbase = (const uint8_t*)a.key_cache + (int64_t)ip.h * a.stride_k_head;
+    const uint8_t* vbase = (const uint8_t*)a.value_cache + (int64_t)ip.h * a.stride_v_head;
+    LDS_AS unsigned char* sk = ring + st * kStageBytes;
+    LDS_AS unsigned char* sv = sk + kKBytes;
+    if (BS16) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const uint8_t* kp = kbase + (int64_t)(hh ? p1 : p0) * a.stride_k_block;
+        const uint8_t* vp = vbase + (int64_t)(hh ? p1 : p0) * a.stride_v_block;
+#pragma unroll
+        for (int q2 = 0; q2 < 2; ++q2) lds_dma16(kp + koff_lane + q2 * 1024, sk + hh * kKHalf + q2 * 1024);
+#pragma unroll
+        for (int q2 = 0; q2 < 2; ++q2) lds_dma16(vp + lane * 16 + q2 * 1024, sv + hh * 2048 + q2 * 1024);
+      }
+    } else {
+      const int s0 = tb & (bs - 1);
+      const uint8_t* kp = kbase + (int64_t)p0 * a.stride_k_block + s0 * 16;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int q2 = 0; q2 < 2; ++q2)
+          lds_dma16(kp + hh * 256 + q2 * (4 * bs * 16) + koff_lane, sk + hh * kKHalf + q2 * 1024);
+      if (a.trans_v) {
+        const uint8_t* vp = vbase + (int64_t)p0 * a.stride_v_block + (s0 >> 4) * (kHead * 16);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int q2 = 0; q2 < 2; ++q2)
+            lds_dma16(vp + hh * 2048 + q2 * 1024 + lane * 16, sv + hh * 2048 + q2 * 1024);
+      } else {
+        const uint8_t* vp = vbase + (int64_t)p0 * a.stride_v_block + s0;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int q2 = 0; q2 < 2; ++q2)
+            lds_dma16(vp + hh * 16 + q2 * (64 * bs) + voff_plain, sv + hh * 2048 + q2 * 1024);
+      }
+    }
+    if (PER_TOKEN) {
+      LDS_AS unsigned char* ss = sv + kVBytes;
+      if (lane < 16) {
+        const int tt = (lane & 7) * 4;
+        const int pg2 = BS16 ? (tt >= 16 ? p1 : p0) : p0;
+        const int sidx = BS16 ? (tt & 15) : (tb & (bs - 1)) + tt;
+        const float* base = (lane < 8 ? key_scale : value_scale) + (int64_t)ip.h * a.stride_ks_head;
+        lds_dma16(base + (int64_t)pg2 * a.stride_ks_block + sidx, ss);
+      }
+    }
+    if (++ic == ip.n) {
+      ic = 0;
+      do {
+        iok = next_piece(iwalk, ip);
+      } while (iok && ip.n == 0);
+    }
+    if (iok) fetch_pages();
+    return q;
+  };
+
+  // ---------------- compute side ----------------
+  const float k_tensor_scale = PER_TOKEN ? 1.0f : key_scale[0];
+  const float v_tensor_scale = PER_TOKEN ? 1.0f : value_scale[0];
+  const float logit_scale = a.softmax_scale * kLog2e * k_tensor_scale;
+  const int krow = (c16 >> 3) * kKHalf + (8 * ((c16 >> 2) & 1) + (c16 & 3)) * 16;
+  WaveState<NCG> st;
+  st.reset();
+  QueryTile<NCG> qt;
+  int cq = 0;  // query image of the next piece to compute
+  int gc = 0;  // chunks computed (stage = gc % 2)
+  if (iok) issue_next(0);
+  Piece cp;
+  while (next_piece(cwalk, cp)) {
+    for (int k = 0; k < cp.n; ++k) {
+      const int stg = gc & 1;
+      if (iok) {
+        // In order: [chunk gc] ... [query rows?] [chunk gc + 1]; wait for
+        // everything up to chunk gc.
+        if (issue_next(stg ^ 1))
+          __builtin_amdgcn_s_waitcnt(vmcnt_only(kLoadsPerChunk + NQ));
+        else
+          __builtin_amdgcn_s_waitcnt(vmcnt_only(kLoadsPerChunk));
+      } else {
+        __builtin_amdgcn_s_waitcnt(0);
+      }
+      ++gc;
+      if (k == 0) {
+        // The piece's query rows arrived before its first chunk.
+        const LDS_AS unsigned char* qs = qimg + cq * kQBytes + c16 * 256;
+        cq ^= 1;
+        i32x4 qraw[1][4];
+        if (c16 < eq) {
+          qraw[0][0] = *(const LDS_AS i32x4*)(qs + 32 * grp);
+          qraw[0][1] = *(const LDS_AS i32x4*)(qs + 32 * grp + 16);
+          qraw[0][2] = *(const LDS_AS i32x4*)(qs + 32 * (grp + 4));
+          qraw[0][3] = *(const LDS_AS i32x4*)(qs + 32 * (grp + 4) + 16);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) qraw[0][i] = i32x4{0, 0, 0, 0};
+        }
+        prepare_query<NCG>(qt, qraw, a.query_dtype, logit_scale, cp.ctx, ql, gqa, W, c16);
+      }
+      compute_chunk<NCG, PER_TOKEN>(st, qt, ring + stg * kStageBytes, krow, grp, c16, cp.tb0 + k * kChunk);
+    }
+    // ---- the piece is complete: output row or partial ----
+    const float vfin = PER_TOKEN ? st.vsmax : v_tensor_scale;
+    const float L = sum_over_groups(st.lsum[0]);
+    const float m = st.m2[0];
+    const int e = c16;
+    if (e < eq) {
+      const int qi = e / gqa;
+      const int g = e - qi * gqa;
+      const int qh = cp.h * gqa + g;
+      const float sc = L > 0.0f ? vfin / L : 0.0f;
+      if (cp.target < 0) {
+        const int64_t off = (int64_t)(cp.orow + qi) * a.stride_out_tok + (int64_t)qh * a.stride_out_head + 4 * grp;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) store_out4(output, a.output_dtype, off + 16 * j, st.acc[0][j] * sc);
+      } else {
+        int64_t po, pl;
+        if (WORKLIST) {
+          po = (int64_t)(cp.target + qi) * a.stride_po_row + (int64_t)qh * kHead;
+          pl = (int64_t)(cp.target + qi) * a.stride_pl_row + qh;
+        } else {
+          pl = (int64_t)cp.target * eq + e;
+          po = pl * kHead;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) *(f32x4*)(part_out + po + 16 * j + 4 * grp) = st.acc[0][j] * sc;
+        if (grp == 0) part_lse[pl] = L > 0.0f ? kLn2 * (m + __builtin_amdgcn_logf(L) - 8.0f) : kNegInf;
+      }
+    }
+    if (!WORKLIST && cp.desc_cnt > 0 && lane == 0)
+      *(i32x2*)(segdesc + 2 * ((int64_t)cp.b * H + cp.h)) = i32x2{cp.target, cp.desc_cnt};
+    st.reset();
+  }
+}
+
+// Log-sum-exp merge of n partial rows into 2 head dims per lane:
+// lse_at(i) and row_at(i) (element offset of the row) address item i.  All
+// loads of a batch of up to kBatch rows are issued before any is used.
+template <int kBatch, typename LseAt, typename RowAt>
+__device__ __forceinline__ void merge_rows(int n, const float* lse, const float* rows, LseAt lse_at, RowAt row_at,
+                                           int lane, float& o0, float& o1) {
+  float M = kNegInf, tot = 0.0f;
+  o0 = 0.0f;
+  o1 = 0.0f;
+  for (int p0 = 0; p0 < n; p0 += kBatch) {
+    const int nb = n - p0 < kBatch ? n - p0 : kBatch;
+    const float l = lane < nb ? lse[lse_at(p0 + lane)] : kNegInf;
+    f32x2 x[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int q = i < nb ? i : nb - 1;
+      x[i] = *(const f32x2*)(rows + row_at(p0 + q) + 2 * lane);
+    }
+    float mb = l;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mb = fmaxf(mb, shfl_xor(mb, o));
+    const float Mn = fmaxf(M, mb);
+    if (Mn == kNegInf) continue;
+    const float w = l == kNegInf ? 0.0f : __expf(l - Mn);
+    float ws = w;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ws += shfl_xor(ws, o);
+    const float fold = M == kNegInf ? 0.0f : __expf(M - Mn);
+    tot = tot * fold + ws;
+    o0 *= fold;
+    o1 *= fold;
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const float wi = __shfl(w, i, 64);
+      if (i < nb) {
+        o0 += wi * x[i][0];
+        o1 += wi * x[i][1];
+      }
+    }
+    M = Mn;
+  }
+  const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
+  o0 *= inv;
+  o1 *= inv;
+}
+
+__device__ __forceinline__ void store_out2(void* out, int dtype, int64_t off, float o0, float o1) {
+  if (dtype == PA_DTYPE_F32) {
+    *(f32x2*)((float*)out + off) = f32x2{o0, o1};
+  } else if (dtype == PA_DTYPE_F16) {
+    *(uint32_t*)((uint16_t*)out + off) = f32_to_f16_bits(o0) | (f32_to_f16_bits(o1) << 16);
+  } else {
+    *(uint32_t*)((uint16_t*)out + off) = f32_to_bf16_bits(o0) | (f32_to_bf16_bits(o1) << 16);
+  }
+}
+
+// Merge of a balanced launch: one wave per (sequence, kv head, column).
+// Pairs held whole by one wave were written by the decode; pairs with no
+// visible key get zeros; split pairs merge their pieces: the first piece
+// is partial id segdesc[0], the others are the first pieces (id 2w) of the
+// following waves.
+__global__ __launch_bounds__(256) void pa_fp8_segment_merge_kernel(const pa_fp8_stream_args a,
+                                                                   const int32_t* segdesc, const float* part_out,
+                                                                   const float* part_lse) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int ql = a.query_length, gqa = a.query_group_size, eq = ql * gqa;
+  const int64_t rows = (int64_t)a.num_seqs * a.num_kv_heads * eq;
+  if (row >= rows) return;
+  const int e = (int)(row % eq);
+  const int h = (int)((row / eq) % a.num_kv_heads);
+  const int b = (int)(row / ((int64_t)eq * a.num_kv_heads));
+  // The pair's descriptor is read together with its length (it is only
+  // meaningful, and only used, when the pair has visible keys).
+  const int ctx = a.context_lengths[b];
+  const i32x2 d = *(const i32x2*)(segdesc + 2 * ((int64_t)b * a.num_kv_heads + h));
+  int rl = 1;
+  if (a.kv_indptr) rl = a.kv_indptr[b + 1] - a.kv_indptr[b];
+  const int nb = rl > 0 ? pa_plan_seq_chunks(ctx, ql, a.sliding_window) : 0;
+  float o0 = 0.0f, o1 = 0.0f;
+  if (nb > 0) {
+    const int pid0 = d[0], cnt = d[1];
+    if (cnt <= 1) return;  // written by the decode
+    const int w0 = pid0 >> 1;
+    auto pid = [&](int i) -> int64_t { return i == 0 ? pid0 : 2 * (int64_t)(w0 + i); };
+    merge_rows<8>(
+        cnt, part_lse, part_out, [&](int i) { return pid(i) * eq + e; },
+        [&](int i) { return (pid(i) * eq + e) * kHead; }, lane, o0, o1);
+  }
+  const int qi = e / gqa, g = e - qi * gqa;
+  const int64_t off = (int64_t)(b * ql + qi) * a.stride_out_tok + (int64_t)(h * gqa + g) * a.stride_out_head + 2 * lane;
+  store_out2(a.output, a.output_dtype, off, o0, o1);
+}
+
+// Merge of work-list partials: one wave per (group, query, query head).
+__global__ __launch_bounds__(256) void pa_fp8_worklist_reduce_kernel(const pa_fp8_worklist_reduce_args a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int Hq = a.num_query_heads, mq = a.max_query_length;
+  if (row >= (int64_t)a.num_groups * mq * Hq) return;
+  const int qh = (int)(row % Hq);
+  const int qi = (int)((row / Hq) % mq);
+  const int g = (int)(row / ((int64_t)Hq * mq));
+  const int p0 = a.reduce_indptr[g], p1 = a.reduce_indptr[g + 1];
+  if (p1 <= p0) return;
+  const int qo0 = a.reduce_final_map[2 * g], qo1 = a.reduce_final_map[2 * g + 1];
+  if (qi >= qo1 - qo0) return;
+  const int32_t* pmap = a.reduce_partial_map + p0;
+  float o0, o1;
+  merge_rows<8>(
+      p1 - p0, a.partial_lse, a.partial_output,
+      [&](int i) { return (int64_t)(pmap[i] + qi) * a.stride_pl_row + qh; },
+      [&](int i) { return (int64_t)(pmap[i] + qi) * a.stride_po_row + (int64_t)qh * kHead; }, lane, o0, o1);
+  store_out2(a.output, a.output_dtype, (int64_t)(qo0 + qi) * a.stride_out_tok + (int64_t)qh * a.stride_out_head + 2 * lane,
+             o0, o1);
 }
 
 // One wave per (sequence, kv head, column); lane l covers head dims 2l,
@@ -887,6 +1475,87 @@ hipError_t dispatch_ncg(const pa_fp8_partition_args& a, unsigned grid, hipStream
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Query DMA instructions per piece of a streaming launch (4 columns each).
+int stream_nq(int eq) { return eq <= 4 ? 1 : (eq <= 8 ? 2 : 4); }
+
+int stream_lds_bytes(int nq, bool per_token) {
+  const int stage = kKBytes + kVBytes + (per_token ? kScaleBytes : 0);
+  return kWaves * (kStages * stage + 2 * nq * 1024);
+}
+
+template <bool PT, bool BS16, bool WL, int NQ>
+hipError_t launch_stream(const pa_fp8_stream_args& a, unsigned grid, hipStream_t s, int32_t* desc, float* po,
+                         float* pl) {
+  hipLaunchKernelGGL((pa_fp8_stream_kernel<PT, BS16, WL, NQ>), dim3(grid), dim3(kThreads), 0, s, a, a.block_tables,
+                     a.kv_indptr, a.context_lengths, a.key_scale, a.value_scale, a.work_indptr, a.work_info,
+                     a.partition_indptr, desc, po, pl, a.output);
+  return hipGetLastError();
+}
+
+template <bool WL, int NQ>
+hipError_t dispatch_stream_nq(const pa_fp8_stream_args& a, unsigned grid, hipStream_t s, int32_t* desc, float* po,
+                              float* pl) {
+  const bool pt = a.per_token_kv != 0;
+  const bool bs16 = a.block_size == 16;
+  if (pt)
+    return bs16 ? launch_stream<true, true, WL, NQ>(a, grid, s, desc, po, pl)
+                : launch_stream<true, false, WL, NQ>(a, grid, s, desc, po, pl);
+  return bs16 ? launch_stream<false, true, WL, NQ>(a, grid, s, desc, po, pl)
+              : launch_stream<false, false, WL, NQ>(a, grid, s, desc, po, pl);
+}
+
+template <bool WL>
+hipError_t dispatch_stream(const pa_fp8_stream_args& a, unsigned grid, hipStream_t s, int32_t* desc, float* po,
+                           float* pl) {
+  switch (stream_nq(a.query_length * a.query_group_size)) {
+    case 1: return dispatch_stream_nq<WL, 1>(a, grid, s, desc, po, pl);
+    case 2: return dispatch_stream_nq<WL, 2>(a, grid, s, desc, po, pl);
+    default: return dispatch_stream_nq<WL, 4>(a, grid, s, desc, po, pl);
+  }
+}
+
+// Checks shared by both streaming entry points.
+int check_stream_args(const pa_fp8_stream_args* a) {
+  if (!a) return PA_ERR_NULL_ARG;
+  if (a->abi_version != PA_FP8_ABI_VERSION) return PA_ERR_ABI;
+  if (!a->output || !a->query || !a->key_cache || !a->value_cache || !a->block_tables || !a->context_lengths ||
+      !a->key_scale || !a->value_scale)
+    return PA_ERR_NULL_ARG;
+  if (a->head_size != kHead) return PA_ERR_HEAD_SIZE;
+  const int bs = a->block_size;
+  if (!(bs == 16 || (bs >= 32 && bs <= 1024 && (bs & (bs - 1)) == 0))) return PA_ERR_BLOCK_SIZE;
+  if (a->num_seqs < 0 || a->num_kv_heads <= 0 || a->query_length <= 0 || a->query_group_size <= 0 ||
+      a->num_blocks <= 0 || a->max_blocks_per_seq <= 0 || a->sliding_window < 0 || a->num_workers <= 0)
+    return PA_ERR_SHAPE;
+  if (a->query_length * a->query_group_size > 16) return PA_ERR_GROUP;
+  if (a->query_dtype != PA_DTYPE_BF16 && a->query_dtype != PA_DTYPE_F16) return PA_ERR_DTYPE;
+  if (a->output_dtype != PA_DTYPE_BF16 && a->output_dtype != PA_DTYPE_F16 && a->output_dtype != PA_DTYPE_F32)
+    return PA_ERR_DTYPE;
+  if (!aligned16(a->query) || (a->stride_q_tok % 8) || (a->stride_q_head % 8)) return PA_ERR_ALIGN;
+  if (!aligned16(a->key_cache) || !aligned16(a->value_cache) || (a->stride_k_block % 16) ||
+      (a->stride_k_head % 16) || (a->stride_v_block % 16) || (a->stride_v_head % 16))
+    return PA_ERR_ALIGN;
+  if (a->per_token_kv &&
+      (!aligned16(a->key_scale) || !aligned16(a->value_scale) || (a->stride_ks_block % 4) || (a->stride_ks_head % 4)))
+    return PA_ERR_ALIGN;
+  if (!aligned16(a->output) || (a->stride_out_tok % 4) || (a->stride_out_head % 4)) return PA_ERR_ALIGN;
+  return PA_OK;
+}
+
+// Balanced workspace: pair descriptors, then partial lse, then partial rows.
+struct BalancedLayout {
+  int64_t desc, lse, out, total;
+};
+BalancedLayout balanced_layout(int B, int H, int eq, int nw) {
+  auto up = [](int64_t x) { return (x + 255) & ~(int64_t)255; };
+  BalancedLayout l;
+  l.desc = 0;
+  l.lse = up((int64_t)B * H * 2 * 4);
+  l.out = l.lse + up((int64_t)2 * nw * eq * 4);
+  l.total = l.out + (int64_t)2 * nw * eq * kHead * 4;
+  return l;
+}
+
 }  // namespace
 
 extern "C" {
@@ -976,6 +1645,116 @@ int pa_fp8_decode_reduce(const pa_fp8_reduce_args* a, void* stream) {
   hipLaunchKernelGGL(pa_fp8_lse_reduce_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, *a);
   hipError_t err = hipGetLastError();
   return err == hipSuccess ? PA_OK : (int)err;
+}
+
+int pa_fp8_stream_workers(int num_cu, int query_length, int query_group_size, int per_token_kv) {
+  if (num_cu <= 0 || query_length <= 0 || query_group_size <= 0) return PA_ERR_SHAPE;
+  const int eq = query_length * query_group_size;
+  if (eq > 16) return PA_ERR_GROUP;
+  const int lds = stream_lds_bytes(stream_nq(eq), per_token_kv != 0);
+  const int per_cu = 160 * 1024 / lds >= 2 ? 2 : 1;
+  return num_cu * per_cu * kWaves;
+}
+
+int64_t pa_fp8_balanced_workspace_bytes(int num_seqs, int num_kv_heads, int query_length, int query_group_size,
+                                        int num_workers) {
+  if (num_seqs < 0 || num_kv_heads <= 0 || query_length <= 0 || query_group_size <= 0 || num_workers <= 0)
+    return PA_ERR_SHAPE;
+  return balanced_layout(num_seqs, num_kv_heads, query_length * query_group_size, num_workers).total;
+}
+
+int pa_fp8_decode_balanced(const pa_fp8_stream_args* a, void* workspace, int64_t workspace_bytes, void* stream) {
+  int rc = check_stream_args(a);
+  if (rc != PA_OK) return rc;
+  if (a->num_seqs > 1024) return PA_ERR_SHAPE;
+  if (!workspace) return PA_ERR_NULL_ARG;
+  if (((uintptr_t)workspace & 255u) != 0) return PA_ERR_ALIGN;
+  const int eq = a->query_length * a->query_group_size;
+  const BalancedLayout l = balanced_layout(a->num_seqs, a->num_kv_heads, eq, a->num_workers);
+  if (workspace_bytes < l.total) return PA_ERR_SHAPE;
+  if (a->num_seqs == 0) return PA_OK;
+  unsigned char* ws = (unsigned char*)workspace;
+  int32_t* desc = (int32_t*)(ws + l.desc);
+  float* pl = (float*)(ws + l.lse);
+  float* po = (float*)(ws + l.out);
+  hipError_t err =
+      dispatch_stream<false>(*a, (unsigned)pa_cdiv(a->num_workers, kWaves), (hipStream_t)stream, desc, po, pl);
+  return err == hipSuccess ? PA_OK : (int)err;
+}
+
+int pa_fp8_merge_balanced(const pa_fp8_stream_args* a, const void* workspace, int64_t workspace_bytes,
+                          void* stream) {
+  int rc = check_stream_args(a);
+  if (rc != PA_OK) return rc;
+  if (a->num_seqs > 1024) return PA_ERR_SHAPE;
+  if (!workspace) return PA_ERR_NULL_ARG;
+  if (((uintptr_t)workspace & 255u) != 0) return PA_ERR_ALIGN;
+  const int eq = a->query_length * a->query_group_size;
+  const BalancedLayout l = balanced_layout(a->num_seqs, a->num_kv_heads, eq, a->num_workers);
+  if (workspace_bytes < l.total) return PA_ERR_SHAPE;
+  const int64_t rows = (int64_t)a->num_seqs * a->num_kv_heads * eq;
+  if (rows == 0) return PA_OK;
+  const unsigned char* ws = (const unsigned char*)workspace;
+  hipLaunchKernelGGL(pa_fp8_segment_merge_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                     (hipStream_t)stream, *a, (const int32_t*)(ws + l.desc), (const float*)(ws + l.out),
+                     (const float*)(ws + l.lse));
+  hipError_t err = hipGetLastError();
+  return err == hipSuccess ? PA_OK : (int)err;
+}
+
+int pa_fp8_decode_worklist(const pa_fp8_stream_args* a, void* stream) {
+  int rc = check_stream_args(a);
+  if (rc != PA_OK) return rc;
+  if (!a->work_indptr || !a->work_info || !a->partition_indptr || !a->partial_output || !a->partial_lse)
+    return PA_ERR_NULL_ARG;
+  if (!aligned16(a->partial_output) || (a->stride_po_row % 4)) return PA_ERR_ALIGN;
+  if (a->num_seqs == 0) return PA_OK;
+  hipError_t err = dispatch_stream<true>(*a, (unsigned)pa_cdiv(a->num_workers, kWaves), (hipStream_t)stream, nullptr,
+                                         a->partial_output, a->partial_lse);
+  return err == hipSuccess ? PA_OK : (int)err;
+}
+
+int pa_fp8_reduce_worklist(const pa_fp8_worklist_reduce_args* a, void* stream) {
+  if (!a) return PA_ERR_NULL_ARG;
+  if (a->abi_version != PA_FP8_ABI_VERSION) return PA_ERR_ABI;
+  if (!a->output || !a->partial_output || !a->partial_lse || !a->reduce_indptr || !a->reduce_final_map ||
+      !a->reduce_partial_map)
+    return PA_ERR_NULL_ARG;
+  if (a->head_size != kHead) return PA_ERR_HEAD_SIZE;
+  if (a->num_groups < 0 || a->num_query_heads <= 0 || a->max_query_length <= 0) return PA_ERR_SHAPE;
+  if (a->output_dtype != PA_DTYPE_BF16 && a->output_dtype != PA_DTYPE_F16 && a->output_dtype != PA_DTYPE_F32)
+    return PA_ERR_DTYPE;
+  if (((uintptr_t)a->partial_output & 7u) || (a->stride_po_row % 2) || ((uintptr_t)a->output & 7u) ||
+      (a->stride_out_tok % 2) || (a->stride_out_head % 2))
+    return PA_ERR_ALIGN;
+  const int64_t rows = (int64_t)a->num_groups * a->max_query_length * a->num_query_heads;
+  if (rows == 0) return PA_OK;
+  if ((rows + 3) / 4 > 0x7fffffffLL) return PA_ERR_SHAPE;
+  hipLaunchKernelGGL(pa_fp8_worklist_reduce_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                     (hipStream_t)stream, *a);
+  hipError_t err = hipGetLastError();
+  return err == hipSuccess ? PA_OK : (int)err;
+}
+
+int pa_fp8_worklist_sizes(int num_seqs, int num_kv_heads, int num_cu, int* max_works, int* max_split_tiles) {
+  if (!max_works || !max_split_tiles) return PA_ERR_NULL_ARG;
+  if (num_seqs < 0 || num_kv_heads <= 0 || num_cu <= 0) return PA_ERR_SHAPE;
+  pa_worklist_sizes(num_seqs, num_kv_heads, num_cu, max_works, max_split_tiles);
+  return PA_OK;
+}
+
+int pa_fp8_plan_worklist(const int32_t* context_lengths, int num_seqs, int num_kv_heads, int query_group_size,
+                         int query_length, int num_cu, int kv_granularity, int32_t* work_indptr, int32_t* work_info,
+                         int32_t* reduce_indptr, int32_t* reduce_final_map, int32_t* reduce_partial_map) {
+  if (!work_indptr || !work_info || !reduce_indptr || !reduce_final_map || !reduce_partial_map) return PA_ERR_NULL_ARG;
+  if (num_seqs > 0 && !context_lengths) return PA_ERR_NULL_ARG;
+  if (num_seqs < 0 || num_kv_heads <= 0 || query_group_size <= 0 || query_length <= 0 || num_cu <= 0 ||
+      (num_cu % num_kv_heads) != 0 || kv_granularity <= 0 || (kv_granularity & (kv_granularity - 1)) != 0)
+    return PA_ERR_SHAPE;
+  const int n = pa_worklist_plan(context_lengths, num_seqs, num_kv_heads, query_group_size, query_length, num_cu,
+                                 kv_granularity, work_indptr, work_info, reduce_indptr, reduce_final_map,
+                                 reduce_partial_map);
+  return n < 0 ? PA_ERR_SHAPE : n;
 }
 
 int pa_fp8_recommended_splits(int num_seqs, int num_kv_heads, int split_kv_blocks, int sliding_window,

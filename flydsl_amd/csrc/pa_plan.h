@@ -71,3 +71,22 @@ PA_HD void pa_plan_visible(int ctx, int qi, int query_length, int sliding_window
   *lo = pa_max(l, 0);
   *hi = pa_max(h, 0);
 }
+
+// 32-token chunks a sequence attends, counted from its first visible token
+// rounded down to a multiple of 32 (the union of every query's keys).
+#define PA_CHUNK_TOKENS 32
+PA_HD int pa_plan_seq_chunks(int ctx, int query_length, int sliding_window) {
+  int lo, hi, unused;
+  pa_plan_visible(ctx, 0, query_length, sliding_window, &lo, &unused);
+  pa_plan_visible(ctx, query_length - 1, query_length, sliding_window, &unused, &hi);
+  if (hi <= lo) return 0;
+  return pa_cdiv(hi - (lo & ~(PA_CHUNK_TOKENS - 1)), PA_CHUNK_TOKENS);
+}
+
+// Balanced split: the T chunks of all (sequence, kv head) segments, laid
+// end to end, are cut into nw runs; run w is [floor(w T / nw),
+// floor((w + 1) T / nw)).  Returns the run holding chunk g (0 <= g < T).
+PA_HD int pa_plan_run_of_chunk(long long g, long long T, int nw) {
+  return (int)(((g + 1) * nw + T - 1) / T) - 1;
+}
+PA_HD long long pa_plan_run_begin(int w, long long T, int nw) { return (long long)w * T / nw; }

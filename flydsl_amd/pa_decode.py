@@ -6,11 +6,14 @@ Drop-in for the reference's Python API in kernels/pa_decode_fp8.py:
 defaults, tensor layouts, validation errors and route strings; the device
 work is done by the HIP kernels of ``libpa_fp8.so`` through its C ABI.
 
-Scheduling (see ``_schedule``): when the batch has enough (sequence, kv
-head) pairs and bounded contexts, one workgroup per pair walks all of its
-slots and merges them itself (one launch); otherwise workgroups take one or
-a few slots each and the reduce kernel merges them (two launches).  Either
-way the slot partials the reference defines are written whenever the caller
+Scheduling (see ``_schedule`` and ``_balanced_ok``): when the batch has
+enough (sequence, kv head) pairs and bounded contexts, one workgroup per
+pair walks all of its slots and merges them itself (one launch).  When the
+caller does not ask for the slot partials and the contexts may be long or
+ragged, every wave of the GPU takes an equal run of the batch's chunks
+(balanced stream split, a decode launch plus a merge launch).  Otherwise
+workgroups take one or a few slots each and the reduce kernel merges them.
+The slot partials the reference defines are written whenever the caller
 passes the buffers for them.
 
 Routes (same dispatch order as the reference, :2883 / :3010 / :3123):
@@ -23,9 +26,12 @@ Routes (same dispatch order as the reference, :2883 / :3010 / :3123):
                                  kernels/pa_decode_swa.py:1228).
   * page size 16 or 64        -> split-context partition pass + LSE reduce
                                  ("ps_small_block").
-  * other page sizes (1024)   -> the same partition pass over the flat
-                                 ``kv_page_indices``/``kv_indptr`` page list
-                                 + LSE reduce ("ps_split_reduce").
+  * other page sizes (1024)   -> flat ``kv_page_indices``/``kv_indptr``
+                                 page list ("ps_split_reduce"): with the
+                                 ``metadata`` of :func:`get_pa_metadata`, the
+                                 work-list decode + its reduce, as the
+                                 reference's persistent route; without it,
+                                 the balanced split or the partition pass.
 """
 
 from __future__ import annotations
@@ -216,27 +222,67 @@ def _schedule(route: str, batch: int, kv_heads: int, P: int, eqgs: int, capacity
     return 1
 
 
+# Balanced stream split: at most this many query columns per kv head (the
+# per-wave query images then leave room for two workgroups per CU) and this
+# many sequences (the in-kernel split scans them in one pass).
+BALANCED_MAX_COLUMNS = 4
+BALANCED_MAX_SEQS = 1024
+# Work-list decode: one 16-column query block.
+STREAM_MAX_COLUMNS = 16
+
+
+def _balanced_ok(route: str, batch: int, eqgs: int, user_partials: bool, owner: bool) -> bool:
+    """Balanced stream split for a call whose slot partials nobody reads and
+    that the owner schedule does not take: every wave gets an equal run of
+    the batch's chunks, so one long sequence no longer sets the duration."""
+    return (route in ("small", "flat") and not user_partials and not owner and eqgs <= BALANCED_MAX_COLUMNS
+            and 0 < batch <= BALANCED_MAX_SEQS)
+
+
 class PreparedDecode:
     """A validated decode call whose C-ABI arguments are already marshalled.
 
     ``launch()`` issues exactly the device work ``pa_decode_ps_launch`` would
-    (one partition launch with the in-kernel merge, or partition + reduce)
-    without re-validating or rebuilding arguments; the tensors captured at
-    preparation must stay alive and unchanged in shape.
+    (partition pass [+ reduce], balanced decode + merge, or work-list decode
+    + reduce) without re-validating or rebuilding arguments; the tensors
+    captured at preparation must stay alive and unchanged in shape.
     """
 
-    def __init__(self, route: str, partition_args, reduce_args, stream, keepalive):
+    def __init__(self, route: str, stream, keepalive, *, partition_args=None, reduce_args=None, stream_args=None,
+                 worklist_reduce_args=None, workspace=None):
         self.route = route
         self._pa = partition_args
         self._ra = reduce_args
+        self._sa = stream_args
+        self._wra = worklist_reduce_args
+        self._ws = workspace
         self._stream = ctypes.c_void_p(stream.cuda_stream)
         self._keep = keepalive
         self._lib = _lib.load()
+        self._kernels = self.kernels()
+
+    def kernels(self):
+        """The call's kernel launches in order, as (C entry point, thunk);
+        the first is the decode kernel, a second one its merge.  The thunks
+        hold the marshalled structs, not this object (no reference cycle:
+        a call's buffers are released as soon as the call is dropped)."""
+        lib, s = self._lib, self._stream
+        pa, ra, sa, wra = self._pa, self._ra, self._sa, self._wra
+        if pa is not None:
+            out = [("pa_fp8_decode_partition", lambda: lib.pa_fp8_decode_partition(ctypes.byref(pa), s))]
+            if ra is not None:
+                out.append(("pa_fp8_decode_reduce", lambda: lib.pa_fp8_decode_reduce(ctypes.byref(ra), s)))
+            return out
+        if wra is not None:
+            return [("pa_fp8_decode_worklist", lambda: lib.pa_fp8_decode_worklist(ctypes.byref(sa), s)),
+                    ("pa_fp8_reduce_worklist", lambda: lib.pa_fp8_reduce_worklist(ctypes.byref(wra), s))]
+        ws, n = self._ws.data_ptr(), self._ws.numel()
+        return [("pa_fp8_decode_balanced", lambda: lib.pa_fp8_decode_balanced(ctypes.byref(sa), ws, n, s)),
+                ("pa_fp8_merge_balanced", lambda: lib.pa_fp8_merge_balanced(ctypes.byref(sa), ws, n, s))]
 
     def launch(self) -> str:
-        _lib.check(self._lib.pa_fp8_decode_partition(ctypes.byref(self._pa), self._stream), "pa_fp8_decode_partition")
-        if self._ra is not None:
-            _lib.check(self._lib.pa_fp8_decode_reduce(ctypes.byref(self._ra), self._stream), "pa_fp8_decode_reduce")
+        for name, fn in self._kernels:
+            _lib.check(fn(), name)
         return self.route
 
 
@@ -405,11 +451,10 @@ def prepare_pa_decode(
         if max_context_partition_num == 0:
             max_context_partition_num = get_recommended_splits(batch_size, num_kv_heads, split_kv_blocks=1)
         kv_ind = kv_indptr
-        if metadata is not None and exp_sums is None and "exp_sums" in metadata:
-            exp_sums = metadata["exp_sums"]
-            max_logits = metadata["max_logits"]
-            temporary_output = metadata["temporary_output"]
-            max_context_partition_num = int(exp_sums.shape[2])
+        if metadata is not None and eqgs <= STREAM_MAX_COLUMNS:
+            return _prepare_worklist(
+                metadata, output, query, key_cache, value_cache, context_lengths, kv_page_indices, kv_indptr,
+                softmax_scale, key_scale, value_scale, per_token_kv, trans_v, query_input_dtype, output_dtype, s)
     if route != "flat":
         _check_int32("block_tables", block_tables, dev)
         if block_tables.dim() != 2 or block_tables.stride(-1) != 1:
@@ -420,6 +465,18 @@ def prepare_pa_decode(
     spw = _schedule(route, batch_size, num_kv_heads, P, eqgs, capacity, _cu_count(dev) if P > 1 else 1)
     owner = spw >= P
     user_partials = exp_sums is not None or max_logits is not None or temporary_output is not None
+    if _balanced_ok(route, batch_size, eqgs, user_partials, owner):
+        route_name = "ps_small_block" if route == "small" else "ps_split_reduce"
+        sa = _stream_args(output, query, key_cache, value_cache, context_lengths,
+                          kv_page_indices if route == "flat" else block_tables, kv_ind, softmax_scale, key_scale,
+                          value_scale, per_token_kv, trans_v, query_input_dtype, output_dtype, sliding_window)
+        sa.num_workers = _lib.stream_workers(_cu_count(dev), query_length, query_group_size, per_token_kv)
+        nbytes = _lib.balanced_workspace_bytes(batch_size, num_kv_heads, query_length, query_group_size,
+                                               sa.num_workers)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        keep = (output, query, key_cache, value_cache, context_lengths, block_tables, kv_page_indices, kv_indptr,
+                key_scale, value_scale, ws)
+        return PreparedDecode(route_name, s, keep, stream_args=sa, workspace=ws)
     fused = owner and not user_partials
     if fused and route != "sw":
         # Nobody observes the slot partials: let each of the workgroup's
@@ -500,7 +557,7 @@ def prepare_pa_decode(
     if route == "sw" and P <= 1:
         route_name = "ps_sw_fused_partitioned"
     if owner:
-        return PreparedDecode(route_name, pa, None, s, keep)
+        return PreparedDecode(route_name, s, keep, partition_args=pa)
 
     ra = _lib.ReduceArgs()
     ra.abi_version = _lib.ABI_VERSION
@@ -522,7 +579,101 @@ def prepare_pa_decode(
     ra.head_size = head_size
     ra.output_dtype = output_dtype
     ra.tmp_dtype = _tmp_dtype_code(temporary_output)
-    return PreparedDecode(route_name, pa, ra, s, keep)
+    return PreparedDecode(route_name, s, keep, partition_args=pa, reduce_args=ra)
+
+
+def _stream_args(output, query, key_cache, value_cache, context_lengths, pages, kv_indptr, softmax_scale, key_scale,
+                 value_scale, per_token_kv, trans_v, query_input_dtype, output_dtype, sliding_window=0):
+    """C-ABI arguments shared by the balanced and work-list decodes.
+    ``pages`` is the [B, max_blocks] block table, or the flat page list
+    when ``kv_indptr`` is given."""
+    sa = _lib.StreamArgs()
+    sa.abi_version = _lib.ABI_VERSION
+    sa.output = output.data_ptr()
+    sa.query = query.data_ptr()
+    sa.key_cache = key_cache.data_ptr()
+    sa.value_cache = value_cache.data_ptr()
+    sa.block_tables = pages.data_ptr()
+    sa.context_lengths = context_lengths.data_ptr()
+    sa.key_scale = key_scale.data_ptr()
+    sa.value_scale = value_scale.data_ptr()
+    if kv_indptr is not None:
+        sa.kv_indptr = kv_indptr.data_ptr()
+        sa.max_blocks_per_seq = max(1, int(pages.numel()))
+    else:
+        sa.stride_bt_seq = pages.stride(0)
+        sa.max_blocks_per_seq = int(pages.shape[1])
+    sa.stride_q_tok, sa.stride_q_head = query.stride(0), query.stride(1)
+    sa.stride_k_block, sa.stride_k_head = key_cache.stride(0), key_cache.stride(1)
+    sa.stride_v_block, sa.stride_v_head = value_cache.stride(0), value_cache.stride(1)
+    if per_token_kv:
+        sa.stride_ks_block, sa.stride_ks_head = key_scale.stride(0), key_scale.stride(1)
+    sa.stride_out_tok, sa.stride_out_head = output.stride(0), output.stride(1)
+    b = int(context_lengths.shape[0])
+    sa.num_seqs = b
+    sa.num_kv_heads = int(key_cache.shape[1])
+    sa.query_length = query.shape[0] // b
+    sa.query_group_size = query.shape[1] // int(key_cache.shape[1])
+    sa.head_size = int(query.shape[-1])
+    sa.block_size = int(key_cache.shape[-2])
+    sa.num_blocks = int(key_cache.shape[0])
+    sa.sliding_window = int(sliding_window)
+    sa.per_token_kv = int(per_token_kv)
+    sa.trans_v = int(trans_v)
+    sa.query_dtype = DTYPE_BF16 if query_input_dtype == "bf16" else DTYPE_F16
+    sa.output_dtype = output_dtype
+    sa.softmax_scale = float(softmax_scale)
+    return sa
+
+
+_METADATA_KEYS = ("work_indptr", "work_info_flat", "partition_indptr", "reduce_indptr", "reduce_final_map",
+                  "reduce_partial_map", "num_sm", "partial_output", "partial_lse")
+
+
+def _prepare_worklist(md, output, query, key_cache, value_cache, context_lengths, kv_page_indices, kv_indptr,
+                      softmax_scale, key_scale, value_scale, per_token_kv, trans_v, query_input_dtype, output_dtype,
+                      s):
+    """Persistent route with precomputed metadata (kernels/pa_decode_fp8.py:
+    3123-3202): work-list decode, then the reduce of split works."""
+    missing = [k for k in _METADATA_KEYS if k not in md]
+    if missing:
+        raise ValueError(f"metadata is missing {missing}; build it with get_pa_metadata()")
+    if int(md.get("partition_size", KV_COMPUTE_BLOCK)) != KV_COMPUTE_BLOCK:
+        raise ValueError(f"metadata must use partition_size={KV_COMPUTE_BLOCK}")
+    b = int(context_lengths.shape[0])
+    ql = query.shape[0] // b
+    if int(md.get("query_length", ql)) != ql or int(md["partition_indptr"].shape[0]) != b + 1:
+        raise ValueError("metadata was built for a different batch or query length")
+    sa = _stream_args(output, query, key_cache, value_cache, context_lengths, kv_page_indices, kv_indptr,
+                      softmax_scale, key_scale, value_scale, per_token_kv, trans_v, query_input_dtype, output_dtype)
+    po, pl = md["partial_output"], md["partial_lse"]
+    sa.work_indptr = md["work_indptr"].data_ptr()
+    sa.work_info = md["work_info_flat"].data_ptr()
+    sa.partition_indptr = md["partition_indptr"].data_ptr()
+    sa.partial_output = po.data_ptr()
+    sa.partial_lse = pl.data_ptr()
+    sa.stride_po_row = int(md.get("stride_po_ql", po.stride(0)))
+    sa.stride_pl_row = int(md.get("stride_pl_ql", pl.stride(0)))
+    sa.num_workers = int(md["num_sm"])
+    wr = _lib.WorklistReduceArgs()
+    wr.abi_version = _lib.ABI_VERSION
+    wr.output = output.data_ptr()
+    # the reduce reads partial rows from row query_length on (:3189-3200)
+    wr.partial_output = po.data_ptr() + ql * sa.stride_po_row * po.element_size()
+    wr.partial_lse = pl.data_ptr() + ql * sa.stride_pl_row * pl.element_size()
+    wr.reduce_indptr = md["reduce_indptr"].data_ptr()
+    wr.reduce_final_map = md["reduce_final_map"].data_ptr()
+    wr.reduce_partial_map = md["reduce_partial_map"].data_ptr()
+    wr.stride_out_tok, wr.stride_out_head = output.stride(0), output.stride(1)
+    wr.stride_po_row, wr.stride_pl_row = sa.stride_po_row, sa.stride_pl_row
+    wr.num_groups = b
+    wr.num_query_heads = int(query.shape[1])
+    wr.head_size = int(query.shape[-1])
+    wr.max_query_length = ql
+    wr.output_dtype = output_dtype
+    keep = (output, query, key_cache, value_cache, context_lengths, kv_page_indices, kv_indptr, key_scale,
+            value_scale, md)
+    return PreparedDecode("ps_split_reduce", s, keep, stream_args=sa, worklist_reduce_args=wr)
 
 
 def get_pa_metadata(
@@ -534,29 +685,59 @@ def get_pa_metadata(
     num_kv_heads: int,
     partition_size: int = KV_COMPUTE_BLOCK,
 ):
-    """Preallocate the partial buffers of the flat-page-list route.
+    """Work list of the persistent route (kernels/pa_decode_fp8.py:1729-1859).
 
-    Returns a dict that ``pa_decode_ps_launch(metadata=...)`` consumes, so the
-    call is graph-capturable.  Keys ``partition_indptr``, ``num_sm`` and
-    ``query_length`` follow kernels/pa_decode_fp8.py:1844-1859;
-    ``exp_sums``/``max_logits``/``temporary_output`` are the slot partials
-    this build's partition pass writes.
+    The scheduler of kernels/pa_metadata.py:145-420 runs on the host
+    (``pa_fp8_plan_worklist``; the context lengths are copied to the host,
+    the synchronisation the reference makes with ``.item()``).  Bins are the
+    waves the work-list decode keeps resident (``num_sm``), rounded down to a
+    multiple of ``num_kv_heads``.  Returns the reference's keys: work list,
+    reduce maps, ``partition_indptr`` and the float32 partial buffers
+    ``partial_output`` [(n + 1) * ql, 1, Hq, D] / ``partial_lse``
+    [(n + 1) * ql, 1, Hq, 1] with their strides; plus ``partition_size``.
     """
     dev = query.device
     batch_size = int(context_lengths.shape[0])
     query_length = query.shape[0] // max(batch_size, 1)
     head_size = int(query.shape[-1])
-    eqgs = query_length * (num_query_heads // num_kv_heads)
-    P = get_recommended_splits(batch_size, num_kv_heads, split_kv_blocks=1)
-    parts = (context_lengths.to(torch.int32) + (partition_size - 1)) // partition_size
-    partition_indptr = torch.zeros(batch_size + 1, dtype=torch.int32, device=dev)
+    gqa = num_query_heads // num_kv_heads
+    eqgs = query_length * gqa
+    num_cu = _cu_count(dev)
+    if eqgs <= STREAM_MAX_COLUMNS:
+        workers = _lib.stream_workers(num_cu, query_length, gqa, True)
+    else:
+        workers = num_cu * 3
+    num_sm = max(num_kv_heads, (workers // num_kv_heads) * num_kv_heads)
+    ctx_host = context_lengths.detach().to("cpu", torch.int32)
+    n_works, plan = _lib.plan_worklist(ctx_host.numpy(), num_kv_heads, gqa, query_length, num_sm, partition_size)
+    parts = (ctx_host + (partition_size - 1)) // partition_size
+    partition_indptr = torch.zeros(batch_size + 1, dtype=torch.int32)
     partition_indptr[1:] = torch.cumsum(parts, dim=0).to(torch.int32)
-    shape = (batch_size, num_kv_heads, P, eqgs)
+    up = lambda a: torch.from_numpy(a).to(dev)
+    # partial rows: every split work's partial_qo_loc + query rows (the
+    # reduce count of the last kv head, as the reference sizes it, unless a
+    # work of another head reaches further)
+    works = plan["work_info"][: max(n_works, 0)]
+    max_loc = int(works[:, 1].max()) if n_works > 0 else -1
+    num_partials = max(int(plan["reduce_indptr"][-1]), max_loc // query_length + 1 if max_loc >= 0 else 0)
+    partial_output = torch.empty(((num_partials + 1) * query_length, 1, num_query_heads, head_size),
+                                 dtype=torch.float32, device=dev)
+    partial_lse = torch.empty(((num_partials + 1) * query_length, 1, num_query_heads, 1), dtype=torch.float32,
+                              device=dev)
     return {
-        "partition_indptr": partition_indptr,
-        "num_sm": _cu_count(dev),
+        "work_indptr": up(plan["work_indptr"]),
+        "work_info_flat": up(plan["work_info"].reshape(-1)),
+        "partition_indptr": partition_indptr.to(dev),
+        "reduce_indptr": up(plan["reduce_indptr"]),
+        "reduce_final_map": up(plan["reduce_final_map"]),
+        "reduce_partial_map": up(plan["reduce_partial_map"]),
+        "num_sm": num_sm,
+        "partial_output": partial_output,
+        "partial_lse": partial_lse,
+        "stride_po_partial": query_length * num_query_heads * head_size,
+        "stride_pl_partial": query_length * num_query_heads,
+        "stride_po_ql": num_query_heads * head_size,
+        "stride_pl_ql": num_query_heads,
         "query_length": query_length,
-        "exp_sums": torch.empty(shape, device=dev, dtype=torch.float32),
-        "max_logits": torch.empty(shape, device=dev, dtype=torch.float32),
-        "temporary_output": torch.empty(shape + (head_size,), device=dev, dtype=torch.bfloat16),
+        "partition_size": partition_size,
     }

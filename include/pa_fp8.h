@@ -164,6 +164,116 @@ typedef struct pa_fp8_reduce_args {
 int pa_fp8_decode_reduce(const pa_fp8_reduce_args* args, void* hip_stream);
 
 /*
+ * Per-wave streaming decode.  Every wave of the launch walks a list of
+ * pieces -- (sequence, kv head, run of 32-token chunks) -- back to back
+ * through one LDS pipeline, and writes each piece either straight into
+ * `output` (the piece is the whole (sequence, kv head)) or as a float32
+ * partial (normalised output row plus its log-sum-exp) for a merge pass.
+ * query_length * query_group_size <= 16.
+ *
+ * pa_fp8_decode_worklist: pieces come from the work list of
+ * pa_fp8_plan_worklist (one bin per wave: num_workers = bins).  Replaces
+ * compile_pa_decode_metadata(...)["launch"] (kernels/pa_decode_fp8.py:
+ * 1030-1721, launched at :3144-3184): a work with partial_qo_loc < 0 writes
+ * output rows qo_start + qi; otherwise partial rows ploc + query_length + qi
+ * of partial_output [rows, Hq, D] / partial_lse [rows, Hq], lse = max
+ * logit + ln(sum), natural-log units.  Merge with pa_fp8_reduce_worklist.
+ *
+ * pa_fp8_decode_balanced: no work list; the kernel cuts the chunks of all
+ * (sequence, kv head) pairs into num_workers equal runs itself (stream-K),
+ * so ragged batches load every wave equally without a host round trip.
+ * Pairs a single wave holds whole go straight to `output`; then
+ * pa_fp8_merge_balanced, on the same stream and with the same arguments
+ * and workspace, merges the pieces of the pairs that were cut (and writes
+ * zeros for pairs with no visible key).  The workspace
+ * (pa_fp8_balanced_workspace_bytes bytes, 256-byte aligned) holds the
+ * pieces' partials; it needs no initialisation.  num_seqs <= 1024.  No
+ * reference counterpart: it serves the small-block and flat-page routes of
+ * pa_decode_ps_launch when the caller does not ask for the slot partials.
+ */
+typedef struct pa_fp8_stream_args {
+  int32_t abi_version;
+  void* output; /* [B * ql, Hq, D] */
+  const void* query;
+  const void* key_cache;
+  const void* value_cache;
+  const int32_t* block_tables; /* [B, max_blocks], or the flat page list when kv_indptr != NULL */
+  const int32_t* kv_indptr;    /* optional [B + 1] offsets into the flat page list */
+  const int32_t* context_lengths;
+  const float* key_scale;
+  const float* value_scale;
+  /* work list (pa_fp8_decode_worklist only) */
+  const int32_t* work_indptr;      /* [num_workers + 1] */
+  const int32_t* work_info;        /* [works, 8] */
+  const int32_t* partition_indptr; /* [B + 1] cumulative 256-token partitions */
+  float* partial_output;           /* [rows, Hq, D] float32 */
+  float* partial_lse;              /* [rows, Hq] float32 */
+  /* element strides */
+  int64_t stride_q_tok, stride_q_head;
+  int64_t stride_k_block, stride_k_head;
+  int64_t stride_v_block, stride_v_head;
+  int64_t stride_bt_seq;
+  int64_t stride_ks_block, stride_ks_head;
+  int64_t stride_out_tok, stride_out_head;
+  int64_t stride_po_row, stride_pl_row; /* work list partial rows */
+  /* sizes */
+  int32_t num_seqs;
+  int32_t num_kv_heads;
+  int32_t query_length;
+  int32_t query_group_size;
+  int32_t head_size;
+  int32_t block_size;
+  int32_t num_blocks;
+  int32_t max_blocks_per_seq;
+  int32_t sliding_window;
+  int32_t per_token_kv;
+  int32_t trans_v;
+  int32_t query_dtype;
+  int32_t output_dtype;
+  int32_t num_workers; /* waves of the launch (4 per workgroup) */
+  float softmax_scale;
+} pa_fp8_stream_args;
+
+int pa_fp8_decode_worklist(const pa_fp8_stream_args* args, void* hip_stream);
+int pa_fp8_decode_balanced(const pa_fp8_stream_args* args, void* workspace, int64_t workspace_bytes,
+                           void* hip_stream);
+int pa_fp8_merge_balanced(const pa_fp8_stream_args* args, const void* workspace, int64_t workspace_bytes,
+                          void* hip_stream);
+int64_t pa_fp8_balanced_workspace_bytes(int num_seqs, int num_kv_heads, int query_length, int query_group_size,
+                                        int num_workers);
+/* Waves a streaming launch keeps resident on num_cu CUs (4 per workgroup;
+ * two workgroups per CU when their LDS fits, else one). */
+int pa_fp8_stream_workers(int num_cu, int query_length, int query_group_size, int per_token_kv);
+
+/*
+ * Log-sum-exp merge of work-list partials.  Replaces aiter's pa_reduce_v1
+ * as called at kernels/pa_decode_fp8.py:3189-3200: partial_output and
+ * partial_lse point at row query_length of the buffers the decode wrote
+ * (the reference passes partial_output[query_length:]).  Group g merges the
+ * partial rows reduce_partial_map[reduce_indptr[g] .. reduce_indptr[g+1]) + qi
+ * into output rows reduce_final_map[g][0] + qi, for qi <
+ * reduce_final_map[g][1] - reduce_final_map[g][0] and every query head.
+ */
+typedef struct pa_fp8_worklist_reduce_args {
+  int32_t abi_version;
+  void* output;
+  const float* partial_output;
+  const float* partial_lse;
+  const int32_t* reduce_indptr;      /* [num_groups + 1] */
+  const int32_t* reduce_final_map;   /* [num_groups, 2] */
+  const int32_t* reduce_partial_map;
+  int64_t stride_out_tok, stride_out_head;
+  int64_t stride_po_row, stride_pl_row;
+  int32_t num_groups; /* entries of reduce_indptr minus one (the batch size) */
+  int32_t num_query_heads;
+  int32_t head_size;
+  int32_t max_query_length;
+  int32_t output_dtype;
+} pa_fp8_worklist_reduce_args;
+
+int pa_fp8_reduce_worklist(const pa_fp8_worklist_reduce_args* args, void* hip_stream);
+
+/*
  * Host-only planning helpers (no GPU needed).
  *
  * pa_fp8_recommended_splits replaces get_recommended_splits
@@ -178,6 +288,22 @@ int pa_fp8_recommended_splits(int num_seqs, int num_kv_heads, int split_kv_block
 int pa_fp8_plan_slot(int context_length, int num_partitions, int slot, int sliding_window, int query_length,
                      int* t0, int* t1);
 int pa_fp8_plan_visible(int context_length, int qi, int query_length, int sliding_window, int* lo, int* hi);
+
+/*
+ * Work list of the persistent route, on the host (host pointers in and
+ * out).  Replaces get_pa_metadata_v1 (kernels/pa_metadata.py:450-524, the
+ * scheduler kernel :145-420) and get_pa_metadata_info_v1 (:53-79) for
+ * causal decode with uniform query length: the ceil(ctx / kv_granularity)
+ * partitions of each sequence are dealt, per kv head, to num_cu /
+ * num_kv_heads bins.  Buffers: work_indptr [num_cu + 1], work_info
+ * [max_works * 8], reduce_indptr [num_seqs + 1], reduce_final_map
+ * [num_seqs * 2], reduce_partial_map [max_split_tiles]; unused entries are
+ * zeroed.  Returns the number of works (>= 0) or a PA_ERR_* code.
+ */
+int pa_fp8_worklist_sizes(int num_seqs, int num_kv_heads, int num_cu, int* max_works, int* max_split_tiles);
+int pa_fp8_plan_worklist(const int32_t* context_lengths, int num_seqs, int num_kv_heads, int query_group_size,
+                         int query_length, int num_cu, int kv_granularity, int32_t* work_indptr, int32_t* work_info,
+                         int32_t* reduce_indptr, int32_t* reduce_final_map, int32_t* reduce_partial_map);
 
 /* Library identification and error names. */
 const char* pa_fp8_version(void);

@@ -324,6 +324,53 @@ def slot_partials(
     return es, ml, to
 
 
+def range_partial(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_table_row,
+    ctx: int,
+    key_scale_flat: Optional[torch.Tensor],
+    value_scale_flat: Optional[torch.Tensor],
+    b: int,
+    h: int,
+    t0: int,
+    t1: int,
+    softmax_scale: float,
+    *,
+    query_length: int = 1,
+    sliding_window: int = 0,
+    dtype: torch.dtype = torch.float64,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Attention of sequence b's queries of kv head h over keys [t0, t1)
+    only (each query further limited to the keys it may see): the normalised
+    output [ql, gqa, D] and its log-sum-exp [ql, gqa] (natural log; -inf and
+    a zero row when no key is visible) -- what one work of the persistent
+    route stores (kernels/pa_decode_fp8.py:1600-1643)."""
+    vc = value_cache if value_cache.dim() == 4 else unshuffle_value_cache_layout(value_cache)
+    hkv, d = vc.shape[1], vc.shape[2]
+    gqa = query.shape[1] // hkv
+    k, v = gather_tokens(key_cache, vc, list(block_table_row), ctx, key_scale_flat, value_scale_flat)
+    k, v = k.to(dtype), v.to(dtype)
+    q = query[b * query_length : (b + 1) * query_length].to(dtype)
+    out = torch.zeros(query_length, gqa, d, dtype=dtype)
+    lse = torch.full((query_length, gqa), float("-inf"), dtype=dtype)
+    for qi in range(query_length):
+        lo, hi = plan.visible_token_range(ctx, qi, query_length, sliding_window)
+        a, e_ = max(t0, lo), min(t1, hi)
+        if e_ <= a:
+            continue
+        kk, vv = k[a:e_, h], v[a:e_, h]
+        for g in range(gqa):
+            l = (kk @ q[qi, h * gqa + g]) * softmax_scale
+            m = l.max()
+            p = torch.exp(l - m)
+            s = p.sum()
+            out[qi, g] = (p[:, None] * vv).sum(0) / s
+            lse[qi, g] = m + torch.log(s)
+    return out, lse
+
+
 def lse_merge(exp_sums: torch.Tensor, max_logits: torch.Tensor, tmp_out: torch.Tensor) -> torch.Tensor:
     """Merge P slot partials: out = sum_p w_p tmp_p with
     w_p = s_p e^{m_p - M} / sum_q s_q e^{m_q - M}, M = max_p m_p.

@@ -47,9 +47,29 @@ def test_null_args_rejected_without_gpu():
     a = _lib.PartitionArgs()
     a.abi_version = 99
     assert lib.pa_fp8_decode_partition(ctypes.byref(a), None) == -8
+    assert lib.pa_fp8_decode_worklist(None, None) == -1
+    assert lib.pa_fp8_decode_balanced(None, None, 0, None) == -1
+    assert lib.pa_fp8_reduce_worklist(None, None) == -1
+    sa = _lib.StreamArgs()
+    sa.abi_version = 99
+    assert lib.pa_fp8_decode_balanced(ctypes.byref(sa), None, 0, None) == -8
 
 
-@pytest.mark.parametrize("struct,cname", [(_lib.PartitionArgs, "pa_fp8_partition_args"), (_lib.ReduceArgs, "pa_fp8_reduce_args")])
+def test_stream_worker_counts():
+    # one query image per wave fits two workgroups per CU; larger ones one
+    assert _lib.stream_workers(256, 1, 4, True) == 2048
+    assert _lib.stream_workers(256, 1, 8, False) == 1024
+    assert _lib.stream_workers(256, 4, 4, True) == 1024
+    with pytest.raises(RuntimeError):
+        _lib.stream_workers(256, 4, 8, True)  # 32 columns: not a streaming shape
+    ws = _lib.balanced_workspace_bytes(128, 8, 1, 4, 2048)
+    assert ws >= 128 * 8 * 8 + 2 * 2048 * 4 * 4 + 2 * 2048 * 4 * 128 * 4
+
+
+@pytest.mark.parametrize("struct,cname", [(_lib.PartitionArgs, "pa_fp8_partition_args"),
+                                          (_lib.ReduceArgs, "pa_fp8_reduce_args"),
+                                          (_lib.StreamArgs, "pa_fp8_stream_args"),
+                                          (_lib.WorklistReduceArgs, "pa_fp8_worklist_reduce_args")])
 def test_struct_layout_matches_header(tmp_path, struct, cname):
     fields = [f for f, _ in struct._fields_]
     src = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){",

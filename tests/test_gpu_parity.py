@@ -48,14 +48,16 @@ SCHEDULES = {
 
 @contextlib.contextmanager
 def schedule(name):
-    """Force the launcher's slots-per-workgroup choice."""
-    saved = pd._schedule
+    """Force the launcher's slots-per-workgroup choice (and, for a forced
+    choice, keep the partition pass: no balanced stream split)."""
+    saved = pd._schedule, pd._balanced_ok
     if SCHEDULES[name] is not None:
         pd._schedule = SCHEDULES[name]
+        pd._balanced_ok = lambda *args: False
     try:
         yield
     finally:
-        pd._schedule = saved
+        pd._schedule, pd._balanced_ok = saved
 
 
 def launch(case, *, P=0, out_dtype=torch.bfloat16, tmp_dtype=torch.bfloat16, flat=False, partials=False,

@@ -1,0 +1,276 @@
+"""GPU parity of the per-wave streaming decodes (balanced split and work
+list) against the CPU oracle, at the same tolerance as the partition pass
+(bf16 outputs within atol 2e-2 / rtol 2e-2, every element).
+
+Each case runs with the GPU's real CU count (thousands of short runs, most
+pairs cut across waves) and with a tiny one (a few long runs, each crossing
+many (sequence, kv head) pairs), so both the cut-and-merge and the
+walk-across-pairs paths are exercised.  Work-list partials are checked row
+by row against the oracle's attention over each work's partition range.
+"""
+
+from __future__ import annotations
+
+import contextlib
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import flydsl_amd.pa_decode as pd
+from flydsl_amd import pa_decode_ps_launch, prepare_pa_decode, workloads
+from oracle import torch_ref
+from tests._cases import flat_scales, make_case, torch_oracle
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-2
+RTOL = 2e-2
+DEV = "cuda:0"
+
+
+def to_dev(case):
+    return {k: (v.to(DEV) if isinstance(v, torch.Tensor) else v) for k, v in case.items()}
+
+
+def to_cpu(case):
+    return {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in case.items()}
+
+
+@contextlib.contextmanager
+def balanced(num_cu=None):
+    """Force the balanced split (when the shape allows it) and optionally
+    pretend the GPU has `num_cu` CUs (fewer, longer runs)."""
+    saved = pd._balanced_ok, pd._cu_count
+    pd._balanced_ok = lambda route, batch, eqgs, user_partials, owner: (
+        route in ("small", "flat") and not user_partials and eqgs <= pd.BALANCED_MAX_COLUMNS)
+    if num_cu is not None:
+        pd._cu_count = lambda device=None: num_cu
+    try:
+        yield
+    finally:
+        pd._balanced_ok, pd._cu_count = saved
+
+
+@contextlib.contextmanager
+def cu_count(num_cu):
+    saved = pd._cu_count
+    if num_cu is not None:
+        pd._cu_count = lambda device=None: num_cu
+    try:
+        yield
+    finally:
+        pd._cu_count = saved
+
+
+def flat_pages(case):
+    bt = case["block_tables"].cpu()
+    ctx = case["context_lengths"].cpu().tolist()
+    bs = case["key_cache"].shape[-2]
+    rows = [bt[b, : math.ceil(c / bs)] for b, c in enumerate(ctx)]
+    pages = torch.cat(rows).to(torch.int32)
+    indptr = torch.tensor([0] + np.cumsum([len(r) for r in rows]).tolist(), dtype=torch.int32)
+    return pages.to(DEV), indptr.to(DEV)
+
+
+def run(case, *, flat=False, out_dtype=torch.bfloat16, metadata=None, pages=None):
+    q = case["query"]
+    out = torch.full(q.shape, float("nan"), dtype=out_dtype, device=DEV)
+    page_idx = indptr = None
+    if flat:
+        page_idx, indptr = pages if pages is not None else flat_pages(case)
+    route = pa_decode_ps_launch(out, q, case["key_cache"], case["value_cache"], case["context_lengths"], page_idx,
+                                indptr, case["softmax_scale"], case["key_scale"], case["value_scale"],
+                                sliding_window=case["sliding_window"], block_tables=None if flat else case["block_tables"],
+                                metadata=metadata)
+    torch.cuda.synchronize()
+    return out, route
+
+
+def assert_parity(out, ref, what):
+    out, ref = out.float().cpu(), ref.float().cpu()
+    bad = ~torch.isclose(out, ref, atol=ATOL, rtol=RTOL)
+    err = (out - ref).abs().max().item()
+    print(f"[parity] {what} max_abs_err={err:.3e} bad={int(bad.sum())}/{out.numel()}", flush=True)
+    assert not torch.isnan(out).any(), what
+    assert int(bad.sum()) == 0, f"{what}: {int(bad.sum())} outside tolerance; max err {err}"
+
+
+BALANCED_CASES = {
+    "c1_tiny": dict(config="c1_tiny"),
+    "ragged_pt": dict(batch=12, per_token=True, ctx=[1, 5, 33, 260, 700, 1500, 3000, 7000, 9000, 40, 2, 12000]),
+    "ctx_edges": dict(batch=12, ctx=[1, 2, 15, 16, 17, 31, 32, 33, 255, 256, 257, 1023]),
+    "mtp_ql4_gqa1": dict(batch=6, query_length=4, num_query_heads=4, num_kv_heads=4, ctx_range=(4, 3000)),
+    "mtp_ql2_gqa2_pt": dict(batch=6, query_length=2, num_query_heads=4, num_kv_heads=2, per_token=True,
+                            ctx_range=(2, 4000)),
+    "gqa1": dict(batch=5, num_query_heads=8, num_kv_heads=8, ctx_range=(1, 2500)),
+    "page64_ragged": dict(batch=7, block_size=64, ctx=[1, 64, 65, 900, 4000, 130, 2049], per_token=True),
+    "uniform_data": dict(batch=6, dist="uniform", ctx_range=(1, 3000)),
+}
+
+
+def build(spec):
+    spec = dict(spec)
+    if "config" in spec:
+        return workloads.build_inputs(workloads.CONFIGS[spec["config"]], device="cpu", seed=123)
+    return make_case(seed=sum(map(ord, str(sorted(spec.items())))) % 1000, **spec)
+
+
+@pytest.mark.parametrize("num_cu", [None, 2])
+@pytest.mark.parametrize("name", sorted(BALANCED_CASES))
+def test_balanced_matches_oracle(name, num_cu):
+    case = build(BALANCED_CASES[name])
+    print(f"[balanced] {name} cu={num_cu} ctx={case['context_lengths'].tolist()[:12]}", flush=True)
+    ref = torch_oracle(case, float_out=False)
+    with balanced(num_cu):
+        out, route = run(to_dev(case))
+    assert route == "ps_small_block"
+    assert_parity(out, ref, f"balanced {name} cu={num_cu}")
+
+
+@pytest.mark.parametrize("num_cu", [None, 3])
+def test_balanced_flat_pages_and_dtypes(num_cu):
+    case = make_case(batch=5, block_size=1024, ctx=[1, 1025, 5000, 3000, 7], per_token=True, seed=131)
+    ref = torch_oracle(case, float_out=True)
+    d = to_dev(case)
+    with balanced(num_cu):
+        out, route = run(d, flat=True, out_dtype=torch.float32)
+        assert route == "ps_split_reduce"
+        assert_parity(out, ref, f"balanced flat f32 cu={num_cu}")
+        d["query"] = d["query"].to(torch.float16)
+        out16, _ = run(d, flat=True, out_dtype=torch.float16)
+    assert_parity(out16, ref, f"balanced flat f16 cu={num_cu}")
+
+
+def test_balanced_plain_value_layout():
+    case = make_case(batch=6, block_size=64, ctx_range=(1, 3000), seed=137)
+    ref = torch_oracle(case, float_out=False)
+    d = to_dev(case)
+    d["value_cache"] = torch_ref.unshuffle_value_cache_layout(case["value_cache"].view(torch.uint8)).view(
+        torch.float8_e4m3fn).to(DEV)
+    with balanced(5):
+        out, _ = run(d)
+    assert_parity(out, ref, "balanced plain V")
+
+
+def test_balanced_graph_capture_replays():
+    case = to_dev(make_case(batch=7, ctx_range=(1, 6000), per_token=True, seed=139))
+    out = torch.empty(case["query"].shape, dtype=torch.bfloat16, device=DEV)
+    s = torch.cuda.Stream()
+    with balanced():
+        call = prepare_pa_decode(out, case["query"], case["key_cache"], case["value_cache"], case["context_lengths"],
+                                 None, None, case["softmax_scale"], case["key_scale"], case["value_scale"],
+                                 block_tables=case["block_tables"], stream=s)
+    assert call._sa is not None and call._pa is None
+    with torch.cuda.stream(s):
+        call.launch()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            call.launch()
+    torch.cuda.synchronize()
+    for i in range(4):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        with torch.cuda.stream(s):
+            call.launch()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"eager after replay {i}"
+
+
+WORKLIST_CASES = {
+    "gqa4": dict(batch=6, ctx=[1, 300, 1025, 4096, 7000, 2500]),
+    "gqa8_pt": dict(batch=5, num_query_heads=16, num_kv_heads=2, per_token=True, ctx_range=(1, 6000)),
+    "ql2_gqa8": dict(batch=4, query_length=2, num_query_heads=16, num_kv_heads=2, ctx_range=(2, 5000)),
+    "ql4_gqa4_pt": dict(batch=4, query_length=4, num_query_heads=8, num_kv_heads=2, per_token=True,
+                        ctx_range=(4, 5000)),
+    "gqa16": dict(batch=3, num_query_heads=16, num_kv_heads=1, ctx_range=(1, 9000)),
+}
+
+
+@pytest.mark.parametrize("num_cu", [None, 2])
+@pytest.mark.parametrize("name", sorted(WORKLIST_CASES))
+def test_worklist_route_matches_oracle(name, num_cu):
+    """Reference persistent route: get_pa_metadata, then the work-list
+    decode writes direct rows and float32 partials + LSE; the reduce merges
+    them.  Partials of split works are checked against the oracle."""
+    spec = dict(WORKLIST_CASES[name])
+    case = make_case(block_size=1024, seed=len(name) * 7 + 3, **spec)
+    print(f"[worklist] {name} cu={num_cu} ctx={case['context_lengths'].tolist()}", flush=True)
+    ref = torch_oracle(case, float_out=False)
+    d = to_dev(case)
+    pages = flat_pages(case)
+    hq, hkv = case["query"].shape[1], case["key_cache"].shape[1]
+    ql = case["query_length"]
+    with cu_count(num_cu):
+        md = pd.get_pa_metadata(d["query"], d["key_cache"], d["context_lengths"], pages[1], hq, hkv)
+        md["partial_output"].fill_(float("nan"))
+        out, route = run(d, flat=True, metadata=md, pages=pages)
+    assert route == "ps_split_reduce"
+    assert_parity(out, ref, f"worklist {name} cu={num_cu}")
+    # partial rows of split works vs the oracle over the work's range
+    info = md["work_info_flat"].view(-1, 8).cpu()
+    n = int(md["work_indptr"][-1])
+    pbase = md["partition_indptr"].cpu().tolist()
+    ks, vs = flat_scales(case)
+    po = md["partial_output"].cpu()
+    pl = md["partial_lse"].cpu()
+    checked = 0
+    gqa = hq // hkv
+    for w in range(n):
+        b, ploc, _, _, kv0, kv1, _, qhr = info[w].tolist()
+        if ploc < 0 or checked >= 6:
+            continue
+        kh = (qhr & 0xFFFF) // gqa
+        o, l = torch_ref.range_partial(case["query"], case["key_cache"], case["value_cache"],
+                                       case["block_tables"][b].tolist(), int(case["context_lengths"][b]), ks, vs, b,
+                                       kh, (kv0 - pbase[b]) * 256, (kv1 - pbase[b]) * 256, case["softmax_scale"],
+                                       query_length=ql)
+        for qi in range(ql):
+            row = ploc + ql + qi
+            for g in range(gqa):
+                qh = kh * gqa + g
+                if math.isinf(float(l[qi, g])):
+                    assert float(pl[row, 0, qh, 0]) == float("-inf")
+                    continue
+                torch.testing.assert_close(float(pl[row, 0, qh, 0]), float(l[qi, g]), atol=1e-2, rtol=0)
+                torch.testing.assert_close(po[row, 0, qh].double(), o[qi, g], atol=ATOL, rtol=RTOL)
+        checked += 1
+
+
+def test_worklist_graph_capture_replays():
+    case = make_case(batch=5, block_size=1024, num_query_heads=16, num_kv_heads=2, ctx_range=(1, 6000), seed=151)
+    d = to_dev(case)
+    pages = flat_pages(case)
+    md = pd.get_pa_metadata(d["query"], d["key_cache"], d["context_lengths"], pages[1], 16, 2)
+    out = torch.empty(d["query"].shape, dtype=torch.bfloat16, device=DEV)
+    s = torch.cuda.Stream()
+
+    def call():
+        return pa_decode_ps_launch(out, d["query"], d["key_cache"], d["value_cache"], d["context_lengths"], pages[0],
+                                   pages[1], d["softmax_scale"], d["key_scale"], d["value_scale"], metadata=md)
+
+    with torch.cuda.stream(s):
+        call()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            call()
+    torch.cuda.synchronize()
+    for i in range(4):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        with torch.cuda.stream(s):
+            call()
+        torch.cuda.synchronize()

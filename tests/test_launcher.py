@@ -33,14 +33,15 @@ def prep(case, **kw):
 
 
 def test_small_block_slot_mode_marshalling():
-    case = make_case(batch=3, ctx=[10, 300, 1000], per_token=True, seed=1)
+    # 8 query columns per kv head: beyond the balanced split's limit
+    case = make_case(batch=3, ctx=[10, 300, 1000], num_query_heads=16, per_token=True, seed=1)
     call = prep(case)
     a = call._pa
     assert call.route == "ps_small_block"
     assert a.num_partitions == 8 and a.slots_per_workgroup in (1, 4)
     assert call._ra is not None  # partials + reduce launch
     assert a.per_token_kv == 1 and a.trans_v == 1 and a.block_size == 16
-    assert a.num_seqs == 3 and a.num_kv_heads == 2 and a.query_group_size == 4 and a.query_length == 1
+    assert a.num_seqs == 3 and a.num_kv_heads == 2 and a.query_group_size == 8 and a.query_length == 1
     assert a.stride_k_block == case["key_cache"].stride(0)
     assert a.stride_ks_block == case["key_scale"].stride(0) and a.stride_ks_head == case["key_scale"].stride(1)
     assert a.output is None  # slot mode: the reduce writes the output
@@ -94,7 +95,55 @@ def test_flat_route_uses_page_list():
     indptr = torch.tensor([0, 1, 4], dtype=torch.int32)
     call = prep(case, block_tables=None, kv_page_indices=pages, kv_indptr=indptr)
     assert call.route == "ps_split_reduce"
-    assert call._pa.kv_indptr == indptr.data_ptr() and call._pa.block_tables == pages.data_ptr()
+    assert call._sa.kv_indptr == indptr.data_ptr() and call._sa.block_tables == pages.data_ptr()
+    assert call._sa.max_blocks_per_seq == 4
+    # with slot partials requested: the partition pass over the same list
+    es = torch.empty(2, 2, 4, 4)
+    call2 = prep(case, block_tables=None, kv_page_indices=pages, kv_indptr=indptr, max_context_partition_num=4,
+                 exp_sums=es, max_logits=torch.empty_like(es),
+                 temporary_output=torch.empty(2, 2, 4, 4, 128, dtype=torch.bfloat16))
+    assert call2._pa.kv_indptr == indptr.data_ptr() and call2._pa.block_tables == pages.data_ptr()
+
+
+def test_balanced_split_marshalling():
+    """Ragged batch, nobody reads the slot partials: balanced stream split
+    over every resident wave, workspace sized by the library."""
+    from flydsl_amd import _lib
+
+    case = make_case(batch=5, ctx=[3, 900, 17000, 40, 2500], per_token=True, seed=9)
+    call = prep(case)
+    assert call.route == "ps_small_block" and call._pa is None and call._wra is None
+    sa = call._sa
+    assert sa.num_workers == 256 * 2 * 4
+    assert sa.kv_indptr is None and sa.stride_bt_seq == case["block_tables"].stride(0)
+    assert sa.max_blocks_per_seq == case["block_tables"].shape[1]
+    assert sa.per_token_kv == 1 and sa.query_group_size == 4 and sa.num_seqs == 5
+    assert sa.stride_ks_block == case["key_scale"].stride(0)
+    assert call._ws.numel() == _lib.balanced_workspace_bytes(5, 2, 1, 4, sa.num_workers)
+    # requested partials, or more columns than the split takes: partition pass
+    es = torch.empty(5, 2, 8, 4)
+    call2 = prep(case, exp_sums=es, max_logits=torch.empty_like(es),
+                 temporary_output=torch.empty(5, 2, 8, 4, 128, dtype=torch.bfloat16))
+    assert call2._sa is None and call2._pa is not None
+
+
+def test_worklist_route_marshalling():
+    case = make_case(batch=3, block_size=1024, ctx=[100, 3000, 5000], seed=10)
+    pages = torch.arange(0, 9, dtype=torch.int32)
+    indptr = torch.tensor([0, 1, 4, 9], dtype=torch.int32)
+    md = pd.get_pa_metadata(case["query"], case["key_cache"], case["context_lengths"], indptr, 8, 2)
+    call = prep(case, block_tables=None, kv_page_indices=pages, kv_indptr=indptr, metadata=md)
+    assert call.route == "ps_split_reduce"
+    sa, wr = call._sa, call._wra
+    assert sa.work_indptr == md["work_indptr"].data_ptr() and sa.work_info == md["work_info_flat"].data_ptr()
+    assert sa.partition_indptr == md["partition_indptr"].data_ptr() and sa.num_workers == md["num_sm"]
+    assert sa.stride_po_row == 8 * 128 and sa.stride_pl_row == 8
+    # the reduce reads from partial row query_length on
+    assert wr.partial_output == md["partial_output"].data_ptr() + 1 * 8 * 128 * 4
+    assert wr.partial_lse == md["partial_lse"].data_ptr() + 1 * 8 * 4
+    assert wr.num_groups == 3 and wr.num_query_heads == 8 and wr.max_query_length == 1
+    with pytest.raises(ValueError, match="missing"):
+        prep(case, block_tables=None, kv_page_indices=pages, kv_indptr=indptr, metadata={"num_sm": 4})
 
 
 def test_rejects_packed_fp8_query():
@@ -134,3 +183,21 @@ def test_partial_buffer_shape_checked():
     with pytest.raises(ValueError, match="exp_sums/max_logits must have shape"):
         prep(case, max_context_partition_num=8, exp_sums=es, max_logits=torch.empty_like(es),
              temporary_output=torch.empty(2, 2, 3, 4, 128, dtype=torch.bfloat16))
+
+
+def test_prepared_call_is_freed_without_the_cycle_collector():
+    """A dropped call releases its buffers at once (its launch thunks do not
+    refer back to it), so per-step workspaces are reused, not reallocated."""
+    import gc
+    import weakref
+
+    case = make_case(batch=5, ctx=[3, 900, 17000, 40, 2500], seed=11)
+    call = prep(case)
+    assert call._ws is not None
+    ref = weakref.ref(call._ws)
+    gc.disable()
+    try:
+        del call
+        assert ref() is None
+    finally:
+        gc.enable()
