@@ -251,16 +251,18 @@ struct QueryTile {
 };
 
 // Raw query rows (bf16 or f16 bits) -> fp8 hi + lo B operands.  Lane
-// (grp, c16) holds, for column cg * 16 + c16, the 32 head dims of 16-dim
-// chunks grp and grp + 4 in qraw[cg][0..3] (8 dims each).  The column is
-// scaled by a power of two putting its amax into [128, 256), which is exact.
+// (grp, c16) holds, for column col0 + cg * 16 + c16, the 32 head dims of
+// 16-dim chunks grp and grp + 4 in qraw[cg][0..3] (8 dims each).  The column
+// is scaled by a power of two putting its amax into [128, 256), which is
+// exact.  The column's query index sets its causal / window bounds.
 template <int NCG>
 __device__ __forceinline__ void prepare_query(QueryTile<NCG>& q, const i32x4 (&qraw)[NCG][4], int query_dtype,
-                                              float logit_scale, int ctx, int ql, int gqa, int W, int c16) {
+                                              float logit_scale, int ctx, int ql, int gqa, int W, int c16,
+                                              int col0 = 0) {
   const int eq = ql * gqa;
 #pragma unroll
   for (int cg = 0; cg < NCG; ++cg) {
-    const int e = cg * 16 + c16;
+    const int e = col0 + cg * 16 + c16;
     const bool valid = e < eq;
     const int qi = valid ? e / gqa : 0;
     float v[32];
@@ -938,6 +940,88 @@ struct WorklistWalk {
   }
 };
 
+// Start of run `wid` of a balanced launch over `num_workers` runs (waves
+// or workgroups): every context length is loaded once (lane l holds
+// sequences l*K .. l*K+K-1, K <= 16), scanned across the wave, and the run's
+// first (sequence, kv head, chunk) is located with a ballot and scalar
+// readlanes.  Returns false when the run is empty.
+__device__ __forceinline__ bool balanced_start(BalancedWalk& w, const pa_fp8_stream_args& a,
+                                               const int32_t* __restrict__ kv_indptr,
+                                               const int32_t* __restrict__ context_lengths, int wid, int lane) {
+  const int H = a.num_kv_heads;
+  const int ql = a.query_length;
+  const int W = a.sliding_window;
+  // Chunks per sequence: lane l holds sequences l*K .. l*K+K-1.
+  const int B = a.num_seqs;
+  const int K = pa_cdiv(B, 64);
+  // All loads first (indices clamped into the batch), then the counts.
+  int cnt[16], rl[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int bb = pa_min(lane * K + k, B - 1);
+    cnt[k] = context_lengths[bb];
+    const int32_t* rows = kv_indptr ? kv_indptr : context_lengths;
+    const int r0 = rows[bb], r1 = rows[kv_indptr ? bb + 1 : bb];
+    rl[k] = kv_indptr ? r1 - r0 : 1;
+  }
+  int mine = 0;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const bool real = k < K && lane * K + k < B;
+    cnt[k] = real && rl[k] > 0 ? pa_plan_seq_chunks(cnt[k], ql, W) : 0;
+    mine += cnt[k];
+  }
+  int incl = mine;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += t;
+  }
+  const int excl = incl - mine;
+  // Wave-uniform from here on (readlane), so the walk lives in SGPRs and
+  // its page lookups are scalar loads.
+  const long long T = (long long)__builtin_amdgcn_readlane(incl, 63) * H;
+  long long nwl = T / kMinChunksPerWave;
+  nwl = nwl < 1 ? 1 : nwl;
+  const int nw = nwl < a.num_workers ? (int)nwl : a.num_workers;
+  if (wid >= nw) return false;
+  const long long g0 = pa_plan_run_begin(wid, T, nw);
+  const long long g1 = pa_plan_run_begin(wid + 1, T, nw);
+  if (g1 <= g0) return false;
+  // The lane whose sequences hold chunk g0, then the sequence itself.
+  const uint64_t hit = __ballot(mine > 0 && (long long)excl * H <= g0 && g0 < (long long)incl * H);
+  if (hit == 0) return false;  // cannot happen: the lanes' ranges tile [0, T)
+  const int ls = __builtin_amdgcn_readfirstlane((int)__builtin_ctzll(hit));
+  long long S = __builtin_amdgcn_readlane(excl, ls);
+  int b0 = -1, n0 = 0;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int ck = __builtin_amdgcn_readlane(cnt[k], ls);
+    if (b0 < 0 && k < K) {
+      if ((S + ck) * H > g0) {
+        b0 = ls * K + k;
+        n0 = ck;
+      } else {
+        S += ck;
+      }
+    }
+  }
+  if (b0 < 0 || n0 <= 0) return false;  // as above
+  const long long off = g0 - S * H;
+  w.b = b0;
+  w.nb = n0;
+  w.h = (int)(off / n0);
+  w.c = (int)(off - (long long)w.h * n0);
+  w.gseg = S * H + (long long)w.h * n0;
+  w.left = (int)(g1 - g0);
+  w.first = 1;
+  w.wid = wid;
+  w.nw = nw;
+  w.T = T;
+  piece_sequence(w.seq, a, kv_indptr, context_lengths, b0);
+  return true;
+}
+
 // 4 consecutive head dims of an output row in the output dtype.
 __device__ __forceinline__ void store_out4(void* out, int dtype, int64_t off, f32x4 v) {
   if (dtype == PA_DTYPE_F32) {
@@ -998,74 +1082,7 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
     iwalk.idx = ld_uniform(work_indptr, wid);
     iwalk.end = ld_uniform(work_indptr, wid + 1);
   } else {
-    // Chunks per sequence: lane l holds sequences l*K .. l*K+K-1.
-    const int B = a.num_seqs;
-    const int K = pa_cdiv(B, 64);
-    // All loads first (indices clamped into the batch), then the counts.
-    int cnt[16], rl[16];
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int bb = pa_min(lane * K + k, B - 1);
-      cnt[k] = context_lengths[bb];
-      const int32_t* rows = kv_indptr ? kv_indptr : context_lengths;
-      const int r0 = rows[bb], r1 = rows[kv_indptr ? bb + 1 : bb];
-      rl[k] = kv_indptr ? r1 - r0 : 1;
-    }
-    int mine = 0;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const bool real = k < K && lane * K + k < B;
-      cnt[k] = real && rl[k] > 0 ? pa_plan_seq_chunks(cnt[k], ql, W) : 0;
-      mine += cnt[k];
-    }
-    int incl = mine;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int t = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += t;
-    }
-    const int excl = incl - mine;
-    // Wave-uniform from here on (readlane), so the walk lives in SGPRs and
-    // its page lookups are scalar loads.
-    const long long T = (long long)__builtin_amdgcn_readlane(incl, 63) * H;
-    long long nwl = T / kMinChunksPerWave;
-    nwl = nwl < 1 ? 1 : nwl;
-    const int nw = nwl < a.num_workers ? (int)nwl : a.num_workers;
-    if (wid >= nw) return;
-    const long long g0 = pa_plan_run_begin(wid, T, nw);
-    const long long g1 = pa_plan_run_begin(wid + 1, T, nw);
-    if (g1 <= g0) return;
-    // The lane whose sequences hold chunk g0, then the sequence itself.
-    const uint64_t hit = __ballot(mine > 0 && (long long)excl * H <= g0 && g0 < (long long)incl * H);
-    if (hit == 0) return;  // cannot happen: the lanes' ranges tile [0, T)
-    const int ls = __builtin_amdgcn_readfirstlane((int)__builtin_ctzll(hit));
-    long long S = __builtin_amdgcn_readlane(excl, ls);
-    int b0 = -1, n0 = 0;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int ck = __builtin_amdgcn_readlane(cnt[k], ls);
-      if (b0 < 0 && k < K) {
-        if ((S + ck) * H > g0) {
-          b0 = ls * K + k;
-          n0 = ck;
-        } else {
-          S += ck;
-        }
-      }
-    }
-    if (b0 < 0 || n0 <= 0) return;  // as above
-    const long long off = g0 - S * H;
-    iwalk.b = b0;
-    iwalk.nb = n0;
-    iwalk.h = (int)(off / n0);
-    iwalk.c = (int)(off - (long long)iwalk.h * n0);
-    iwalk.gseg = S * H + (long long)iwalk.h * n0;
-    iwalk.left = (int)(g1 - g0);
-    iwalk.first = 1;
-    iwalk.wid = wid;
-    iwalk.nw = nw;
-    iwalk.T = T;
-    piece_sequence(iwalk.seq, a, kv_indptr, context_lengths, b0);
+    if (!balanced_start(iwalk, a, kv_indptr, context_lengths, wid, lane)) return;
   }
   Walk cwalk = iwalk;  // the compute side replays the issue side's walk
   auto next_piece = [&](Walk& walk, Piece& p) -> bool {
@@ -1254,6 +1271,251 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
     if (!WORKLIST && cp.desc_cnt > 0 && lane == 0)
       *(i32x2*)(segdesc + 2 * ((int64_t)cp.b * H + cp.h)) = i32x2{cp.target, cp.desc_cnt};
     st.reset();
+  }
+}
+
+// Cooperative column-split decode for 17..64 query columns per kv head
+// (two to four 16-column blocks).  A workgroup has one wave per column
+// block; all of its waves read the same 32-token chunks from one shared
+// LDS ring of kCoopStages stages, each wave DMAing an equal share of every
+// chunk, with one barrier per chunk.  A wave therefore holds only its own
+// block's accumulators and query operands (no register spills, several
+// waves per SIMD), and the chunk is fetched from HBM once for all blocks.
+// Work comes from the same walks as pa_fp8_stream_kernel, at workgroup
+// granularity (one run or one bin per workgroup); every wave writes its own
+// columns of each piece (no merge inside the workgroup).  A piece's query
+// rows are loaded into registers during the previous piece's last chunk.
+constexpr int kCoopStages = 4;
+
+template <int NW, bool PER_TOKEN, bool BS16, bool WORKLIST>
+__global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
+    const pa_fp8_stream_args a, const int32_t* __restrict__ block_tables, const int32_t* __restrict__ kv_indptr,
+    const int32_t* __restrict__ context_lengths, const float* __restrict__ key_scale,
+    const float* __restrict__ value_scale, const int32_t* __restrict__ work_indptr,
+    const int32_t* __restrict__ work_info, const int32_t* __restrict__ partition_indptr,
+    int32_t* __restrict__ segdesc, float* __restrict__ part_out, float* __restrict__ part_lse,
+    void* __restrict__ output) {
+  static_assert(NW == 2 || NW == 4, "two or four waves share a chunk");
+  constexpr int S = kCoopStages;
+  constexpr int kStageBytes = kKBytes + kVBytes + (PER_TOKEN ? kScaleBytes : 0);
+  constexpr int kDmaPerWave = 8 / NW;  // of the chunk's 8 one-KiB key/value loads
+  constexpr int kLoads = kDmaPerWave + (PER_TOKEN ? 1 : 0);
+  __shared__ __attribute__((aligned(16))) unsigned char smem[S * kStageBytes];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = lane >> 4;
+  const int c16 = lane & 15;
+  const int wid = blockIdx.x;
+  const int H = a.num_kv_heads;
+  const int ql = a.query_length;
+  const int gqa = a.query_group_size;
+  const int eq = ql * gqa;
+  const int W = a.sliding_window;
+  const int bs = a.block_size;
+  const int bs_shift = BS16 ? 4 : __builtin_ctz((unsigned)bs);
+  const int nblocks = a.num_blocks;
+  const int e = wave * 16 + c16;  // this lane's query column
+
+  using Walk = typename std::conditional<WORKLIST, WorklistWalk, BalancedWalk>::type;
+  Walk iwalk;
+  if constexpr (WORKLIST) {
+    if (wid >= a.num_workers) return;
+    iwalk.idx = ld_uniform(work_indptr, wid);
+    iwalk.end = ld_uniform(work_indptr, wid + 1);
+  } else {
+    if (!balanced_start(iwalk, a, kv_indptr, context_lengths, wid, lane)) return;
+  }
+  Walk cwalk = iwalk;
+  auto next_piece = [&](Walk& walk, Piece& p) -> bool {
+    if constexpr (WORKLIST)
+      return walk.next(p, a, kv_indptr, context_lengths, work_info, partition_indptr);
+    else
+      return walk.next(p, a, kv_indptr, context_lengths);
+  };
+  const int koff_lane = BS16 ? lane * 16 : (lane >> 4) * (bs * 16) + (lane & 15) * 16;
+  const int voff_plain = lane * bs;
+  auto clamp_page = [&](int p) -> int {
+    p = p < 0 ? 0 : p;
+    return p < nblocks ? p : nblocks - 1;
+  };
+
+  // ---------------- issue side: this wave's share of every chunk ----------------
+  Piece ip;
+  bool iok = next_piece(iwalk, ip);
+  while (iok && ip.n == 0) iok = next_piece(iwalk, ip);
+  int ic = 0;
+  auto issue_next = [&](int st) {
+    const int tb = ip.tb0 + ic * kChunk;
+    const int lp0 = tb >> bs_shift;
+    const int p0 = clamp_page(ld_uniform(block_tables, ip.bt_off + pa_min(lp0, ip.last_page)));
+    const int p1 = BS16 ? clamp_page(ld_uniform(block_tables, ip.bt_off + pa_min(lp0 + 1, ip.last_page))) : p0;
+    const uint8_t* kbase = (const uint8_t*)a.key_cache + (int64_t)ip.h * a.stride_k_head;
+    const uint8_t* vbase = (const uint8_t*)a.value_cache + (int64_t)ip.h * a.stride_v_head;
+    LDS_AS unsigned char* sk = (LDS_AS unsigned char*)smem + st * kStageBytes;
+    LDS_AS unsigned char* sv = sk + kKBytes;
+    // Load i (0..7): i < 4 keys, else values; half hh = (i >> 1) & 1, 1 KiB piece q2 = i & 1.
+#pragma unroll
+    for (int j = 0; j < kDmaPerWave; ++j) {
+      const int i = wave * kDmaPerWave + j;
+      const bool isk = i < 4;
+      const int hh = (i >> 1) & 1, q2 = i & 1;
+      if (BS16) {
+        const int pg = hh ? p1 : p0;
+        if (isk)
+          lds_dma16(kbase + (int64_t)pg * a.stride_k_block + koff_lane + q2 * 1024, sk + hh * kKHalf + q2 * 1024);
+        else
+          lds_dma16(vbase + (int64_t)pg * a.stride_v_block + lane * 16 + q2 * 1024, sv + hh * 2048 + q2 * 1024);
+      } else {
+        const int s0 = tb & (bs - 1);
+        if (isk) {
+          lds_dma16(kbase + (int64_t)p0 * a.stride_k_block + s0 * 16 + hh * 256 + q2 * (4 * bs * 16) + koff_lane,
+                    sk + hh * kKHalf + q2 * 1024);
+        } else if (a.trans_v) {
+          lds_dma16(vbase + (int64_t)p0 * a.stride_v_block + (s0 >> 4) * (kHead * 16) + hh * 2048 + q2 * 1024 +
+                        lane * 16,
+                    sv + hh * 2048 + q2 * 1024);
+        } else {
+          lds_dma16(vbase + (int64_t)p0 * a.stride_v_block + s0 + hh * 16 + q2 * (64 * bs) + voff_plain,
+                    sv + hh * 2048 + q2 * 1024);
+        }
+      }
+    }
+    if (PER_TOKEN) {
+      // Every wave writes the same 256 bytes of scales: each wave's own
+      // wait then covers them.
+      LDS_AS unsigned char* ss = sv + kVBytes;
+      if (lane < 16) {
+        const int tt = (lane & 7) * 4;
+        const int pg2 = BS16 ? (tt >= 16 ? p1 : p0) : p0;
+        const int sidx = BS16 ? (tt & 15) : (tb & (bs - 1)) + tt;
+        const float* base = (lane < 8 ? key_scale : value_scale) + (int64_t)ip.h * a.stride_ks_head;
+        lds_dma16(base + (int64_t)pg2 * a.stride_ks_block + sidx, ss);
+      }
+    }
+    if (++ic == ip.n) {
+      ic = 0;
+      do {
+        iok = next_piece(iwalk, ip);
+      } while (iok && ip.n == 0);
+    }
+  };
+
+  // ---------------- query rows of a piece (registers) ----------------
+  i32x4 qraw[1][4];
+  auto load_query = [&](const Piece& p) {
+    if (e < eq) {
+      const int qi = e / gqa;
+      const int g = e - qi * gqa;
+      const uint16_t* qp = (const uint16_t*)a.query + (int64_t)(p.orow + qi) * a.stride_q_tok +
+                           (int64_t)(p.h * gqa + g) * a.stride_q_head;
+      qraw[0][0] = *(const i32x4*)(qp + 16 * grp);
+      qraw[0][1] = *(const i32x4*)(qp + 16 * grp + 8);
+      qraw[0][2] = *(const i32x4*)(qp + 16 * (grp + 4));
+      qraw[0][3] = *(const i32x4*)(qp + 16 * (grp + 4) + 8);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qraw[0][i] = i32x4{0, 0, 0, 0};
+    }
+  };
+
+  const float k_tensor_scale = PER_TOKEN ? 1.0f : key_scale[0];
+  const float v_tensor_scale = PER_TOKEN ? 1.0f : value_scale[0];
+  const float logit_scale = a.softmax_scale * kLog2e * k_tensor_scale;
+  const int krow = (c16 >> 3) * kKHalf + (8 * ((c16 >> 2) & 1) + (c16 & 3)) * 16;
+  WaveState<1> st;
+  st.reset();
+  QueryTile<1> qt;
+
+  // Compute side.  A piece's query rows are consumed at its first chunk and
+  // the next non-empty piece's rows are loaded during its last chunk, so a
+  // single register set carries them, in the same in-order load queue as
+  // the chunks.
+  Piece cp;
+  bool cok = next_piece(cwalk, cp);
+  auto next_nonempty = [&](Walk w, Piece p, bool ok, Piece& out) -> bool {
+    while (ok && p.n == 0) ok = next_piece(w, p);
+    out = p;
+    return ok;
+  };
+  {
+    Piece q0;
+    if (next_nonempty(cwalk, cp, cok, q0)) load_query(q0);
+  }
+  int issued = 0;  // chunks this workgroup has issued
+#pragma unroll
+  for (int k = 0; k < S - 1; ++k)
+    if (iok) {
+      issue_next(k);
+      ++issued;
+    }
+
+  int gc = 0;  // chunks computed
+  while (cok) {
+    Piece np;
+    const bool nok = next_piece(cwalk, np);
+    for (int k = 0; k < cp.n; ++k) {
+      // Wait for this wave's loads of chunk gc: newer chunks (up to S - 2)
+      // may stay in flight.  Loads retire in order; query rows or stores
+      // issued in between are only waited for early.
+      const int newer = issued - gc - 1;
+      if (newer >= 2)
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * kLoads));
+      else if (newer == 1)
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(kLoads));
+      else
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+      // Every wave's share of chunk gc is now in LDS and every wave is done
+      // with chunk gc - 1, whose stage the next issue reuses.  A bare
+      // s_barrier: the DMA completion was awaited explicitly above (a fenced
+      // barrier would also wait for the chunks still in flight).
+      asm volatile("s_barrier" ::: "memory");
+      if (k == 0) prepare_query<1>(qt, qraw, a.query_dtype, logit_scale, cp.ctx, ql, gqa, W, c16, wave * 16);
+      if (k == cp.n - 1) {
+        Piece q;
+        if (next_nonempty(cwalk, np, nok, q)) load_query(q);
+      }
+      if (iok) {
+        issue_next((gc + S - 1) % S);
+        ++issued;
+      }
+      compute_chunk<1, PER_TOKEN>(st, qt, (const LDS_AS unsigned char*)smem + (gc % S) * kStageBytes, krow, grp, c16,
+                                  cp.tb0 + k * kChunk);
+      ++gc;
+    }
+    // ---- the piece is complete: this wave's columns ----
+    const float vfin = PER_TOKEN ? st.vsmax : v_tensor_scale;
+    const float L = sum_over_groups(st.lsum[0]);
+    const float m = st.m2[0];
+    if (e < eq) {
+      const int qi = e / gqa;
+      const int g = e - qi * gqa;
+      const int qh = cp.h * gqa + g;
+      const float sc = L > 0.0f ? vfin / L : 0.0f;
+      if (cp.target < 0) {
+        const int64_t off = (int64_t)(cp.orow + qi) * a.stride_out_tok + (int64_t)qh * a.stride_out_head + 4 * grp;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) store_out4(output, a.output_dtype, off + 16 * j, st.acc[0][j] * sc);
+      } else {
+        int64_t po, pl;
+        if (WORKLIST) {
+          po = (int64_t)(cp.target + qi) * a.stride_po_row + (int64_t)qh * kHead;
+          pl = (int64_t)(cp.target + qi) * a.stride_pl_row + qh;
+        } else {
+          pl = (int64_t)cp.target * eq + e;
+          po = pl * kHead;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) *(f32x4*)(part_out + po + 16 * j + 4 * grp) = st.acc[0][j] * sc;
+        if (grp == 0) part_lse[pl] = L > 0.0f ? kLn2 * (m + __builtin_amdgcn_logf(L) - 8.0f) : kNegInf;
+      }
+    }
+    if (!WORKLIST && cp.desc_cnt > 0 && wave == 0 && lane == 0)
+      *(i32x2*)(segdesc + 2 * ((int64_t)cp.b * H + cp.h)) = i32x2{cp.target, cp.desc_cnt};
+    st.reset();
+    cp = np;
+    cok = nok;
   }
 }
 
@@ -1514,6 +1776,44 @@ hipError_t dispatch_stream(const pa_fp8_stream_args& a, unsigned grid, hipStream
   }
 }
 
+template <int NW, bool PT, bool BS16, bool WL>
+hipError_t launch_coop(const pa_fp8_stream_args& a, unsigned grid, hipStream_t s, int32_t* desc, float* po,
+                       float* pl) {
+  hipLaunchKernelGGL((pa_fp8_coop_kernel<NW, PT, BS16, WL>), dim3(grid), dim3(64 * NW), 0, s, a, a.block_tables,
+                     a.kv_indptr, a.context_lengths, a.key_scale, a.value_scale, a.work_indptr, a.work_info,
+                     a.partition_indptr, desc, po, pl, a.output);
+  return hipGetLastError();
+}
+
+template <int NW, bool WL>
+hipError_t dispatch_coop_nw(const pa_fp8_stream_args& a, unsigned grid, hipStream_t s, int32_t* desc, float* po,
+                            float* pl) {
+  const bool pt = a.per_token_kv != 0;
+  const bool bs16 = a.block_size == 16;
+  if (pt)
+    return bs16 ? launch_coop<NW, true, true, WL>(a, grid, s, desc, po, pl)
+                : launch_coop<NW, true, false, WL>(a, grid, s, desc, po, pl);
+  return bs16 ? launch_coop<NW, false, true, WL>(a, grid, s, desc, po, pl)
+              : launch_coop<NW, false, false, WL>(a, grid, s, desc, po, pl);
+}
+
+// Waves per cooperative workgroup: one per 16-column query block (three
+// blocks run on four waves, the fourth computing only masked columns).
+int coop_waves(int eq) { return eq <= 32 ? 2 : 4; }
+
+// Resident cooperative workgroups per CU (LDS: kCoopStages chunk stages
+// per workgroup; registers: three waves per SIMD).
+int coop_per_cu(int nw) { return nw == 2 ? 4 : 3; }
+
+// One launch of the per-wave (<= 16 columns) or cooperative kernel.
+template <bool WL>
+hipError_t dispatch_streaming(const pa_fp8_stream_args& a, hipStream_t s, int32_t* desc, float* po, float* pl) {
+  const int eq = a.query_length * a.query_group_size;
+  if (eq <= 16) return dispatch_stream<WL>(a, (unsigned)pa_cdiv(a.num_workers, kWaves), s, desc, po, pl);
+  return coop_waves(eq) == 2 ? dispatch_coop_nw<2, WL>(a, (unsigned)a.num_workers, s, desc, po, pl)
+                             : dispatch_coop_nw<4, WL>(a, (unsigned)a.num_workers, s, desc, po, pl);
+}
+
 // Checks shared by both streaming entry points.
 int check_stream_args(const pa_fp8_stream_args* a) {
   if (!a) return PA_ERR_NULL_ARG;
@@ -1527,7 +1827,7 @@ int check_stream_args(const pa_fp8_stream_args* a) {
   if (a->num_seqs < 0 || a->num_kv_heads <= 0 || a->query_length <= 0 || a->query_group_size <= 0 ||
       a->num_blocks <= 0 || a->max_blocks_per_seq <= 0 || a->sliding_window < 0 || a->num_workers <= 0)
     return PA_ERR_SHAPE;
-  if (a->query_length * a->query_group_size > 16) return PA_ERR_GROUP;
+  if (a->query_length * a->query_group_size > 64) return PA_ERR_GROUP;
   if (a->query_dtype != PA_DTYPE_BF16 && a->query_dtype != PA_DTYPE_F16) return PA_ERR_DTYPE;
   if (a->output_dtype != PA_DTYPE_BF16 && a->output_dtype != PA_DTYPE_F16 && a->output_dtype != PA_DTYPE_F32)
     return PA_ERR_DTYPE;
@@ -1650,7 +1950,8 @@ int pa_fp8_decode_reduce(const pa_fp8_reduce_args* a, void* stream) {
 int pa_fp8_stream_workers(int num_cu, int query_length, int query_group_size, int per_token_kv) {
   if (num_cu <= 0 || query_length <= 0 || query_group_size <= 0) return PA_ERR_SHAPE;
   const int eq = query_length * query_group_size;
-  if (eq > 16) return PA_ERR_GROUP;
+  if (eq > 64) return PA_ERR_GROUP;
+  if (eq > 16) return num_cu * coop_per_cu(coop_waves(eq));
   const int lds = stream_lds_bytes(stream_nq(eq), per_token_kv != 0);
   const int per_cu = 160 * 1024 / lds >= 2 ? 2 : 1;
   return num_cu * per_cu * kWaves;
@@ -1677,8 +1978,7 @@ int pa_fp8_decode_balanced(const pa_fp8_stream_args* a, void* workspace, int64_t
   int32_t* desc = (int32_t*)(ws + l.desc);
   float* pl = (float*)(ws + l.lse);
   float* po = (float*)(ws + l.out);
-  hipError_t err =
-      dispatch_stream<false>(*a, (unsigned)pa_cdiv(a->num_workers, kWaves), (hipStream_t)stream, desc, po, pl);
+  hipError_t err = dispatch_streaming<false>(*a, (hipStream_t)stream, desc, po, pl);
   return err == hipSuccess ? PA_OK : (int)err;
 }
 
@@ -1709,8 +2009,7 @@ int pa_fp8_decode_worklist(const pa_fp8_stream_args* a, void* stream) {
     return PA_ERR_NULL_ARG;
   if (!aligned16(a->partial_output) || (a->stride_po_row % 4)) return PA_ERR_ALIGN;
   if (a->num_seqs == 0) return PA_OK;
-  hipError_t err = dispatch_stream<true>(*a, (unsigned)pa_cdiv(a->num_workers, kWaves), (hipStream_t)stream, nullptr,
-                                         a->partial_output, a->partial_lse);
+  hipError_t err = dispatch_streaming<true>(*a, (hipStream_t)stream, nullptr, a->partial_output, a->partial_lse);
   return err == hipSuccess ? PA_OK : (int)err;
 }
 

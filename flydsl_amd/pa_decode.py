@@ -222,21 +222,29 @@ def _schedule(route: str, batch: int, kv_heads: int, P: int, eqgs: int, capacity
     return 1
 
 
-# Balanced stream split: at most this many query columns per kv head (the
-# per-wave query images then leave room for two workgroups per CU) and this
-# many sequences (the in-kernel split scans them in one pass).
+# Balanced stream split: per-wave runs for at most BALANCED_MAX_COLUMNS query
+# columns per kv head (the per-wave query images then leave room for two
+# workgroups per CU), cooperative workgroup runs above STREAM_MAX_COLUMNS
+# (one wave per 16-column block), up to this many sequences (the in-kernel
+# split scans them in one pass).
 BALANCED_MAX_COLUMNS = 4
 BALANCED_MAX_SEQS = 1024
-# Work-list decode: one 16-column query block.
+# Per-wave streaming decode: one 16-column query block; cooperative beyond.
 STREAM_MAX_COLUMNS = 16
+COOP_MAX_COLUMNS = 64
 
 
 def _balanced_ok(route: str, batch: int, eqgs: int, user_partials: bool, owner: bool) -> bool:
-    """Balanced stream split for a call whose slot partials nobody reads and
-    that the owner schedule does not take: every wave gets an equal run of
-    the batch's chunks, so one long sequence no longer sets the duration."""
-    return (route in ("small", "flat") and not user_partials and not owner and eqgs <= BALANCED_MAX_COLUMNS
-            and 0 < batch <= BALANCED_MAX_SEQS)
+    """Balanced stream split for a call whose slot partials nobody reads:
+    every wave (or, for more than 16 query columns, every cooperative
+    workgroup) gets an equal run of the batch's chunks, so one long sequence
+    no longer sets the duration.  Up to 16 columns the owner schedule keeps
+    the calls it takes (one launch, nothing to merge)."""
+    if route not in ("small", "flat") or user_partials or not 0 < batch <= BALANCED_MAX_SEQS:
+        return False
+    if eqgs <= BALANCED_MAX_COLUMNS:
+        return not owner
+    return STREAM_MAX_COLUMNS < eqgs <= COOP_MAX_COLUMNS
 
 
 class PreparedDecode:
@@ -451,7 +459,7 @@ def prepare_pa_decode(
         if max_context_partition_num == 0:
             max_context_partition_num = get_recommended_splits(batch_size, num_kv_heads, split_kv_blocks=1)
         kv_ind = kv_indptr
-        if metadata is not None and eqgs <= STREAM_MAX_COLUMNS:
+        if metadata is not None and eqgs <= COOP_MAX_COLUMNS:
             return _prepare_worklist(
                 metadata, output, query, key_cache, value_cache, context_lengths, kv_page_indices, kv_indptr,
                 softmax_scale, key_scale, value_scale, per_token_kv, trans_v, query_input_dtype, output_dtype, s)
@@ -703,10 +711,7 @@ def get_pa_metadata(
     gqa = num_query_heads // num_kv_heads
     eqgs = query_length * gqa
     num_cu = _cu_count(dev)
-    if eqgs <= STREAM_MAX_COLUMNS:
-        workers = _lib.stream_workers(num_cu, query_length, gqa, True)
-    else:
-        workers = num_cu * 3
+    workers = _lib.stream_workers(num_cu, query_length, gqa, True)
     num_sm = max(num_kv_heads, (workers // num_kv_heads) * num_kv_heads)
     ctx_host = context_lengths.detach().to("cpu", torch.int32)
     n_works, plan = _lib.plan_worklist(ctx_host.numpy(), num_kv_heads, gqa, query_length, num_sm, partition_size)

@@ -169,7 +169,10 @@ int pa_fp8_decode_reduce(const pa_fp8_reduce_args* args, void* hip_stream);
  * through one LDS pipeline, and writes each piece either straight into
  * `output` (the piece is the whole (sequence, kv head)) or as a float32
  * partial (normalised output row plus its log-sum-exp) for a merge pass.
- * query_length * query_group_size <= 16.
+ * Up to 16 query columns per kv head (query_length * gqa) every wave walks
+ * its own pieces; 17..64 columns run cooperatively: a workgroup has one
+ * wave per 16-column block, the waves share each chunk through LDS and the
+ * workgroup walks the pieces (num_workers then counts workgroups).
  *
  * pa_fp8_decode_worklist: pieces come from the work list of
  * pa_fp8_plan_worklist (one bin per wave: num_workers = bins).  Replaces
@@ -230,7 +233,7 @@ typedef struct pa_fp8_stream_args {
   int32_t trans_v;
   int32_t query_dtype;
   int32_t output_dtype;
-  int32_t num_workers; /* waves of the launch (4 per workgroup) */
+  int32_t num_workers; /* runs or bins: waves (<= 16 columns) or workgroups */
   float softmax_scale;
 } pa_fp8_stream_args;
 
@@ -241,8 +244,9 @@ int pa_fp8_merge_balanced(const pa_fp8_stream_args* args, const void* workspace,
                           void* hip_stream);
 int64_t pa_fp8_balanced_workspace_bytes(int num_seqs, int num_kv_heads, int query_length, int query_group_size,
                                         int num_workers);
-/* Waves a streaming launch keeps resident on num_cu CUs (4 per workgroup;
- * two workgroups per CU when their LDS fits, else one). */
+/* Runs a streaming launch keeps resident on num_cu CUs: waves for up to 16
+ * query columns (4 per workgroup; two workgroups per CU when their LDS
+ * fits, else one), cooperative workgroups for 17..64 columns. */
 int pa_fp8_stream_workers(int num_cu, int query_length, int query_group_size, int per_token_kv);
 
 /*

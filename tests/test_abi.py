@@ -60,8 +60,11 @@ def test_stream_worker_counts():
     assert _lib.stream_workers(256, 1, 4, True) == 2048
     assert _lib.stream_workers(256, 1, 8, False) == 1024
     assert _lib.stream_workers(256, 4, 4, True) == 1024
+    # 17..64 columns: cooperative workgroups (4 per CU for 2-wave, 3 for 4-wave groups)
+    assert _lib.stream_workers(256, 4, 8, True) == 1024
+    assert _lib.stream_workers(256, 4, 16, True) == 768
     with pytest.raises(RuntimeError):
-        _lib.stream_workers(256, 4, 8, True)  # 32 columns: not a streaming shape
+        _lib.stream_workers(256, 4, 32, True)  # 128 columns: not supported
     ws = _lib.balanced_workspace_bytes(128, 8, 1, 4, 2048)
     assert ws >= 128 * 8 * 8 + 2 * 2048 * 4 * 4 + 2 * 2048 * 4 * 128 * 4
 

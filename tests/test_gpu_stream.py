@@ -44,7 +44,8 @@ def balanced(num_cu=None):
     pretend the GPU has `num_cu` CUs (fewer, longer runs)."""
     saved = pd._balanced_ok, pd._cu_count
     pd._balanced_ok = lambda route, batch, eqgs, user_partials, owner: (
-        route in ("small", "flat") and not user_partials and eqgs <= pd.BALANCED_MAX_COLUMNS)
+        route in ("small", "flat") and not user_partials
+        and (eqgs <= pd.BALANCED_MAX_COLUMNS or pd.STREAM_MAX_COLUMNS < eqgs <= pd.COOP_MAX_COLUMNS))
     if num_cu is not None:
         pd._cu_count = lambda device=None: num_cu
     try:
@@ -107,6 +108,13 @@ BALANCED_CASES = {
     "gqa1": dict(batch=5, num_query_heads=8, num_kv_heads=8, ctx_range=(1, 2500)),
     "page64_ragged": dict(batch=7, block_size=64, ctx=[1, 64, 65, 900, 4000, 130, 2049], per_token=True),
     "uniform_data": dict(batch=6, dist="uniform", ctx_range=(1, 3000)),
+    # cooperative workgroups (17..64 query columns per kv head)
+    "coop_ql4_gqa16_pt_page64": dict(batch=6, query_length=4, num_query_heads=64, num_kv_heads=4, block_size=64,
+                                     per_token=True, ctx_range=(4, 3000)),
+    "coop_ql2_gqa16": dict(batch=5, query_length=2, num_query_heads=16, num_kv_heads=1, ctx_range=(2, 2500)),
+    "coop_ql3_gqa16_pt": dict(batch=5, query_length=3, num_query_heads=32, num_kv_heads=2, per_token=True,
+                              ctx=[3, 40, 700, 2100, 5000]),
+    "coop_gqa32_edges": dict(batch=9, num_query_heads=32, num_kv_heads=1, ctx=[1, 2, 31, 32, 33, 255, 257, 1023, 4000]),
 }
 
 
@@ -191,6 +199,9 @@ WORKLIST_CASES = {
     "ql4_gqa4_pt": dict(batch=4, query_length=4, num_query_heads=8, num_kv_heads=2, per_token=True,
                         ctx_range=(4, 5000)),
     "gqa16": dict(batch=3, num_query_heads=16, num_kv_heads=1, ctx_range=(1, 9000)),
+    "coop_ql4_gqa16_pt": dict(batch=4, query_length=4, num_query_heads=32, num_kv_heads=2, per_token=True,
+                              ctx_range=(4, 6000)),
+    "coop_gqa32": dict(batch=4, num_query_heads=32, num_kv_heads=1, ctx_range=(1, 7000)),
 }
 
 
