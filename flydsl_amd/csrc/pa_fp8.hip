@@ -374,8 +374,12 @@ __device__ __forceinline__ void compute_chunk(WaveState<NCG>& s, const QueryTile
     for (int j = 0; j < 8; ++j) cmax = fmaxf(cmax, vsc[j]);
     cmax = max_over_groups(cmax);
     const float vnew = fmaxf(s.vsmax, cmax);
-    vratio = vnew > 0.0f ? s.vsmax / vnew : 1.0f;
-    vinv = vnew > 0.0f ? 1.0f / vnew : 0.0f;
+    // Both factors are ratios against the same running maximum, applied to
+    // the probabilities and to the accumulator alike; rcp's rounding cancels
+    // when the final output multiplies by that maximum again.
+    const float rv = __builtin_amdgcn_rcpf(vnew);
+    vratio = vnew > 0.0f ? s.vsmax * rv : 1.0f;
+    vinv = vnew > 0.0f ? rv : 0.0f;
     s.vsmax = vnew;
   }
 
@@ -386,15 +390,22 @@ __device__ __forceinline__ void compute_chunk(WaveState<NCG>& s, const QueryTile
     f32x4 lb = mfma_fp8_k128(KB, q.hi[cg], zz);
     la = mfma_fp8_k128(KA, q.lo[cg], la);
     lb = mfma_fp8_k128(KB, q.lo[cg], lb);
+    // Base-2 logits l = raw * fac (* per-token key scale).  When the factor
+    // is one positive constant for the column (per-tensor scales) the
+    // maximum is taken on the raw products, which orders them the same way,
+    // and the exponent is one FMA per logit.
     float lg[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      lg[i] = la[i] * q.fac[cg];
-      lg[4 + i] = lb[i] * q.fac[cg];
+      lg[i] = la[i];
+      lg[4 + i] = lb[i];
     }
-    if (PER_TOKEN) {
+    const float fac = q.fac[cg];
+    const bool prescale = PER_TOKEN || !(fac > 0.0f);  // wave-uniform
+    const float post = prescale ? 1.0f : fac;
+    if (prescale) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) lg[j] *= ksc[j];
+      for (int j = 0; j < 8; ++j) lg[j] *= PER_TOKEN ? fac * ksc[j] : fac;
     }
     if (!interior) {
 #pragma unroll
@@ -405,7 +416,7 @@ __device__ __forceinline__ void compute_chunk(WaveState<NCG>& s, const QueryTile
     }
     float cmax =
         fmaxf(fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3])), fmaxf(fmaxf(lg[4], lg[5]), fmaxf(lg[6], lg[7])));
-    cmax = max_over_groups(cmax);
+    cmax = max_over_groups(cmax) * post;  // post > 0: -inf stays -inf
     const float mnew = fmaxf(s.m2[cg], cmax);
     const float muse = mnew == kNegInf ? 0.0f : mnew;
     const float alpha = __builtin_amdgcn_exp2f(s.m2[cg] - muse);
@@ -415,7 +426,7 @@ __device__ __forceinline__ void compute_chunk(WaveState<NCG>& s, const QueryTile
     const float bias = 8.0f - muse;  // 256 * exp(l - m)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      pr[j] = __builtin_amdgcn_exp2f(lg[j] + bias);
+      pr[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(lg[j], post, bias));
       psum += pr[j];
     }
     s.lsum[cg] = s.lsum[cg] * alpha + psum;
@@ -1575,22 +1586,29 @@ __device__ __forceinline__ void store_out2(void* out, int dtype, int64_t off, fl
   }
 }
 
-// Merge of a balanced launch: one wave per (sequence, kv head, column).
-// Pairs held whole by one wave were written by the decode; pairs with no
-// visible key get zeros; split pairs merge their pieces: the first piece
-// is partial id segdesc[0], the others are the first pieces (id 2w) of the
-// following waves.
+// Merge of a balanced launch: one wave per (sequence, kv head, block of
+// 64 / LPC query columns); lane l takes column l % (64 / LPC) of the block
+// and 128 / LPC head dims, and folds that column's pieces itself (running
+// log-sum-exp), with every load of a batch of pieces issued before use.
+// Pairs a single run held whole were written by the decode; pairs with no
+// visible key get zeros; a cut pair's pieces are partial id segdesc[0] (the
+// first run's) and the first piece (id 2r) of each following run r.
+template <int LPC>
 __global__ __launch_bounds__(256) void pa_fp8_segment_merge_kernel(const pa_fp8_stream_args a,
                                                                    const int32_t* segdesc, const float* part_out,
                                                                    const float* part_lse) {
+  constexpr int kCols = 64 / LPC;       // columns per wave
+  constexpr int kVec = 128 / LPC / 4;   // f32x4 per lane per piece
+  constexpr int kBatch = 16 / kVec;     // pieces whose loads are in flight together
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int ql = a.query_length, gqa = a.query_group_size, eq = ql * gqa;
-  const int64_t rows = (int64_t)a.num_seqs * a.num_kv_heads * eq;
+  const int nblk = (eq + kCols - 1) / kCols;
+  const int64_t rows = (int64_t)a.num_seqs * a.num_kv_heads * nblk;
   if (row >= rows) return;
-  const int e = (int)(row % eq);
-  const int h = (int)((row / eq) % a.num_kv_heads);
-  const int b = (int)(row / ((int64_t)eq * a.num_kv_heads));
+  const int blk = (int)(row % nblk);
+  const int h = (int)((row / nblk) % a.num_kv_heads);
+  const int b = (int)(row / ((int64_t)nblk * a.num_kv_heads));
   // The pair's descriptor is read together with its length (it is only
   // meaningful, and only used, when the pair has visible keys).
   const int ctx = a.context_lengths[b];
@@ -1598,19 +1616,51 @@ __global__ __launch_bounds__(256) void pa_fp8_segment_merge_kernel(const pa_fp8_
   int rl = 1;
   if (a.kv_indptr) rl = a.kv_indptr[b + 1] - a.kv_indptr[b];
   const int nb = rl > 0 ? pa_plan_seq_chunks(ctx, ql, a.sliding_window) : 0;
-  float o0 = 0.0f, o1 = 0.0f;
+  const int e = blk * kCols + lane % kCols;
+  const int d0 = 4 * kVec * (lane / kCols);
+  f32x4 o[kVec];
+#pragma unroll
+  for (int i = 0; i < kVec; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   if (nb > 0) {
     const int pid0 = d[0], cnt = d[1];
     if (cnt <= 1) return;  // written by the decode
-    const int w0 = pid0 >> 1;
-    auto pid = [&](int i) -> int64_t { return i == 0 ? pid0 : 2 * (int64_t)(w0 + i); };
-    merge_rows<8>(
-        cnt, part_lse, part_out, [&](int i) { return pid(i) * eq + e; },
-        [&](int i) { return (pid(i) * eq + e) * kHead; }, lane, o0, o1);
+    if (e < eq) {
+      const int w0 = pid0 >> 1;
+      float M = kNegInf, tot = 0.0f;
+      for (int i0 = 0; i0 < cnt; i0 += kBatch) {
+        float l[kBatch];
+        f32x4 x[kBatch][kVec];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          const int i = i0 + k < cnt ? i0 + k : cnt - 1;
+          const int64_t pid = i == 0 ? pid0 : 2 * (int64_t)(w0 + i);
+          l[k] = part_lse[pid * eq + e];
+          const f32x4* src = (const f32x4*)(part_out + (pid * eq + e) * kHead + d0);
+#pragma unroll
+          for (int j = 0; j < kVec; ++j) x[k][j] = src[j];
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          if (i0 + k >= cnt || l[k] == kNegInf) continue;
+          const float Mn = fmaxf(M, l[k]);
+          const float fold = M == kNegInf ? 0.0f : __expf(M - Mn);
+          const float w = __expf(l[k] - Mn);
+          tot = tot * fold + w;
+#pragma unroll
+          for (int j = 0; j < kVec; ++j) o[j] = o[j] * fold + x[k][j] * w;
+          M = Mn;
+        }
+      }
+      const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
+#pragma unroll
+      for (int j = 0; j < kVec; ++j) o[j] *= inv;
+    }
   }
+  if (e >= eq) return;
   const int qi = e / gqa, g = e - qi * gqa;
-  const int64_t off = (int64_t)(b * ql + qi) * a.stride_out_tok + (int64_t)(h * gqa + g) * a.stride_out_head + 2 * lane;
-  store_out2(a.output, a.output_dtype, off, o0, o1);
+  const int64_t off = (int64_t)(b * ql + qi) * a.stride_out_tok + (int64_t)(h * gqa + g) * a.stride_out_head + d0;
+#pragma unroll
+  for (int j = 0; j < kVec; ++j) store_out4(a.output, a.output_dtype, off + 4 * j, o[j]);
 }
 
 // Merge of work-list partials: one wave per (group, query, query head).
@@ -1992,12 +2042,19 @@ int pa_fp8_merge_balanced(const pa_fp8_stream_args* a, const void* workspace, in
   const int eq = a->query_length * a->query_group_size;
   const BalancedLayout l = balanced_layout(a->num_seqs, a->num_kv_heads, eq, a->num_workers);
   if (workspace_bytes < l.total) return PA_ERR_SHAPE;
-  const int64_t rows = (int64_t)a->num_seqs * a->num_kv_heads * eq;
+  // Up to 4 columns: 16 lanes per column (all lanes busy); else 4.
+  const bool narrow = eq <= 4;
+  const int cols = narrow ? 4 : 16;
+  const int64_t rows = (int64_t)a->num_seqs * a->num_kv_heads * ((eq + cols - 1) / cols);
   if (rows == 0) return PA_OK;
   const unsigned char* ws = (const unsigned char*)workspace;
-  hipLaunchKernelGGL(pa_fp8_segment_merge_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
-                     (hipStream_t)stream, *a, (const int32_t*)(ws + l.desc), (const float*)(ws + l.out),
-                     (const float*)(ws + l.lse));
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  if (narrow)
+    hipLaunchKernelGGL(pa_fp8_segment_merge_kernel<16>, grid, dim3(256), 0, (hipStream_t)stream, *a,
+                       (const int32_t*)(ws + l.desc), (const float*)(ws + l.out), (const float*)(ws + l.lse));
+  else
+    hipLaunchKernelGGL(pa_fp8_segment_merge_kernel<4>, grid, dim3(256), 0, (hipStream_t)stream, *a,
+                       (const int32_t*)(ws + l.desc), (const float*)(ws + l.out), (const float*)(ws + l.lse));
   hipError_t err = hipGetLastError();
   return err == hipSuccess ? PA_OK : (int)err;
 }
