@@ -332,6 +332,68 @@ def test_owner_launch_without_partials_writes_only_output():
     assert_parity(call._keep[0], ref, "owner, output only")
 
 
+OWNER_PAIR_CASES = {
+    # 768 (sequence, kv head) pairs, three per CU; empty sequences
+    "pairs3_empty": dict(num_query_heads=32, num_kv_heads=8,
+                         ctx=[0 if i % 7 == 3 else 1 + (37 * i) % 400 for i in range(96)]),
+    # 2400 pairs, several dispatch rounds; per-token scales
+    "pairs8_pt": dict(batch=300, num_query_heads=8, num_kv_heads=8, ctx_range=(1, 120), per_token=True),
+    # 64-token pages under a window
+    "pairs2_page64_window": dict(batch=70, num_query_heads=16, num_kv_heads=8, ctx_range=(1, 900), block_size=64,
+                                 sliding_window=200),
+    # two causal queries per sequence (four columns)
+    "pairs5_ql2": dict(batch=150, query_length=2, num_query_heads=16, num_kv_heads=8, ctx_range=(2, 500)),
+}
+
+
+@pytest.mark.parametrize("name", sorted(OWNER_PAIR_CASES))
+def test_fused_owner_many_pairs(name):
+    """Fused owner calls (no partial buffers) with more (sequence, kv head)
+    pairs than CUs, so several workgroups share a CU or run in later rounds.
+    Empty sequences give zero rows."""
+    spec = OWNER_PAIR_CASES[name]
+    case = make_case(seed=len(name), **spec)
+    ctx = case["context_lengths"]
+    ref = torch_oracle(dict(case, context_lengths=ctx.clamp(min=1)), float_out=False)
+    ql = case["query_length"]
+    for b in torch.nonzero(ctx == 0).flatten().tolist():
+        ref[b * ql:(b + 1) * ql] = 0
+    out, route, _ = launch(to_dev(case), sched="owner")
+    assert route == ("ps_sw_partitioned" if case["sliding_window"] else "ps_small_block")
+    assert_parity(out, ref, f"owner pairs/{name}")
+
+
+def test_fused_owner_graph_replays():
+    """A captured fused owner launch replays bit for bit."""
+    case = to_dev(make_case(batch=80, num_query_heads=32, num_kv_heads=8, ctx_range=(1, 700), seed=83))
+    out = torch.empty(case["query"].shape, dtype=torch.bfloat16, device=DEV)
+    s = torch.cuda.Stream()
+    with schedule("owner"):
+        call = prepare_pa_decode(out, case["query"], case["key_cache"], case["value_cache"], case["context_lengths"],
+                                 None, None, case["softmax_scale"], case["key_scale"], case["value_scale"],
+                                 block_tables=case["block_tables"], max_context_partition_num=8, stream=s)
+    assert call._ra is None and call._pa.exp_sums is None
+    with torch.cuda.stream(s):
+        call.launch()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            call.launch()
+    torch.cuda.synchronize()
+    for i in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        with torch.cuda.stream(s):
+            call.launch()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"eager after replay {i}"
+
+
 @pytest.mark.parametrize("sched", ["owner", "slot"])
 def test_graph_capture_every_schedule(sched):
     case = to_dev(make_case(batch=5, ctx_range=(1, 2500), seed=81, per_token=True))
