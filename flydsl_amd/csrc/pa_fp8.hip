@@ -475,8 +475,8 @@ __device__ __forceinline__ void compute_chunk(WaveState<NCG>& s, const QueryTile
 // pointers so that their wave-uniform loads become scalar (SMEM) loads:
 // page lookups then count on lgkmcnt and never force a wait on the vmcnt
 // of the direct-to-LDS data loads in flight.
-template <int NCG, bool PER_TOKEN, bool BS16, int STAGES, bool MULTI>
-__global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8_partition_args a,
+template <int NCG, bool PER_TOKEN, bool BS16, int STAGES, bool MULTI, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void pa_fp8_partition_kernel(const pa_fp8_partition_args a,
                                                                     const int32_t* __restrict__ block_tables,
                                                                     const int32_t* __restrict__ kv_indptr,
                                                                     const int32_t* __restrict__ context_lengths,
@@ -484,8 +484,9 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
                                                                     const float* __restrict__ value_scale) {
   constexpr int kStageBytes = kKBytes + kVBytes + (PER_TOKEN ? kScaleBytes : 0);
   constexpr int kWaveBytes = STAGES * kStageBytes;
-  constexpr int kMergeBytes = 2 * kWaves * 16 * 4 + kWaves * kHead * 16 * 4;
-  constexpr int kSmemBytes = kWaves * kWaveBytes > kMergeBytes ? kWaves * kWaveBytes : kMergeBytes;
+  constexpr int kNT = 64 * WAVES;
+  constexpr int kMergeBytes = 2 * WAVES * 16 * 4 + WAVES * kHead * 16 * 4;
+  constexpr int kSmemBytes = WAVES * kWaveBytes > kMergeBytes ? WAVES * kWaveBytes : kMergeBytes;
   __shared__ __attribute__((aligned(16))) unsigned char smem[kSmemBytes];
 
   const int tid = threadIdx.x;
@@ -507,8 +508,8 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
   const bool owner = PG == 1;
   const bool direct_out = owner && a.output != nullptr;
   const bool want_partials = a.exp_sums != nullptr;
-  const int wslot = nslots >= kWaves ? 1 : kWaves / nslots;
-  const int groups = kWaves / wslot;
+  const int wslot = nslots >= WAVES ? 1 : WAVES / nslots;
+  const int groups = WAVES / wslot;
   const int gid = wave / wslot;
   const int rank = wave - gid * wslot;
 
@@ -553,14 +554,14 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
     pa_plan_slot_tokens(ctx, P, zs, W, ql, &t0, &t1);
     if (!(pa_min(t1, hi_all) > pa_max(t0, lo_all) && has_pages)) {
       const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      for (int idx = tid; idx < eq * (kHead / 8); idx += kThreads) {
+      for (int idx = tid; idx < eq * (kHead / 8); idx += kNT) {
         const int e = idx / (kHead / 8);
         const int d0 = (idx % (kHead / 8)) * 8;
         if (want_partials) store_partial8(a, b, h, zs, e, d0, z);
         if (direct_out) store_output8(a, b, h, e, d0, z);
       }
       if (want_partials)
-        for (int e = tid; e < eq; e += kThreads) store_stats(a, b, h, zs, e, 0.0f, kNegInf);
+        for (int e = tid; e < eq; e += kNT) store_stats(a, b, h, zs, e, 0.0f, kNegInf);
       return;
     }
   }
@@ -780,8 +781,8 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
   // for a workgroup that covers every slot, all waves into the output.
   const float vfin_end = PER_TOKEN ? st.vsmax : v_tensor_scale;
   float* mbuf = (float*)smem;             // [wave][16]
-  float* lbuf = mbuf + kWaves * 16;       // [wave][16]
-  float* abuf = lbuf + kWaves * 16;       // [wave][head dim][16]
+  float* lbuf = mbuf + WAVES * 16;        // [wave][16]
+  float* abuf = lbuf + WAVES * 16;        // [wave][head dim][16]
   const int ngp = (!MULTI && want_partials) ? pa_min(groups, nslots) : 0;
   const int nsets = ngp + (direct_out ? 1 : 0);
 #pragma unroll
@@ -807,14 +808,14 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_partition_kernel(const pa_fp8
       for (int i = 0; i < 4; ++i)
         abuf[(wave * kHead + 16 * j + 4 * grp + i) * 16 + c16] = (MULTI ? accC[cg][j][i] : st.acc[cg][j][i]) * sc;
     __syncthreads();
-    for (int idx = tid; idx < nsets * 256; idx += kThreads) {
+    for (int idx = tid; idx < nsets * 256; idx += kNT) {
       const int set = idx >> 8;
       const int col = (idx >> 4) & 15;
       const int d0 = (idx & 15) * 8;
       const int e = cg * 16 + col;
       if (e >= eq) continue;
       const int w0 = set < ngp ? set * wslot : 0;
-      const int w1 = set < ngp ? w0 + wslot : kWaves;
+      const int w1 = set < ngp ? w0 + wslot : WAVES;
       float Mc = kNegInf;
       for (int w = w0; w < w1; ++w) Mc = fmaxf(Mc, mbuf[w * 16 + col]);
       const float Mcu = Mc == kNegInf ? 0.0f : Mc;
@@ -1777,22 +1778,34 @@ __global__ __launch_bounds__(256) void pa_fp8_lse_reduce_kernel(const pa_fp8_red
   }
 }
 
-template <int NCG, bool PT, bool BS16, bool MULTI>
+template <int NCG, bool PT, bool BS16, bool MULTI, int WAVES>
 hipError_t launch_partition(const pa_fp8_partition_args& a, unsigned grid, hipStream_t s) {
-  hipLaunchKernelGGL((pa_fp8_partition_kernel<NCG, PT, BS16, kStages, MULTI>), dim3(grid), dim3(kThreads), 0, s, a,
-                     a.block_tables, a.kv_indptr, a.context_lengths, a.key_scale, a.value_scale);
+  hipLaunchKernelGGL((pa_fp8_partition_kernel<NCG, PT, BS16, kStages, MULTI, WAVES>), dim3(grid), dim3(64 * WAVES), 0,
+                     s, a, a.block_tables, a.kv_indptr, a.context_lengths, a.key_scale, a.value_scale);
   return hipGetLastError();
 }
 
-template <int NCG, bool MULTI>
+template <int NCG, bool MULTI, int WAVES = kWaves>
 hipError_t dispatch_ncg(const pa_fp8_partition_args& a, unsigned grid, hipStream_t s) {
   const bool pt = a.per_token_kv != 0;
   const bool bs16 = a.block_size == 16;
   if (pt)
-    return bs16 ? launch_partition<NCG, true, true, MULTI>(a, grid, s)
-                : launch_partition<NCG, true, false, MULTI>(a, grid, s);
-  return bs16 ? launch_partition<NCG, false, true, MULTI>(a, grid, s)
-              : launch_partition<NCG, false, false, MULTI>(a, grid, s);
+    return bs16 ? launch_partition<NCG, true, true, MULTI, WAVES>(a, grid, s)
+                : launch_partition<NCG, true, false, MULTI, WAVES>(a, grid, s);
+  return bs16 ? launch_partition<NCG, false, true, MULTI, WAVES>(a, grid, s)
+              : launch_partition<NCG, false, false, MULTI, WAVES>(a, grid, s);
+}
+
+// Compute units of the current device (cached per device; -1 if unknown).
+int device_cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  static int cache[64];
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return -1;
+  if (dev >= 0 && dev < 64) cache[dev] = n;
+  return n;
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -1966,14 +1979,22 @@ int pa_fp8_decode_partition(const pa_fp8_partition_args* a, void* stream) {
   const int64_t grid = (int64_t)a->num_seqs * a->num_kv_heads * pa_cdiv(a->num_partitions, spw);
   if (grid == 0) return PA_OK;
   if (grid > 0x7fffffffLL) return PA_ERR_SHAPE;
+  const int ncg = (eq + 15) / 16;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t err;
+  // A launch of at most one workgroup per CU runs 8-wave workgroups (one
+  // per CU by LDS): twice the loads in flight per CU of a 4-wave one.
+  const int cus = ncg == 1 ? device_cu_count() : -1;
+  if (cus > 0 && grid <= cus) {
+    const bool multi8 = pa_min(spw, a->num_partitions) > 8;
+    err = multi8 ? dispatch_ncg<1, true, 8>(*a, (unsigned)grid, s) : dispatch_ncg<1, false, 8>(*a, (unsigned)grid, s);
+    return err == hipSuccess ? PA_OK : (int)err;
+  }
   // A wave owns several slots only when a workgroup covers more slots than
   // it has waves; that form keeps a second accumulator set, built for one
   // 16-column group only.
   const bool multi = pa_min(spw, a->num_partitions) > kWaves;
-  const int ncg = (eq + 15) / 16;
   if (multi && ncg > 1) return PA_ERR_GROUP;
-  hipStream_t s = (hipStream_t)stream;
-  hipError_t err;
   if (multi) {
     err = dispatch_ncg<1, true>(*a, (unsigned)grid, s);
   } else {

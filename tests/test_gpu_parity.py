@@ -157,6 +157,26 @@ def test_any_partition_count(P, sched):
     assert_parity(out, ref, f"P={P}/{sched}")
 
 
+FOUR_WAVE_VARIANTS = {
+    "plain": dict(),
+    "per_token": dict(per_token=True),
+    "window": dict(sliding_window=150),
+    "page64": dict(block_size=64),
+}
+
+
+@pytest.mark.parametrize("sched", ["owner", "slot", "wave_slot"])
+@pytest.mark.parametrize("variant", sorted(FOUR_WAVE_VARIANTS))
+def test_grids_beyond_one_workgroup_per_cu(variant, sched):
+    """260+ workgroups (more than one per CU) keep two 4-wave workgroups per
+    CU; the small cases above launch at most one workgroup per CU and so run
+    8-wave workgroups."""
+    case = make_case(batch=130, ctx_range=(1, 600), seed=47 + len(variant), **FOUR_WAVE_VARIANTS[variant])
+    ref = torch_oracle(case, float_out=False)
+    out, _, _ = launch(to_dev(case), P=8, sched=sched)
+    assert_parity(out, ref, f"4-wave {variant}/{sched}")
+
+
 @pytest.mark.parametrize("window", [2, 100, 700])
 def test_window_fused_and_partitioned(window):
     case = make_case(batch=5, ctx=[1, 60, 255, 900, 2500], sliding_window=window, seed=21 + window)
