@@ -13,8 +13,13 @@ caller does not ask for the slot partials and the contexts may be long or
 ragged, every wave of the GPU takes an equal run of the batch's chunks
 (balanced stream split, a decode launch plus a merge launch).  Otherwise
 workgroups take one or a few slots each and the reduce kernel merges them.
-The slot partials the reference defines are written whenever the caller
-passes the buffers for them.
+
+``exp_sums`` / ``max_logits`` / ``temporary_output`` are workspace, as in
+the reference (preallocated so that graph capture allocates nothing,
+:2898-2902, :3030-3034): the slot routes write the reference's slot
+partials into them and the reduce reads them back; an owner launch, which
+merges in LDS, leaves them untouched.  (The C ABI still writes them from an
+owner launch when its arguments carry them.)
 
 Routes (same dispatch order as the reference, :2883 / :3010 / :3123):
   * ``sliding_window > 0``    -> window partition pass + LSE reduce
@@ -485,7 +490,11 @@ def prepare_pa_decode(
         keep = (output, query, key_cache, value_cache, context_lengths, block_tables, kv_page_indices, kv_indptr,
                 key_scale, value_scale, ws)
         return PreparedDecode(route_name, s, keep, stream_args=sa, workspace=ws)
-    fused = owner and not user_partials
+    # An owner launch needs no slot partials; caller buffers stay unused
+    # (validated all the same, as the slot routes validate them).
+    if exp_sums is not None and max_logits is not None and temporary_output is not None:
+        _check_partials(exp_sums, max_logits, temporary_output, (batch_size, num_kv_heads, P, eqgs), head_size)
+    fused = owner
     if fused and route != "sw":
         # Nobody observes the slot partials: let each of the workgroup's
         # waves stream one contiguous quarter of the context.  (The window

@@ -100,6 +100,37 @@ def _launch(case, *, P, out_dtype, tmp_dtype, flat, partials):
     return out, route, (es, ml, to)
 
 
+def launch_owner_with_partials(case, P, tmp_dtype=torch.float32):
+    """Owner launch (one workgroup per (sequence, kv head) merging in LDS)
+    whose C-ABI arguments carry the slot-partial buffers: the library then
+    writes them as well.  The Python launcher treats caller partial buffers
+    as workspace and leaves them out of owner launches, so this prepares the
+    owner call and fills the partial fields of its arguments."""
+    q = case["query"]
+    b = case["context_lengths"].shape[0]
+    hkv = case["key_cache"].shape[1]
+    eq = case["query_length"] * (q.shape[1] // hkv)
+    out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+    es = torch.full((b, hkv, P, eq), 7.0, device=q.device)
+    ml = torch.full((b, hkv, P, eq), 7.0, device=q.device)
+    to = torch.full((b, hkv, P, eq, 128), 7.0, device=q.device, dtype=tmp_dtype)
+    with schedule("owner"):
+        call = prepare_pa_decode(out, q, case["key_cache"], case["value_cache"], case["context_lengths"], None, None,
+                                 case["softmax_scale"], case["key_scale"], case["value_scale"],
+                                 sliding_window=case["sliding_window"], block_tables=case["block_tables"],
+                                 max_context_partition_num=P)
+    pa = call._pa
+    assert call._ra is None and pa.output is not None and pa.exp_sums is None
+    pa.num_partitions = pa.slots_per_workgroup = P
+    pa.exp_sums, pa.max_logits, pa.tmp_out = es.data_ptr(), ml.data_ptr(), to.data_ptr()
+    pa.stride_es_seq, pa.stride_es_head, pa.stride_es_part = es.stride()[:3]
+    pa.stride_to_seq, pa.stride_to_head, pa.stride_to_part, pa.stride_to_group = to.stride()[:4]
+    pa.tmp_dtype = _lib.DTYPE_F32 if tmp_dtype == torch.float32 else _lib.DTYPE_BF16
+    call.launch()
+    torch.cuda.synchronize()
+    return out, (es, ml, to)
+
+
 def assert_parity(out, ref, what=""):
     out = out.float().cpu()
     ref = ref.float().cpu()
@@ -221,7 +252,10 @@ def test_slot_partials_match_oracle(window, ql, sched):
                      sliding_window=window, per_token=True, seed=51 + ql)
     P = plan.sw_partition_count(window, query_length=ql) if window else 6
     es_r, ml_r, to_r = slot_partials(case, P)
-    _, _, (es, ml, to) = launch(to_dev(case), P=P, partials=True, tmp_dtype=torch.float32, sched=sched)
+    if sched == "owner":
+        _, (es, ml, to) = launch_owner_with_partials(to_dev(case), P)
+    else:
+        _, _, (es, ml, to) = launch(to_dev(case), P=P, partials=True, tmp_dtype=torch.float32, sched=sched)
     es, ml, to = es.cpu().double(), ml.cpu().double(), to.cpu().double()
     empty = torch.isinf(ml_r)
     assert torch.equal(torch.isinf(ml), empty), "non-empty slot set differs"
@@ -321,14 +355,19 @@ def test_benchmark_config_full_size(name):
 @pytest.mark.parametrize("P", [4, 6, 9])
 def test_owner_launch_matches_two_pass_reduce(P):
     """One launch that merges in LDS (owner workgroups) == partition pass
-    with one slot per workgroup + pa_fp8_decode_reduce; same partials."""
+    with one slot per workgroup + pa_fp8_decode_reduce; same partials (the
+    owner launch writes them when its C-ABI arguments carry them), and the
+    Python launcher's owner launch leaves caller buffers untouched."""
     case = to_dev(make_case(batch=6, ctx_range=(1, 3000), per_token=P != 9, query_length=2 if P != 9 else 1,
                             num_query_heads=16 if P != 9 else 8, num_kv_heads=4 if P != 9 else 2, seed=71 + P))
     ref = torch_oracle({k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in case.items()},
                        float_out=False)
-    out1, _, (es1, ml1, to1) = launch(case, P=P, partials=True, sched="owner", tmp_dtype=torch.float32)
+    out1, (es1, ml1, to1) = launch_owner_with_partials(case, P)
     out2, _, (es2, ml2, to2) = launch(case, P=P, partials=True, sched="slot", tmp_dtype=torch.float32)
+    out3, _, (es3, ml3, to3) = launch(case, P=P, partials=True, sched="owner", tmp_dtype=torch.float32)
     assert_parity(out1, ref, f"owner P={P}")
+    assert_parity(out3, ref, f"owner via launcher P={P}")
+    assert bool((es3 == 7.0).all()) and bool((ml3 == 7.0).all()) and bool((to3 == 7.0).all())
     assert_parity(out2, ref, f"slot+reduce P={P}")
     assert torch.equal(torch.isinf(ml1), torch.isinf(ml2))
     fin = ~torch.isinf(ml1)

@@ -58,13 +58,19 @@ def test_owner_mode_for_large_uniform_batch():
     assert call._pa.exp_sums is None  # caller passed no partial buffers
 
 
-def test_owner_mode_still_writes_requested_partials():
+def test_owner_mode_leaves_caller_workspace_unused():
+    """Caller partial buffers are workspace (the reference preallocates them
+    for graph capture); an owner launch merges in LDS and needs none."""
     cfg = workloads.DecodeConfig("x", 64, 1, 32, 8, 16, "fixed:64", False)
     case = workloads.build_inputs(cfg, device="cpu", seed=0, context_lengths=[4096] * 64)
     es = torch.empty(64, 8, 8, 4)
     call = prep(case, max_context_partition_num=8, exp_sums=es, max_logits=torch.empty_like(es),
                 temporary_output=torch.empty(64, 8, 8, 4, 128, dtype=torch.bfloat16))
-    assert call._ra is None and call._pa.exp_sums == es.data_ptr()
+    assert call._ra is None and call._pa.exp_sums is None and call._pa.output is not None
+    # ... but they are validated as on the slot routes
+    with pytest.raises(ValueError, match="exp_sums/max_logits must have shape"):
+        prep(case, max_context_partition_num=8, exp_sums=es[:, :4], max_logits=torch.empty_like(es[:, :4]),
+             temporary_output=torch.empty(64, 8, 8, 4, 128, dtype=torch.bfloat16))
 
 
 def test_schedule_policy():
