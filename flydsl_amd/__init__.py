@@ -1,9 +1,12 @@
 """MI355X-native FP8 paged-attention decode (drop-in for FlyDSL's pa_decode_ps_launch).
 
-Public API (same names and signatures as kernels/pa_decode_fp8.py of the
-reference): :func:`pa_decode_ps_launch`, :func:`get_recommended_splits`,
-:func:`get_pa_metadata`.  Device work runs in the hand-written gfx950 HIP
-kernels of ``libpa_fp8.so`` (C ABI: ``include/pa_fp8.h``).
+Public API (same names and signatures as the reference):
+  * kernels/pa_decode_fp8.py: :func:`pa_decode_ps_launch`,
+    :func:`get_recommended_splits`, :func:`get_pa_metadata`;
+  * kernels/fused_rope_cache_kernel.py: :func:`build_fused_rope_cache_module`
+    (the KV-cache writer that produces the cache the decode reads).
+Device work runs in the hand-written gfx950 HIP kernels of ``libpa_fp8.so``
+(C ABI: ``include/pa_fp8.h``).
 """
 
 from .pa_decode import (  # noqa: F401
@@ -14,6 +17,7 @@ from .pa_decode import (  # noqa: F401
     pa_decode_ps_launch,
     prepare_pa_decode,
 )
+from .rope_cache import build_fused_rope_cache_module  # noqa: F401
 
 __all__ = [
     "pa_decode_ps_launch",
@@ -22,4 +26,5 @@ __all__ = [
     "prepare_pa_decode",
     "PreparedDecode",
     "KV_COMPUTE_BLOCK",
+    "build_fused_rope_cache_module",
 ]

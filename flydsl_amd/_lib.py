@@ -19,6 +19,10 @@ DTYPE_BF16 = 0
 DTYPE_F16 = 1
 DTYPE_F32 = 2
 
+CACHE_FLASH = 0
+CACHE_ATOM = 1
+CACHE_ATOM_TRANS_V = 2
+
 ERRORS = {
     -1: "PA_ERR_NULL_ARG",
     -2: "PA_ERR_HEAD_SIZE",
@@ -46,6 +50,7 @@ EXPORTED_SYMBOLS = (
     "pa_fp8_reduce_worklist",
     "pa_fp8_worklist_sizes",
     "pa_fp8_plan_worklist",
+    "pa_fp8_rope_cache",
 )
 
 _i32 = ctypes.c_int32
@@ -212,6 +217,51 @@ class WorklistReduceArgs(ctypes.Structure):
     ]
 
 
+class RopeCacheArgs(ctypes.Structure):
+    """Mirror of ``pa_fp8_rope_cache_args``."""
+
+    _fields_ = [
+        ("abi_version", _i32),
+        ("q", _vp),
+        ("k", _vp),
+        ("v", _vp),
+        ("positions", _vp),
+        ("cos_cache", _vp),
+        ("sin_cache", _vp),
+        ("slot_mapping", _vp),
+        ("key_cache", _vp),
+        ("value_cache", _vp),
+        ("q_out", _vp),
+        ("k_out", _vp),
+        ("k_scale", _vp),
+        ("v_scale", _vp),
+        ("stride_q_tok", _i64),
+        ("stride_q_head", _i64),
+        ("stride_k_tok", _i64),
+        ("stride_k_head", _i64),
+        ("stride_v_tok", _i64),
+        ("stride_v_head", _i64),
+        ("stride_qo_tok", _i64),
+        ("stride_qo_head", _i64),
+        ("stride_ko_tok", _i64),
+        ("stride_ko_head", _i64),
+        ("stride_cos_pos", _i64),
+        ("stride_sin_pos", _i64),
+        ("num_tokens", _i32),
+        ("num_q_heads", _i32),
+        ("num_kv_heads", _i32),
+        ("head_dim", _i32),
+        ("block_size", _i32),
+        ("num_blocks", _i32),
+        ("max_pos", _i32),
+        ("dtype", _i32),
+        ("cache_layout", _i32),
+        ("apply_scale", _i32),
+        ("reuse_freqs_front_part", _i32),
+        ("index_i64", _i32),
+    ]
+
+
 _LIB: Optional[ctypes.CDLL] = None
 
 
@@ -260,6 +310,8 @@ def load(path: Optional[str] = None) -> ctypes.CDLL:
     lib.pa_fp8_worklist_sizes.restype = ctypes.c_int
     lib.pa_fp8_plan_worklist.argtypes = [_vp] + [ctypes.c_int] * 6 + [_vp] * 5
     lib.pa_fp8_plan_worklist.restype = ctypes.c_int
+    lib.pa_fp8_rope_cache.argtypes = [ctypes.POINTER(RopeCacheArgs), _vp]
+    lib.pa_fp8_rope_cache.restype = ctypes.c_int
     if path is None:
         _LIB = lib
     return lib

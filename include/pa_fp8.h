@@ -309,6 +309,71 @@ int pa_fp8_plan_worklist(const int32_t* context_lengths, int num_seqs, int num_k
                          int query_length, int num_cu, int kv_granularity, int32_t* work_indptr, int32_t* work_info,
                          int32_t* reduce_indptr, int32_t* reduce_final_map, int32_t* reduce_partial_map);
 
+/*
+ * KV-cache writer: NeoX RoPE on the new tokens' Q and K, K and V written into
+ * the paged cache.  Replaces the launch function built by
+ * build_fused_rope_cache_module (kernels/fused_rope_cache_kernel.py:49-512:
+ * kernel :105-412, launch :460-512), which fuses the same three steps.
+ *
+ *   q, q_out          [T, QH, D]  bf16 or f16 (token / head strides)
+ *   k, v, k_out       [T, KH, D]  same dtype
+ *   positions, slot_mapping [T]   int32, or int64 read as their low words
+ *                                 (index_i64 = 1); slot < 0 skips the cache
+ *   cos_cache, sin_cache [max_pos, D / 2] (reuse_freqs_front_part = 1) or
+ *                        [max_pos, D], same dtype as q (row strides)
+ *   key_cache, value_cache, contiguous, by cache_layout:
+ *     PA_CACHE_FLASH         K, V [NB, bs, KH, D]
+ *     PA_CACHE_ATOM          K [NB, KH, D / 16, bs, 16], V [NB, KH, D, bs]
+ *     PA_CACHE_ATOM_TRANS_V  K as ATOM, V [NB, KH, bs / 16, D, 16] (the
+ *                            layout the decode kernels read fastest; no
+ *                            counterpart in the reference writer)
+ *     element: the input dtype, or fp8 e4m3fn when apply_scale = 1 (value *
+ *     1 / k_scale[0] or 1 / v_scale[0], saturated at +-448)
+ * D in {16, 32, 64, 128, 256}.
+ */
+enum pa_fp8_cache_layout {
+  PA_CACHE_FLASH = 0,
+  PA_CACHE_ATOM = 1,
+  PA_CACHE_ATOM_TRANS_V = 2,
+};
+
+typedef struct {
+  int32_t abi_version; /* = PA_FP8_ABI_VERSION */
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* positions;
+  const void* cos_cache;
+  const void* sin_cache;
+  const void* slot_mapping;
+  void* key_cache;
+  void* value_cache;
+  void* q_out;
+  void* k_out;
+  const float* k_scale;
+  const float* v_scale;
+  int64_t stride_q_tok, stride_q_head;
+  int64_t stride_k_tok, stride_k_head;
+  int64_t stride_v_tok, stride_v_head;
+  int64_t stride_qo_tok, stride_qo_head;
+  int64_t stride_ko_tok, stride_ko_head;
+  int64_t stride_cos_pos, stride_sin_pos;
+  int32_t num_tokens;
+  int32_t num_q_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t block_size;
+  int32_t num_blocks;  /* slots past the cache are not written */
+  int32_t max_pos;     /* rows of cos/sin; positions are clamped into them */
+  int32_t dtype;       /* PA_DTYPE_BF16 / PA_DTYPE_F16 */
+  int32_t cache_layout;
+  int32_t apply_scale;
+  int32_t reuse_freqs_front_part;
+  int32_t index_i64;
+} pa_fp8_rope_cache_args;
+
+int pa_fp8_rope_cache(const pa_fp8_rope_cache_args* args, void* hip_stream);
+
 /* Library identification and error names. */
 const char* pa_fp8_version(void);
 const char* pa_fp8_error_string(int code);

@@ -53,6 +53,17 @@ def test_null_args_rejected_without_gpu():
     sa = _lib.StreamArgs()
     sa.abi_version = 99
     assert lib.pa_fp8_decode_balanced(ctypes.byref(sa), None, 0, None) == -8
+    assert lib.pa_fp8_rope_cache(None, None) == -1
+    ra = _lib.RopeCacheArgs()
+    ra.abi_version = 99
+    assert lib.pa_fp8_rope_cache(ctypes.byref(ra), None) == -8
+    ra.abi_version = _lib.ABI_VERSION
+    ra.head_dim, ra.block_size, ra.max_pos, ra.num_tokens, ra.num_q_heads = 96, 16, 8, 1, 1
+    assert lib.pa_fp8_rope_cache(ctypes.byref(ra), None) == -2  # 12 lanes per row do not tile a wave
+    ra.head_dim = 128
+    assert lib.pa_fp8_rope_cache(ctypes.byref(ra), None) == -1  # no tensors
+    ra.num_tokens = 0
+    assert lib.pa_fp8_rope_cache(ctypes.byref(ra), None) == 0  # nothing to do
 
 
 def test_stream_worker_counts():
@@ -72,7 +83,8 @@ def test_stream_worker_counts():
 @pytest.mark.parametrize("struct,cname", [(_lib.PartitionArgs, "pa_fp8_partition_args"),
                                           (_lib.ReduceArgs, "pa_fp8_reduce_args"),
                                           (_lib.StreamArgs, "pa_fp8_stream_args"),
-                                          (_lib.WorklistReduceArgs, "pa_fp8_worklist_reduce_args")])
+                                          (_lib.WorklistReduceArgs, "pa_fp8_worklist_reduce_args"),
+                                          (_lib.RopeCacheArgs, "pa_fp8_rope_cache_args")])
 def test_struct_layout_matches_header(tmp_path, struct, cname):
     fields = [f for f, _ in struct._fields_]
     src = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){",
