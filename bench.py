@@ -50,7 +50,9 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=100)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--config", default="c2_llama8b", help="c1_tiny|c2_llama8b|c3_ragged|c4_window|c5_mtp|all")
+    p.add_argument("--config", default="c2_llama8b",
+                   help="c1_tiny|c2_llama8b|c3_ragged|c4_window|c5_mtp|all (decode), "
+                        "rope_decode_llama8b|rope_prefill_llama8b (KV-cache writer)")
     p.add_argument("--seed", type=int, default=7)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
@@ -295,6 +297,129 @@ def run_config(name: str, args) -> dict:
     return line
 
 
+def rope_cpu_baseline(case_gpu, cfg, budget_s: float) -> dict:
+    """Time the writer's CPU oracle over growing samples of the workload's
+    tokens until the budget is spent; scaled to GB/s of algorithmic bytes."""
+    import torch
+
+    from flydsl_amd import workloads
+    from oracle import rope_cache as rc
+
+    per_tok = workloads.rope_bytes(cfg) / cfg.num_tokens
+    c = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in case_gpu.items()}
+    kc = c["key_cache"].view(torch.uint8)
+    vc = c["value_cache"].view(torch.uint8)
+    done, spent, n = 0, 0.0, 8
+    while spent < budget_s and done < cfg.num_tokens:
+        m = min(n, cfg.num_tokens - done)
+        sl = slice(done, done + m)
+        t0 = time.perf_counter()
+        rc.rope_cache_ref(c["q"][sl], c["k"][sl], c["v"][sl], c["positions"][sl], c["cos"], c["sin"],
+                          c["slot_mapping"][sl], kc, vc, block_size=cfg.block_size, layout=rc.ATOM_TRANS_V,
+                          apply_scale=True, k_scale=float(c["k_scale"][0]), v_scale=float(c["v_scale"][0]),
+                          inplace=True)
+        spent += time.perf_counter() - t0
+        done += m
+        n *= 2
+    return {
+        "value": round(done * per_tok / spent / 1e9, 4),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{done} of {cfg.num_tokens} tokens of {cfg.name} through the torch oracle "
+        f"(oracle/rope_cache.py rope_cache_ref, caches written in place), {spent:.1f} s; "
+        f"host {cpu_model()}, affinity {len(os.sched_getaffinity(0))} cpus, os.cpu_count {os.cpu_count()}",
+    }
+
+
+def run_rope_config(name: str, args) -> dict:
+    """One KV-cache writer call per step (prepared, as a serving loop makes
+    it); inputs rotate over copies so no step reads what the last one left
+    in the Infinity Cache."""
+    import torch
+
+    from flydsl_amd import build_fused_rope_cache_module, workloads
+
+    cfg = workloads.ROPE_CONFIGS[name]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    case = workloads.build_rope_inputs(cfg, device=dev, seed=args.seed)
+    algo = workloads.rope_bytes(cfg)
+    in_bytes = sum(case[k].numel() * case[k].element_size() for k in ("q", "k", "v"))
+    if args.copies:
+        copies = args.copies
+    elif in_bytes > 64 << 20:
+        copies = max(2, math.ceil(2 * MALL_BYTES / in_bytes) + 1)
+    else:
+        copies = 1  # a decode batch's few MB stay cache-resident whatever the rotation
+    ins = [(case["q"], case["k"], case["v"])]
+    for _ in range(copies - 1):
+        ins.append(tuple(t.clone() for t in ins[0]))
+    q_out = torch.empty_like(case["q"])
+    k_out = torch.empty_like(case["k"])
+    launch = build_fused_rope_cache_module(head_dim=cfg.head_size, num_q_heads=cfg.num_q_heads,
+                                           num_kv_heads=cfg.num_kv_heads, block_size=cfg.block_size,
+                                           flash_layout=False, dtype_str="bf16", apply_scale=True)
+    calls = [launch.prepare(q, k, v, case["positions"], case["cos"], case["sin"], case["slot_mapping"],
+                            case["key_cache"], case["value_cache"], q_out, k_out, cfg.num_tokens, case["k_scale"],
+                            case["v_scale"]) for q, k, v in ins]
+    for i in range(max(3, args.warmup)):
+        calls[i % copies].launch()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(args.steps):
+        calls[i % copies].launch()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    value = algo / (ms * 1e-3) / 1e9
+    line = {
+        "metric": "KV-cache writer HBM GB/s (% of peak) + us/call, NeoX RoPE + fp8 paged K/V write",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_step": round(ms * 1e3, 2),
+        "pct_of_peak": round(100.0 * value / PEAK_HBM_GBPS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 Q/K/V, 10000-base rotary tables, permuted cache pages)",
+        "config": {
+            "workload": name,
+            "num_tokens": cfg.num_tokens,
+            "tokens_per_sequence": cfg.tokens_per_seq,
+            "num_query_heads": cfg.num_q_heads,
+            "num_kv_heads": cfg.num_kv_heads,
+            "head_size": cfg.head_size,
+            "block_size": cfg.block_size,
+            "cache": "fp8 e4m3fn, K [NB, KH, D/16, bs, 16], V [NB, KH, bs/16, D, 16], per-tensor scales",
+            "algorithmic_bytes_per_call": algo,
+            "input_copies_rotated": copies,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "pa_rope_cache_kernel",
+            "kernels_per_step": 1,
+            "achieved": round(value, 2),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(value / PEAK_HBM_GBPS, 4),
+            "traffic": load_traffic(name),
+            "kernel_us": round(ms * 1e3, 2),
+            "algorithmic_bytes": algo,
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = rope_cpu_baseline(case, cfg, args.cpu_seconds)
+    return line
+
+
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -306,7 +431,7 @@ def main():
         return
     names = ["c2_llama8b", "c3_ragged", "c4_window", "c5_mtp"] if args.config == "all" else [args.config]
     for n in names:
-        line = run_config(n, args)
+        line = run_rope_config(n, args) if n.startswith("rope_") else run_config(n, args)
         print(json.dumps(line), flush=True)
 
 

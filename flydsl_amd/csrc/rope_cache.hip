@@ -6,12 +6,11 @@
 //
 // Work decomposition.  A head row (one token, one Q or K head, head_dim D
 // values) is held by D/8 lanes, 8 consecutive values (16 bytes) each, so a
-// wave holds 64/(D/8) rows and a 256-thread workgroup 4x that.  Rows
-// 0 .. QH-1 of a token are its Q heads, rows QH .. QH+KH-1 its K heads; a
-// K row also loads the matching V head and writes both to the cache.  The
-// NeoX partner of value d (d +- D/2) sits in the lane D/16 further along the
-// row and comes over with a lane shuffle.  All global accesses are 16-byte
-// vectors except the cache layouts whose value dimension is strided.
+// wave holds 64/(D/8) rows at a time: rows of Q heads of one token, or one
+// K head's rows of consecutive tokens (which also carry the V rows and the
+// cache writes; see the kernel).  The NeoX partner of value d (d +- D/2)
+// sits in the lane D/16 further along the row and comes over with a lane
+// shuffle.
 //
 // Arithmetic is the reference's: in the input precision (bf16 or f16),
 // every product and the sum rounded to it (round to nearest even):
@@ -31,6 +30,8 @@ namespace {
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 
+#define LDS_AS __attribute__((address_space(3)))
+
 constexpr int kRcWaves = 4;
 constexpr int kRcThreads = 64 * kRcWaves;
 constexpr float kFp8Max = 448.0f;
@@ -43,21 +44,24 @@ __device__ __forceinline__ float h2f(uint32_t bits, bool bf) {
   return (float)h;
 }
 
-// float -> bf16 / f16 bits, round to nearest even (NaN stays NaN).
+// float -> bf16 / f16 bits, round to nearest even (NaN stays NaN); gfx950
+// converts to bf16 in hardware (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t f2h(float f, bool bf) {
-  if (bf) {
-    const uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  }
-  _Float16 h = (_Float16)f;
   uint16_t s;
-  __builtin_memcpy(&s, &h, 2);
+  if (bf) {
+    const __bf16 h = (__bf16)f;
+    __builtin_memcpy(&s, &h, 2);
+  } else {
+    const _Float16 h = (_Float16)f;
+    __builtin_memcpy(&s, &h, 2);
+  }
   return s;
 }
 
 // Round a float to the input precision and back.
-__device__ __forceinline__ float rnd(float f, bool bf) { return h2f(f2h(f, bf), bf); }
+__device__ __forceinline__ float rnd(float f, bool bf) {
+  return bf ? (float)(__bf16)f : (float)(_Float16)f;
+}
 
 // Saturate at the e4m3fn range; NaN stays NaN.
 __device__ __forceinline__ float sat_e4m3(float x) { return x > kFp8Max ? kFp8Max : (x < -kFp8Max ? -kFp8Max : x); }
@@ -74,52 +78,17 @@ __device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float 
 }
 
 // Low 32 bits of element t of an int32 or int64 index tensor (the reference
-// reads int64 positions and slots as their low words).
+// reads int64 positions and slots as their low words).  t is wave-uniform:
+// read through the constant address space, a scalar load.
 __device__ __forceinline__ int load_index(const void* p, int64_t t, bool i64) {
-  return i64 ? ((const int32_t*)p)[2 * t] : ((const int32_t*)p)[t];
+  const __attribute__((address_space(4))) int32_t* c = (const __attribute__((address_space(4))) int32_t*)p;
+  return i64 ? c[2 * t] : c[t];
 }
 
-template <bool BF16, int LAYOUT, bool SCALE>
-__global__ __launch_bounds__(kRcThreads) void pa_rope_cache_kernel(const pa_fp8_rope_cache_args a) {
-  const int D = a.head_dim;
-  const int lpr = D >> 3;                 // lanes per head row
-  const int rpw = 64 / lpr;               // head rows per wave
-  const int half = lpr >> 1;              // lanes per half row
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int rw = lane / lpr;              // row within the wave
-  const int l = lane - rw * lpr;          // lane within the row
-  const int rows = a.num_q_heads + a.num_kv_heads;
-  const int wg_per_token = (rows + rpw * kRcWaves - 1) / (rpw * kRcWaves);
-  const int64_t t = blockIdx.x / wg_per_token;
-  const int row = (int)(blockIdx.x - t * wg_per_token) * rpw * kRcWaves + wave * rpw + rw;
-  const bool live = rw < rpw && row < rows && t < a.num_tokens;
-  const bool is_q = row < a.num_q_heads;
-  const int kh = row - a.num_q_heads;
-
-  // this lane's 8 values of the row (dims 8l .. 8l+7)
-  i32x4 x = {0, 0, 0, 0};
-  if (live) {
-    const uint16_t* src = is_q ? (const uint16_t*)a.q + t * a.stride_q_tok + (int64_t)row * a.stride_q_head
-                               : (const uint16_t*)a.k + t * a.stride_k_tok + (int64_t)kh * a.stride_k_head;
-    x = *(const i32x4*)(src + 8 * l);
-  }
-  // NeoX partner values from the lane half a row away (every lane takes
-  // part in the shuffle; rows beyond the wave's last read their own lane).
-  const bool first = l < half;
-  const int partner = rw < rpw ? rw * lpr + (first ? l + half : l - half) : lane;
-  i32x4 xp;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) xp[i] = __shfl(x[i], partner, 64);
-  if (!live) return;
-
-  int pos = load_index(a.positions, t, a.index_i64 != 0);
-  pos = pos < 0 ? 0 : (pos >= a.max_pos ? a.max_pos - 1 : pos);  // never read outside the tables
-  const int cidx = a.reuse_freqs_front_part ? (8 * l) % (D >> 1) : 8 * l;
-  const i32x4 cs = *(const i32x4*)((const uint16_t*)a.cos_cache + (int64_t)pos * a.stride_cos_pos + cidx);
-  const i32x4 sn = *(const i32x4*)((const uint16_t*)a.sin_cache + (int64_t)pos * a.stride_sin_pos + cidx);
-
-  float o[8];
+// Rotated values o[0..7] of this lane's 8 dims (reference rounding).
+template <bool BF16>
+__device__ __forceinline__ void rotate8(const i32x4& x, const i32x4& xp, const i32x4& cs, const i32x4& sn, bool first,
+                                        float (&o)[8]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int sh = (i & 1) * 16;
@@ -131,70 +100,244 @@ __global__ __launch_bounds__(kRcThreads) void pa_rope_cache_kernel(const pa_fp8_
     const float ps = rnd(pv * sv, BF16);
     o[i] = rnd(first ? xc - ps : xc + ps, BF16);
   }
+}
+
+template <bool BF16>
+__device__ __forceinline__ i32x4 pack8(const float (&o)[8]) {
   i32x4 ob;
 #pragma unroll
   for (int i = 0; i < 4; ++i) ob[i] = (int)(f2h(o[2 * i], BF16) | (f2h(o[2 * i + 1], BF16) << 16));
-  uint16_t* dst = is_q ? (uint16_t*)a.q_out + t * a.stride_qo_tok + (int64_t)row * a.stride_qo_head
-                       : (uint16_t*)a.k_out + t * a.stride_ko_tok + (int64_t)kh * a.stride_ko_head;
-  *(i32x4*)(dst + 8 * l) = ob;
-  if (is_q) return;
+  return ob;
+}
 
-  // ---------------- cache write (K rows) ----------------
-  const int slot = load_index(a.slot_mapping, t, a.index_i64 != 0);
-  if (slot < 0) return;  // padding token: nothing cached
-  const int bs = a.block_size;
-  const int64_t bi = slot / bs;
-  const int bp = slot - (int)bi * bs;
-  if (bi >= a.num_blocks) return;  // outside the cache: nothing written
-  const i32x4 vv = *(const i32x4*)((const uint16_t*)a.v + t * a.stride_v_tok + (int64_t)kh * a.stride_v_head + 8 * l);
+// Tokens of one cache page sub-block that the value transpose writes whole.
+constexpr int kSub = 16;
+// LDS of a K/V workgroup: value rows [tokens][D] (2048 elements of at most
+// 2 bytes whatever D) and the tokens' slots.
+constexpr int kRcLdsElems = 2048;
+constexpr int kRcMaxGroup = 128;
+// Q wave-units per wave (four rows' loads in flight per lane).
+constexpr int kRcQUnits = 4;
+
+// Two kinds of workgroups in one launch.
+//
+// Q workgroups (blockIdx.x < nq): wave-unit u covers Q rows rs*rpw ..
+// rs*rpw + rpw - 1 of token u / ceil(QH / rpw); a wave takes kRcQUnits
+// consecutive units.  Token positions are scalar loads; the cos/sin rows
+// they select and the head rows are all issued before anything waits.
+//
+// K/V workgroups: one kv head over a group of G = 4 * rpw consecutive
+// tokens, wave w holding tokens w*rpw .. w*rpw + rpw - 1 (one per row).
+// Each row is rotated, written to K_out and to the key cache.  Value rows
+// go through LDS: a 16-token sub-block whose slots fill 16 consecutive
+// positions of one page (the prefill case) is written transposed, 8 tokens
+// of one value dim per thread, as whole 8- or 16-byte stores, instead of
+// 128 single-element stores per token into as many cache lines; other
+// tokens (decode, ragged slots) are written one by one.
+template <bool BF16, int LAYOUT, bool SCALE>
+__global__ __launch_bounds__(kRcThreads) void pa_rope_cache_kernel(const pa_fp8_rope_cache_args a) {
+  // one LDS array: value rows, then the group's slots
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kRcLdsElems * 2 + kRcMaxGroup * 4];
+  LDS_AS unsigned char* const lds_v = (LDS_AS unsigned char*)lds;
+  LDS_AS int* const lds_slot = (LDS_AS int*)(lds_v + kRcLdsElems * 2);
+
+  const int D = a.head_dim;
+  const int lpr = D >> 3;                 // lanes per head row
+  const int rpw = 64 / lpr;               // head rows per wave
+  const int half = lpr >> 1;              // lanes per half row
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rw = lane / lpr;              // row within the wave
+  const int l = lane - rw * lpr;          // lane within the row
+  const bool first = l < half;
+  const int partner = rw * lpr + (first ? l + half : l - half);
+  const int cidx = a.reuse_freqs_front_part ? (8 * l) % (D >> 1) : 8 * l;
+  const int QH = a.num_q_heads;
   const int KH = a.num_kv_heads;
-  const int d0 = 8 * l;
+  const int T = a.num_tokens;
+  const bool i64 = a.index_i64 != 0;
+  const uint32_t qwpt = (QH + rpw - 1) / rpw;  // Q wave-units per token
+  const uint32_t qunits = (uint32_t)T * qwpt;   // < 2^31 (checked at launch)
+  const uint32_t nq = (qunits + kRcWaves * kRcQUnits - 1) / (kRcWaves * kRcQUnits);
 
-  // element offsets (cache element = 1 byte fp8 or 2 bytes bf16/f16)
-  int64_t k_off, v_off, v_step;
-  if (LAYOUT == PA_CACHE_FLASH) {  // [NB, bs, KH, D] both
-    k_off = ((bi * bs + bp) * KH + kh) * D + d0;
-    v_off = k_off;
-    v_step = 1;
-  } else {
-    // K [NB, KH, D/16, bs, 16]
-    k_off = (((bi * KH + kh) * (D >> 4) + (d0 >> 4)) * bs + bp) * 16 + (d0 & 15);
-    if (LAYOUT == PA_CACHE_ATOM) {  // V [NB, KH, D, bs]
-      v_off = ((bi * KH + kh) * D + d0) * bs + bp;
-      v_step = bs;
-    } else {  // V [NB, KH, bs/16, D, 16]
-      v_off = ((bi * KH + kh) * (bs >> 4) + (bp >> 4)) * (int64_t)D * 16 + (int64_t)d0 * 16 + (bp & 15);
-      v_step = 16;
+  if (blockIdx.x < nq) {
+    // ---------------- Q rows: kRcQUnits wave-units per wave ----------------
+    // Loads are unconditional (a dead lane reads a valid row and drops it),
+    // so nothing branches between the loads and their first use.
+    i32x4 x[kRcQUnits], cs[kRcQUnits], sn[kRcQUnits];
+    uint32_t tq[kRcQUnits];
+    int rq[kRcQUnits];
+    bool lq[kRcQUnits];
+#pragma unroll
+    for (int j = 0; j < kRcQUnits; ++j) {
+      const uint32_t u = (blockIdx.x * kRcWaves + wave) * kRcQUnits + j;
+      const uint32_t t = u / qwpt;
+      const int row = (int)(u - t * qwpt) * rpw + rw;
+      tq[j] = t;
+      rq[j] = row;
+      lq[j] = u < qunits && row < QH;
+      const uint32_t tc = __builtin_amdgcn_readfirstlane(u < qunits ? t : (uint32_t)T - 1);
+      const int rc = row < QH ? row : QH - 1;
+      int p = load_index(a.positions, tc, i64);
+      p = p < 0 ? 0 : (p >= a.max_pos ? a.max_pos - 1 : p);  // never read outside the tables
+      cs[j] = *(const i32x4*)((const uint16_t*)a.cos_cache + (int64_t)p * a.stride_cos_pos + cidx);
+      sn[j] = *(const i32x4*)((const uint16_t*)a.sin_cache + (int64_t)p * a.stride_sin_pos + cidx);
+      x[j] = *(const i32x4*)((const uint16_t*)a.q + (int64_t)tc * a.stride_q_tok + (int64_t)rc * a.stride_q_head + 8 * l);
     }
+    asm volatile("" ::: "memory");  // every load above is issued before the first wait
+#pragma unroll
+    for (int j = 0; j < kRcQUnits; ++j) {
+      i32x4 xp;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xp[i] = __shfl(x[j][i], partner, 64);
+      if (!lq[j]) continue;
+      float o[8];
+      rotate8<BF16>(x[j], xp, cs[j], sn[j], first, o);
+      *(i32x4*)((uint16_t*)a.q_out + (int64_t)tq[j] * a.stride_qo_tok + (int64_t)rq[j] * a.stride_qo_head + 8 * l) =
+          pack8<BF16>(o);
+    }
+    return;
   }
 
+  // ---------------- K / V rows ----------------
+  const int G = kRcWaves * rpw;  // tokens per workgroup
+  const uint32_t b = blockIdx.x - nq;
+  const uint32_t g = b / KH;
+  const int kh = (int)(b - g * KH);
+  const int gi = wave * rpw + rw;         // token within the group
+  const int tok = (int)g * G + gi;        // this row's token
+  const bool live = tok < T;
+  const int d0 = 8 * l;
+
+  float krcp = 1.0f, vrcp = 1.0f;
   if (SCALE) {
-    const float krcp = 1.0f / a.k_scale[0];
-    const float vrcp = 1.0f / a.v_scale[0];
+    krcp = 1.0f / ((const __attribute__((address_space(4))) float*)a.k_scale)[0];
+    vrcp = 1.0f / ((const __attribute__((address_space(4))) float*)a.v_scale)[0];
+  }
+  int p = 0, slot = -1;
+  if (live) {
+    p = i64 ? ((const int32_t*)a.positions)[2 * (int64_t)tok] : ((const int32_t*)a.positions)[tok];
+    slot = i64 ? ((const int32_t*)a.slot_mapping)[2 * (int64_t)tok] : ((const int32_t*)a.slot_mapping)[tok];
+  }
+  i32x4 x = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
+  if (live) {
+    x = *(const i32x4*)((const uint16_t*)a.k + (int64_t)tok * a.stride_k_tok + (int64_t)kh * a.stride_k_head + d0);
+    vv = *(const i32x4*)((const uint16_t*)a.v + (int64_t)tok * a.stride_v_tok + (int64_t)kh * a.stride_v_head + d0);
+  }
+  asm volatile("" ::: "memory");  // row loads issued before the tables wait on the positions
+  p = p < 0 ? 0 : (p >= a.max_pos ? a.max_pos - 1 : p);
+  const i32x4 cs = *(const i32x4*)((const uint16_t*)a.cos_cache + (int64_t)p * a.stride_cos_pos + cidx);
+  const i32x4 sn = *(const i32x4*)((const uint16_t*)a.sin_cache + (int64_t)p * a.stride_sin_pos + cidx);
+  i32x4 xp;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xp[i] = __shfl(x[i], partner, 64);
+  float o[8];
+  rotate8<BF16>(x, xp, cs, sn, first, o);
+  const i32x4 ob = pack8<BF16>(o);
+  const int bs = a.block_size;
+  const int64_t bi = slot >= 0 ? slot / bs : 0;
+  const int bp = slot >= 0 ? slot - (int)bi * bs : 0;
+  const bool cached = live && slot >= 0 && bi < a.num_blocks;
+
+  // value cache elements of this lane's 8 dims when fp8
+  uint32_t v8[2] = {0, 0};
+  if (SCALE) {
     float vf[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) vf[i] = h2f(((uint32_t)vv[i >> 1] >> ((i & 1) * 16)) & 0xffffu, BF16) * vrcp;
-    const uint32_t k0 = pack4_e4m3(o[0] * krcp, o[1] * krcp, o[2] * krcp, o[3] * krcp);
-    const uint32_t k1 = pack4_e4m3(o[4] * krcp, o[5] * krcp, o[6] * krcp, o[7] * krcp);
-    *(i32x2*)((uint8_t*)a.key_cache + k_off) = i32x2{(int)k0, (int)k1};
-    const uint32_t v0 = pack4_e4m3(vf[0], vf[1], vf[2], vf[3]);
-    const uint32_t v1 = pack4_e4m3(vf[4], vf[5], vf[6], vf[7]);
+    v8[0] = pack4_e4m3(vf[0], vf[1], vf[2], vf[3]);
+    v8[1] = pack4_e4m3(vf[4], vf[5], vf[6], vf[7]);
+  }
+
+  if (live)
+    *(i32x4*)((uint16_t*)a.k_out + (int64_t)tok * a.stride_ko_tok + (int64_t)kh * a.stride_ko_head + d0) = ob;
+  if (cached) {
+    int64_t k_off;
+    if (LAYOUT == PA_CACHE_FLASH)  // [NB, bs, KH, D]
+      k_off = ((bi * bs + bp) * KH + kh) * D + d0;
+    else  // [NB, KH, D/16, bs, 16]
+      k_off = (((bi * KH + kh) * (D >> 4) + (d0 >> 4)) * bs + bp) * 16 + (d0 & 15);
+    if (SCALE) {
+      const uint32_t k0 = pack4_e4m3(o[0] * krcp, o[1] * krcp, o[2] * krcp, o[3] * krcp);
+      const uint32_t k1 = pack4_e4m3(o[4] * krcp, o[5] * krcp, o[6] * krcp, o[7] * krcp);
+      *(i32x2*)((uint8_t*)a.key_cache + k_off) = i32x2{(int)k0, (int)k1};
+    } else {
+      *(i32x4*)((uint16_t*)a.key_cache + k_off) = ob;
+    }
+    if (LAYOUT == PA_CACHE_FLASH) {  // value rows are contiguous in this layout
+      if (SCALE)
+        *(i32x2*)((uint8_t*)a.value_cache + k_off) = i32x2{(int)v8[0], (int)v8[1]};
+      else
+        *(i32x4*)((uint16_t*)a.value_cache + k_off) = vv;
+    }
+  }
+  if (LAYOUT == PA_CACHE_FLASH) return;
+
+  // value rows -> LDS [token in group][D] (element = 1 or 2 bytes), slots
+  if (SCALE)
+    *(LDS_AS i32x2*)(lds_v + gi * D + d0) = i32x2{(int)v8[0], (int)v8[1]};
+  else
+    *(LDS_AS i32x4*)(lds_v + (gi * D + d0) * 2) = vv;
+  if (l == 0) lds_slot[gi] = cached ? slot : -1;
+  __syncthreads();
+
+  // a 16-token sub-block is written whole when its slots are one page's
+  // positions bp0 .. bp0 + 15 in order (bp0 a multiple of 16)
+  auto whole = [&](int m) -> bool {
+    const int s0 = lds_slot[m * kSub];
+    if (s0 < 0 || (bs % kSub) != 0 || ((s0 % bs) % kSub) != 0) return false;
+    for (int i = 1; i < kSub; ++i)
+      if (lds_slot[m * kSub + i] != s0 + i) return false;
+    return true;
+  };
+  const int nsub = G / kSub;  // 0 when D = 256 (8 tokens per group)
+  // transposed writes: item = (sub-block m, value dim d, token half h)
+  for (int item = threadIdx.x; item < nsub * D * 2; item += kRcThreads) {
+    const int m = item / (2 * D);
+    const int d = (item >> 1) - m * D;
+    const int h = item & 1;
+    if (!whole(m)) continue;
+    const int s0 = lds_slot[m * kSub];
+    const int64_t sb = s0 / bs;
+    const int sp = s0 - (int)sb * bs + 8 * h;  // page position of the first of the 8 tokens
+    int64_t v_off;
+    if (LAYOUT == PA_CACHE_ATOM)  // [NB, KH, D, bs]
+      v_off = ((sb * KH + kh) * D + d) * bs + sp;
+    else  // [NB, KH, bs/16, D, 16]
+      v_off = ((sb * KH + kh) * (bs >> 4) + (sp >> 4)) * (int64_t)D * 16 + (int64_t)d * 16 + (sp & 15);
+    const int r0 = m * kSub + 8 * h;
+    if (SCALE) {
+      uint32_t w[2] = {0, 0};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) w[k >> 2] |= (uint32_t)lds_v[(r0 + k) * D + d] << (8 * (k & 3));
+      *(i32x2*)((uint8_t*)a.value_cache + v_off) = i32x2{(int)w[0], (int)w[1]};
+    } else {
+      uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        w[k >> 1] |= (uint32_t)((LDS_AS uint16_t*)lds_v)[(r0 + k) * D + d] << (16 * (k & 1));
+      *(i32x4*)((uint16_t*)a.value_cache + v_off) = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    }
+  }
+
+  // tokens outside whole sub-blocks: one element per value dim
+  if (!cached || (gi / kSub < nsub && whole(gi / kSub))) return;
+  int64_t v_off, v_step;
+  if (LAYOUT == PA_CACHE_ATOM) {  // [NB, KH, D, bs]
+    v_off = ((bi * KH + kh) * D + d0) * bs + bp;
+    v_step = bs;
+  } else {  // [NB, KH, bs/16, D, 16]
+    v_off = ((bi * KH + kh) * (bs >> 4) + (bp >> 4)) * (int64_t)D * 16 + (int64_t)d0 * 16 + (bp & 15);
+    v_step = 16;
+  }
+  if (SCALE) {
     uint8_t* vd = (uint8_t*)a.value_cache + v_off;
-    if (LAYOUT == PA_CACHE_FLASH) {
-      *(i32x2*)vd = i32x2{(int)v0, (int)v1};
-    } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) vd[i * v_step] = (uint8_t)(((i < 4 ? v0 : v1) >> (8 * (i & 3))) & 0xffu);
-    }
+    for (int i = 0; i < 8; ++i) vd[i * v_step] = (uint8_t)((v8[i >> 2] >> (8 * (i & 3))) & 0xffu);
   } else {
-    *(i32x4*)((uint16_t*)a.key_cache + k_off) = ob;
     uint16_t* vd = (uint16_t*)a.value_cache + v_off;
-    if (LAYOUT == PA_CACHE_FLASH) {
-      *(i32x4*)vd = vv;
-    } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) vd[i * v_step] = (uint16_t)(((uint32_t)vv[i >> 1] >> ((i & 1) * 16)) & 0xffffu);
-    }
+    for (int i = 0; i < 8; ++i) vd[i * v_step] = (uint16_t)(((uint32_t)vv[i >> 1] >> ((i & 1) * 16)) & 0xffffu);
   }
 }
 
@@ -254,8 +397,11 @@ extern "C" int pa_fp8_rope_cache(const pa_fp8_rope_cache_args* a, void* stream) 
       !al16(a->sin_cache) || !al16(a->key_cache) || !al16(a->value_cache))
     return PA_ERR_ALIGN;
   const int rpw = 64 / (D >> 3);
-  const int64_t wg_per_token = (rows + rpw * kRcWaves - 1) / (rpw * kRcWaves);
-  const int64_t grid = wg_per_token * a->num_tokens;
+  const int64_t qunits = (int64_t)((a->num_q_heads + rpw - 1) / rpw) * a->num_tokens;
+  if (qunits > 0x7fffffffLL) return PA_ERR_SHAPE;
+  const int G = kRcWaves * rpw;  // tokens per K/V workgroup
+  const int64_t grid = (qunits + kRcWaves * kRcQUnits - 1) / (kRcWaves * kRcQUnits) +
+                       (int64_t)((a->num_tokens + G - 1) / G) * a->num_kv_heads;
   if (grid > 0x7fffffffLL) return PA_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   const hipError_t err = a->dtype == PA_DTYPE_BF16 ? dispatch_rope_cache<true>(*a, (unsigned)grid, s)

@@ -78,8 +78,10 @@ def build_fused_rope_cache_module(
         if t.stride(-1) != 1:
             raise ValueError(f"{name} must be contiguous in its last dimension")
 
-    def launch_fused_rope_cache(Q, K, V, Positions, CosCache, SinCache, SlotMapping, KeyCache, ValueCache, Q_out, K_out,
-                                num_tokens, KScale, VScale, stream=None):
+    def prepare(Q, K, V, Positions, CosCache, SinCache, SlotMapping, KeyCache, ValueCache, Q_out, K_out, num_tokens,
+                KScale, VScale, stream=None):
+        """Validate and marshal one call; ``.launch()`` then issues it with
+        no further Python work (the tensors must stay alive)."""
         T = int(num_tokens)
         _check("Q", Q, (T, num_q_heads, D), dtype)
         _check("K", K, (T, num_kv_heads, D), dtype)
@@ -147,7 +149,25 @@ def build_fused_rope_cache_module(
         a.reuse_freqs_front_part = int(bool(reuse_freqs_front_part))
         a.index_i64 = int(pos_dtype == "i64")
         s = stream if stream is not None else torch.cuda.current_stream(dev)
-        lib = _lib.load()
-        _lib.check(lib.pa_fp8_rope_cache(ctypes.byref(a), ctypes.c_void_p(s.cuda_stream)), "pa_fp8_rope_cache")
+        return PreparedRopeCache(a, s, tuple(tensors))
 
+    def launch_fused_rope_cache(Q, K, V, Positions, CosCache, SinCache, SlotMapping, KeyCache, ValueCache, Q_out, K_out,
+                                num_tokens, KScale, VScale, stream=None):
+        prepare(Q, K, V, Positions, CosCache, SinCache, SlotMapping, KeyCache, ValueCache, Q_out, K_out, num_tokens,
+                KScale, VScale, stream).launch()
+
+    launch_fused_rope_cache.prepare = prepare
     return launch_fused_rope_cache
+
+
+class PreparedRopeCache:
+    """A validated writer call with its C-ABI arguments marshalled."""
+
+    def __init__(self, args, stream, keepalive):
+        self.args = args
+        self._stream = ctypes.c_void_p(stream.cuda_stream)
+        self._keep = keepalive
+        self._lib = _lib.load()
+
+    def launch(self) -> None:
+        _lib.check(self._lib.pa_fp8_rope_cache(ctypes.byref(self.args), self._stream), "pa_fp8_rope_cache")

@@ -173,3 +173,85 @@ def kv_bytes(cfg: DecodeConfig, ctx: List[int], include_scales: bool = False) ->
     if include_scales and cfg.per_token:
         per_tok += cfg.num_kv_heads * 8
     return toks * per_tok
+
+
+# ---------------------------------------------------------------------------
+# KV-cache writer workloads (NeoX RoPE on Q/K + paged K/V cache write)
+# ---------------------------------------------------------------------------
+
+
+@dataclasses.dataclass(frozen=True)
+class RopeCacheConfig:
+    name: str
+    num_tokens: int
+    num_q_heads: int
+    num_kv_heads: int
+    head_size: int
+    block_size: int
+    num_blocks: int
+    tokens_per_seq: int  # consecutive tokens of one sequence (1: decode, one token per sequence)
+    max_pos: int = 8192
+
+
+# Llama-3-8B heads, fp8 cache in the decode kernels' layout (K [NB, KH, D/16,
+# bs, 16], V [NB, KH, bs/16, D, 16]), per-tensor scales, half cos/sin tables:
+#   decode:  one new token for each of 64 sequences (the C2 batch)
+#   prefill: 4 sequences x 4096 tokens
+ROPE_CONFIGS: Dict[str, RopeCacheConfig] = {
+    "rope_decode_llama8b": RopeCacheConfig("rope_decode_llama8b", 64, 32, 8, 128, 16, 16384, 1),
+    "rope_prefill_llama8b": RopeCacheConfig("rope_prefill_llama8b", 16384, 32, 8, 128, 16, 16384, 4096),
+}
+
+
+def build_rope_inputs(cfg: RopeCacheConfig, device="cpu", seed: int = 0) -> dict:
+    """Inputs of one writer call: bf16 Q/K/V N(0,1), half cos/sin tables of
+    a 10000-base rotary embedding, token positions and cache slots (each
+    sequence's tokens fill its pages in order; pages are a random
+    permutation of the cache), fp8 caches and per-tensor scales."""
+    device = torch.device(device)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    T, d = cfg.num_tokens, cfg.head_size
+    q = torch.randn(T, cfg.num_q_heads, d, generator=gen, device=device).to(torch.bfloat16)
+    k = torch.randn(T, cfg.num_kv_heads, d, generator=gen, device=device).to(torch.bfloat16)
+    v = torch.randn(T, cfg.num_kv_heads, d, generator=gen, device=device).to(torch.bfloat16)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, d, 2, dtype=torch.float64) / d))
+    ang = torch.arange(cfg.max_pos, dtype=torch.float64)[:, None] * inv[None, :]
+    cos = torch.cos(ang).to(torch.bfloat16).to(device)
+    sin = torch.sin(ang).to(torch.bfloat16).to(device)
+    rng = np.random.default_rng(seed + 1)
+    nseq = T // cfg.tokens_per_seq
+    pages = -(-cfg.tokens_per_seq // cfg.block_size)
+    perm = rng.permutation(cfg.num_blocks)[: nseq * pages].reshape(nseq, pages)
+    tok = np.arange(cfg.tokens_per_seq)
+    if cfg.tokens_per_seq == 1:
+        # decode: the new token of a sequence whose context already fills part of a page
+        pos = rng.integers(1, cfg.max_pos, size=nseq)
+        slots = perm[:, 0] * cfg.block_size + pos % cfg.block_size
+    else:
+        pos = np.tile(tok, nseq)
+        slots = (perm[:, tok // cfg.block_size] * cfg.block_size + tok % cfg.block_size).reshape(-1)
+    nb, kh, bs = cfg.num_blocks, cfg.num_kv_heads, cfg.block_size
+    return {
+        "config": cfg,
+        "q": q,
+        "k": k,
+        "v": v,
+        "cos": cos,
+        "sin": sin,
+        "positions": torch.from_numpy(pos.astype(np.int32)).to(device),
+        "slot_mapping": torch.from_numpy(slots.astype(np.int32)).to(device),
+        "key_cache": torch.zeros(nb, kh, d // 16, bs, 16, dtype=torch.uint8, device=device).view(FP8),
+        "value_cache": torch.zeros(nb, kh, bs // 16, d, 16, dtype=torch.uint8, device=device).view(FP8),
+        "k_scale": torch.tensor([k.abs().max().item() / FP8_MAX * 1.5], dtype=torch.float32, device=device),
+        "v_scale": torch.tensor([v.abs().max().item() / FP8_MAX], dtype=torch.float32, device=device),
+    }
+
+
+def rope_bytes(cfg: RopeCacheConfig) -> int:
+    """Algorithmic HBM bytes of one writer call: Q/K/V, cos/sin rows and the
+    two indices read per token; Q_out/K_out and the fp8 K/V cache rows
+    written."""
+    d, qh, kh = cfg.head_size, cfg.num_q_heads, cfg.num_kv_heads
+    read = (qh + 2 * kh) * d * 2 + 2 * (d // 2) * 2 + 2 * 4
+    write = (qh + kh) * d * 2 + 2 * kh * d
+    return cfg.num_tokens * (read + write)

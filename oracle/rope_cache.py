@@ -77,18 +77,20 @@ def rope_cache_ref(
     apply_scale: bool = False,
     k_scale: Optional[float] = None,
     v_scale: Optional[float] = None,
+    inplace: bool = False,
 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """(q_out, k_out, key_cache', value_cache') on the CPU.
 
-    The caches are returned as new tensors; with apply_scale they are uint8
-    (fp8 e4m3fn bytes), otherwise of q's dtype.  Positions index the
-    cos / sin tables after clamping into [0, max_pos), as the kernel does.
+    The caches are returned as new tensors (or written in place with
+    ``inplace``); with apply_scale they are uint8 (fp8 e4m3fn bytes),
+    otherwise of q's dtype.  Positions index the cos / sin tables after
+    clamping into [0, max_pos), as the kernel does.
     """
     pos = low_words(positions).clamp(0, cos_cache.shape[0] - 1)
     cos_rows, sin_rows = cos_cache[pos], sin_cache[pos]
     q_out = rope_neox(q, cos_rows, sin_rows, reuse_freqs_front_part)
     k_out = rope_neox(k, cos_rows, sin_rows, reuse_freqs_front_part)
-    kc, vc = key_cache.clone(), value_cache.clone()
+    kc, vc = (key_cache, value_cache) if inplace else (key_cache.clone(), value_cache.clone())
     if apply_scale:
         kw, vw = fp8_bytes(k_out, k_scale), fp8_bytes(v, v_scale)
     else:

@@ -152,6 +152,42 @@ def test_scattered_slots_and_decode_value_layout(block_size, apply_scale):
     run(200, 16, 4, 128, flash=False, scattered=True, block_size=block_size, apply_scale=apply_scale, seed=7)
 
 
+@pytest.mark.parametrize("apply_scale", [False, True])
+@pytest.mark.parametrize("trans_v", [False, True])
+@pytest.mark.parametrize("block_size,D", [(16, 128), (64, 128), (16, 64), (64, 64)])
+def test_prefill_page_runs(block_size, D, trans_v, apply_scale):
+    """Slots 0..T-1 fill whole pages in order (the prefill pattern the value
+    transpose writes 16 tokens at a time), with a ragged tail."""
+    run(16 * 13 + 5, 8, 2, D, flash=False, trans_v=trans_v, block_size=block_size, apply_scale=apply_scale)
+
+
+def test_prefill_page_runs_misaligned():
+    """A sequence starting mid-page: page runs that begin off a 16-token
+    boundary take the per-token path, aligned ones the transpose."""
+    T, QH, KH, D, bs = 150, 8, 2, 128, 64
+    torch.manual_seed(11)
+    tdt = torch.bfloat16
+    q, k, v = (torch.randn(T, h, D, dtype=tdt) for h in (QH, KH, KH))
+    cos = torch.randn(MAX_POS, D // 2, dtype=tdt)
+    sin = torch.randn(MAX_POS, D // 2, dtype=tdt)
+    pos = torch.arange(T, dtype=torch.int32) + 7
+    slots = (torch.arange(T, dtype=torch.int32) + 7 + 64 * 3)  # starts at page 3, position 7
+    nb = 12
+    kc = torch.zeros(nb, KH, D // 16, bs, 16, dtype=torch.uint8)
+    vc = torch.zeros(nb, KH, bs // 16, D, 16, dtype=torch.uint8)
+    launch = build_fused_rope_cache_module(head_dim=D, num_q_heads=QH, num_kv_heads=KH, block_size=bs,
+                                           flash_layout=False, apply_scale=True)
+    dev = [t.to(DEV) for t in (q, k, v, pos, cos, sin, slots)]
+    kc_d, vc_d = kc.to(DEV).view(torch.float8_e4m3fn), vc.to(DEV).view(torch.float8_e4m3fn)
+    ks, vs = torch.tensor([0.05], device=DEV), torch.tensor([0.05], device=DEV)
+    q_out, k_out = torch.empty_like(dev[0]), torch.empty_like(dev[1])
+    launch(dev[0], dev[1], dev[2], dev[3], dev[4], dev[5], dev[6], kc_d, vc_d, q_out, k_out, T, ks, vs)
+    torch.cuda.synchronize()
+    _, _, rkc, rvc = rc.rope_cache_ref(q, k, v, pos, cos, sin, slots, kc, vc, block_size=bs, layout=rc.ATOM_TRANS_V,
+                                       apply_scale=True, k_scale=0.05, v_scale=0.05)
+    assert torch.equal(kc_d.view(torch.uint8).cpu(), rkc) and torch.equal(vc_d.view(torch.uint8).cpu(), rvc)
+
+
 @pytest.mark.parametrize("D", [16, 32, 256])
 def test_other_head_sizes(D):
     run(33, 6, 2, D, flash=True, scattered=True)
