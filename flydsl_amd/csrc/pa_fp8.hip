@@ -345,20 +345,8 @@ __device__ __forceinline__ void compute_chunk(WaveState<NCG>& s, const QueryTile
   const int tok0 = tb + 8 * grp;
   const bool interior = tb >= q.lo_max && tb + kChunk <= q.hi_min;
   const bool edge = tb < q.lo_all || tb + kChunk > q.hi_all;
-  if (edge) {
-    // Zero value bytes of tokens no query sees (stale page tails).
-    uint64_t keep = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int t = tok0 + j;
-      if (t >= q.lo_all && t < q.hi_all) keep |= (uint64_t)0xff << (8 * j);
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) V[j] = (long)((uint64_t)V[j] & keep);
-  }
 
   float ksc[8], vsc[8];
-  float vratio = 1.0f, vinv = 1.0f;
   if (PER_TOKEN) {
     const LDS_AS float* ss = (const LDS_AS float*)(sv + kVBytes);
     f32x4 k0 = *(const LDS_AS f32x4*)(ss + 8 * grp);
@@ -372,24 +360,41 @@ __device__ __forceinline__ void compute_chunk(WaveState<NCG>& s, const QueryTile
       vsc[j] = w0[j];
       vsc[4 + j] = w1[j];
     }
-    if (edge) {
+  }
+  if (__builtin_expect(edge, 0)) {
+    // Tokens j in [jlo, jhi) of this lane are visible to some column.  Zero
+    // the value bytes (and value scales) of the others: stale page tails
+    // must not inject NaN.  One block computes the bounds once, so nothing
+    // of it is evaluated on interior chunks.
+    const int jlo = pa_min(pa_max(q.lo_all - tok0, 0), 8);
+    const int jhi = pa_min(pa_max(q.hi_all - tok0, jlo), 8);
+    const uint64_t below_hi = jhi >= 8 ? ~0ull : (1ull << (8 * jhi)) - 1;
+    const uint64_t below_lo = jlo >= 8 ? ~0ull : (1ull << (8 * jlo)) - 1;
+    const uint64_t keep = below_hi & ~below_lo;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int t = tok0 + j;
-        if (!(t >= q.lo_all && t < q.hi_all)) vsc[j] = 0.0f;
-      }
+    for (int j = 0; j < 8; ++j) V[j] = (long)((uint64_t)V[j] & keep);
+    if (PER_TOKEN) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) vsc[j] = (j >= jlo && j < jhi) ? vsc[j] : 0.0f;
     }
+  }
+
+  // vratio rescales the accumulator when the running maximum of the value
+  // scales grows; vmul is that maximum (1 while it is still 0) and vlog its
+  // base-2 logarithm, which the exponent subtracts so that the
+  // probabilities come out already divided by it.
+  float vratio = 1.0f, vmul = 1.0f, vlog = 0.0f;
+  if (PER_TOKEN) {
     float cmax = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) cmax = fmaxf(cmax, vsc[j]);
     cmax = max_over_groups(cmax);
     const float vnew = fmaxf(s.vsmax, cmax);
-    // Both factors are ratios against the same running maximum, applied to
-    // the probabilities and to the accumulator alike; rcp's rounding cancels
-    // when the final output multiplies by that maximum again.
-    const float rv = __builtin_amdgcn_rcpf(vnew);
-    vratio = vnew > 0.0f ? s.vsmax * rv : 1.0f;
-    vinv = vnew > 0.0f ? rv : 0.0f;
+    // The probabilities and the accumulator are both taken relative to the
+    // same running maximum; the final output multiplies by it again.
+    vratio = vnew > 0.0f ? s.vsmax * __builtin_amdgcn_rcpf(vnew) : 1.0f;
+    vmul = vnew > 0.0f ? vnew : 1.0f;
+    vlog = __builtin_amdgcn_logf(vmul);
     s.vsmax = vnew;
   }
 
@@ -400,10 +405,10 @@ __device__ __forceinline__ void compute_chunk(WaveState<NCG>& s, const QueryTile
     f32x4 lb = mfma_fp8_k128(KB, q.hi[cg], zz);
     la = mfma_fp8_k128(KA, q.lo[cg], la);
     lb = mfma_fp8_k128(KB, q.lo[cg], lb);
-    // Base-2 logits l = raw * fac (* per-token key scale).  When the factor
-    // is one positive constant for the column (per-tensor scales) the
-    // maximum is taken on the raw products, which orders them the same way,
-    // and the exponent is one FMA per logit.
+    // Base-2 logits l = raw * fac (* per-token key scale).  The column
+    // factor is positive unless the softmax or key scale is not: then the
+    // maximum is taken on the products without it, which orders them the
+    // same way, and the factor goes into the exponent's FMA.
     float lg[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -411,18 +416,20 @@ __device__ __forceinline__ void compute_chunk(WaveState<NCG>& s, const QueryTile
       lg[4 + i] = lb[i];
     }
     const float fac = q.fac[cg];
-    const bool prescale = PER_TOKEN || !(fac > 0.0f);  // wave-uniform
+    const bool prescale = __ballot(!(fac > 0.0f)) != 0;  // wave-uniform
     const float post = prescale ? 1.0f : fac;
+    if (PER_TOKEN) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) lg[j] *= ksc[j];
+    }
     if (prescale) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) lg[j] *= PER_TOKEN ? fac * ksc[j] : fac;
+      for (int j = 0; j < 8; ++j) lg[j] *= fac;
     }
-    if (!interior) {
+    if (__builtin_expect(!interior, 0)) {
+      const int jl = q.vis_lo[cg] - tok0, jh = q.vis_hi[cg] - tok0;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int t = tok0 + j;
-        lg[j] = (t >= q.vis_lo[cg] && t < q.vis_hi[cg]) ? lg[j] : kNegInf;
-      }
+      for (int j = 0; j < 8; ++j) lg[j] = (j >= jl && j < jh) ? lg[j] : kNegInf;
     }
     float cmax =
         fmaxf(fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3])), fmaxf(fmaxf(lg[4], lg[5]), fmaxf(lg[6], lg[7])));
@@ -434,15 +441,23 @@ __device__ __forceinline__ void compute_chunk(WaveState<NCG>& s, const QueryTile
     float pr[8];
     float psum = 0.0f;
     const float bias = 8.0f - muse;  // 256 * exp(l - m)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      pr[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(lg[j], post, bias));
-      psum += pr[j];
-    }
-    s.lsum[cg] = s.lsum[cg] * alpha + psum;
     if (PER_TOKEN) {
+      // ev = 256 * exp(l - m) / vmul; the probability fed to PV is ev * vsc.
+      const float bv = bias - vlog;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pr[j] *= vsc[j] * vinv;
+      for (int j = 0; j < 8; ++j) {
+        const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(lg[j], post, bv));
+        psum += ev;
+        pr[j] = ev * vsc[j];
+      }
+      s.lsum[cg] = s.lsum[cg] * alpha + psum * vmul;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        pr[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(lg[j], post, bias));
+        psum += pr[j];
+      }
+      s.lsum[cg] = s.lsum[cg] * alpha + psum;
     }
     long phi, plo;
     split8_fp8(pr, phi, plo);
@@ -1087,27 +1102,24 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
   const int grp = lane >> 4;
   const int c16 = lane & 15;
   const int wid = blockIdx.x * kWaves + wave;
-  const int H = a.num_kv_heads;
   const int ql = a.query_length;
   const int gqa = a.query_group_size;
   const int eq = ql * gqa;
-  const int W = a.sliding_window;
   const int bs = a.block_size;
   const int bs_shift = BS16 ? 4 : __builtin_ctz((unsigned)bs);
   const int nblocks = a.num_blocks;
 
   // ---------------- this wave's walk ----------------
   using Walk = typename std::conditional<WORKLIST, WorklistWalk, BalancedWalk>::type;
-  Walk iwalk;
+  Walk walk;
   if constexpr (WORKLIST) {
     if (wid >= a.num_workers) return;
-    iwalk.idx = ld_uniform(work_indptr, wid);
-    iwalk.end = ld_uniform(work_indptr, wid + 1);
+    walk.idx = ld_uniform(work_indptr, wid);
+    walk.end = ld_uniform(work_indptr, wid + 1);
   } else {
-    if (!balanced_start(iwalk, a, kv_indptr, context_lengths, wid, lane)) return;
+    if (!balanced_start(walk, a, kv_indptr, context_lengths, wid, lane)) return;
   }
-  Walk cwalk = iwalk;  // the compute side replays the issue side's walk
-  auto next_piece = [&](Walk& walk, Piece& p) -> bool {
+  auto next_piece = [&](Piece& p) -> bool {
     if constexpr (WORKLIST)
       return walk.next(p, a, kv_indptr, context_lengths, work_info, partition_indptr);
     else
@@ -1118,29 +1130,54 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
   LDS_AS unsigned char* qimg = ring + kStages * kStageBytes;
   const int koff_lane = BS16 ? lane * 16 : (lane >> 4) * (bs * 16) + (lane & 15) * 16;
   const int voff_plain = lane * bs;
-
-  // ---------------- issue side ----------------
-  Piece ip;
-  bool iok = next_piece(iwalk, ip);
-  while (iok && ip.n == 0) iok = next_piece(iwalk, ip);
-  int ic = 0;     // next chunk of ip to issue
-  int iq = 0;     // query image the next piece's rows go to
-  int np0 = 0, np1 = 0;
-  auto fetch_pages = [&]() {
-    const int lp0 = (ip.tb0 + ic * kChunk) >> bs_shift;
-    np0 = ld_uniform(block_tables, ip.bt_off + pa_min(lp0, ip.last_page));
-    np1 = BS16 ? ld_uniform(block_tables, ip.bt_off + pa_min(lp0 + 1, ip.last_page)) : np0;
-  };
   auto clamp_page = [&](int p) -> int {
     p = p < 0 ? 0 : p;
     return p < nblocks ? p : nblocks - 1;
   };
-  if (iok) fetch_pages();
+
+  // ---------------- piece window ----------------
+  // `cur` is being computed, `nxt` follows.  The issue side, one chunk
+  // ahead, never goes past `nxt` (it pauses instead), so one walker serves
+  // both sides and the scalar state stays in SGPRs.
+  Piece cur, nxt;
+  bool has_cur = next_piece(cur);
+  if (!has_cur) return;
+  bool has_nxt = next_piece(nxt);
+
+  // Issue cursor: next chunk at token itb, irem chunks left in its piece
+  // (nxt when iw, else cur); ifirst: that chunk opens the piece.
+  int itb = 0, ih = 0, ilast = 0, irem = 0, iw = 0, iorow = 0;
+  int64_t ibt = 0;
+  bool iok = false, ifirst = false;
+  int np0 = 0, np1 = 0;  // page ids of the next chunk (prefetched)
+  auto fetch_pages = [&]() {
+    const int lp0 = itb >> bs_shift;
+    np0 = ld_uniform(block_tables, ibt + pa_min(lp0, ilast));
+    np1 = BS16 ? ld_uniform(block_tables, ibt + pa_min(lp0 + 1, ilast)) : np0;
+  };
+  auto issue_enter = [&](const Piece& p, int which) {
+    itb = p.tb0;
+    ih = p.h;
+    ibt = p.bt_off;
+    ilast = p.last_page;
+    irem = p.n;
+    iorow = p.orow;
+    iw = which;
+    iok = true;
+    ifirst = true;
+    fetch_pages();
+  };
+  if (cur.n > 0)
+    issue_enter(cur, 0);
+  else if (has_nxt && nxt.n > 0)
+    issue_enter(nxt, 1);
+
+  int iq = 0;  // query image the next piece's rows go to
   // Issues the next chunk (and, first in a piece, the piece's query rows)
   // into stage st; returns whether query rows were issued.
-  auto issue_next = [&](int st) -> bool {
-    bool q = false;
-    if (ic == 0) {
+  auto issue_chunk = [&](int st) -> bool {
+    const bool q = ifirst;
+    if (ifirst) {
       // Query rows of columns 4i + lane/16 (clamped to a real column).
       LDS_AS unsigned char* qd = qimg + iq * kQBytes;
 #pragma unroll
@@ -1149,19 +1186,19 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
         const int qi = e / gqa;
         const int g = e - qi * gqa;
         const unsigned char* src = (const unsigned char*)a.query +
-                                   2 * ((int64_t)(ip.orow + qi) * a.stride_q_tok +
-                                        (int64_t)(ip.h * gqa + g) * a.stride_q_head) +
+                                   2 * ((int64_t)(iorow + qi) * a.stride_q_tok +
+                                        (int64_t)(ih * gqa + g) * a.stride_q_head) +
                                    (lane & 15) * 16;
         lds_dma16_cached(src, qd + i * 1024);
       }
       iq ^= 1;
-      q = true;
+      ifirst = false;
     }
-    const int tb = ip.tb0 + ic * kChunk;
+    const int tb = itb;
     const int p0 = clamp_page(np0);
     const int p1 = BS16 ? clamp_page(np1) : p0;
-    const uint8_t* kbase = (const uint8_t*)a.key_cache + (int64_t)ip.h * a.stride_k_head;
-    const uint8_t* vbase = (const uint8_t*)a.value_cache + (int64_t)ip.h * a.stride_v_head;
+    const uint8_t* kbase = (const uint8_t*)a.key_cache + (int64_t)ih * a.stride_k_head;
+    const uint8_t* vbase = (const uint8_t*)a.value_cache + (int64_t)ih * a.stride_v_head;
     LDS_AS unsigned char* sk = ring + st * kStageBytes;
     LDS_AS unsigned char* sv = sk + kKBytes;
     if (BS16) {
@@ -1204,17 +1241,17 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
         const int tt = (lane & 7) * 4;
         const int pg2 = BS16 ? (tt >= 16 ? p1 : p0) : p0;
         const int sidx = BS16 ? (tt & 15) : (tb & (bs - 1)) + tt;
-        const float* base = (lane < 8 ? key_scale : value_scale) + (int64_t)ip.h * a.stride_ks_head;
+        const float* base = (lane < 8 ? key_scale : value_scale) + (int64_t)ih * a.stride_ks_head;
         lds_dma16(base + (int64_t)pg2 * a.stride_ks_block + sidx, ss);
       }
     }
-    if (++ic == ip.n) {
-      ic = 0;
-      do {
-        iok = next_piece(iwalk, ip);
-      } while (iok && ip.n == 0);
-    }
-    if (iok) fetch_pages();
+    itb += kChunk;
+    if (--irem > 0)
+      fetch_pages();
+    else if (iw == 0 && has_nxt && nxt.n > 0)
+      issue_enter(nxt, 1);
+    else
+      iok = false;
     return q;
   };
 
@@ -1226,17 +1263,26 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
   WaveState<NCG> st;
   st.reset();
   QueryTile<NCG> qt;
-  int cq = 0;  // query image of the next piece to compute
-  int gc = 0;  // chunks computed (stage = gc % 2)
-  if (iok) issue_next(0);
-  Piece cp;
-  while (next_piece(cwalk, cp)) {
-    for (int k = 0; k < cp.n; ++k) {
+  int cq = 0;      // query image of the next piece to compute
+  int gc = 0;      // chunks computed (stage = gc % 2)
+  int issued = 0;  // chunks issued
+  if (iok) {
+    issue_chunk(0);
+    issued = 1;
+  }
+  while (has_cur) {
+    for (int k = 0; k < cur.n; ++k) {
       const int stg = gc & 1;
+      if (issued == gc) {
+        // The issue side paused past an empty piece: chunk gc goes now.
+        issue_chunk(stg);
+        ++issued;
+      }
       if (iok) {
         // In order: [chunk gc] ... [query rows?] [chunk gc + 1]; wait for
         // everything up to chunk gc.
-        if (issue_next(stg ^ 1))
+        ++issued;
+        if (issue_chunk(stg ^ 1))
           __builtin_amdgcn_s_waitcnt(vmcnt_only(kLoadsPerChunk + NQ));
         else
           __builtin_amdgcn_s_waitcnt(vmcnt_only(kLoadsPerChunk));
@@ -1258,9 +1304,9 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
 #pragma unroll
           for (int i = 0; i < 4; ++i) qraw[0][i] = i32x4{0, 0, 0, 0};
         }
-        prepare_query<NCG>(qt, qraw, a.query_dtype, logit_scale, cp.ctx, ql, gqa, W, c16);
+        prepare_query<NCG>(qt, qraw, a.query_dtype, logit_scale, cur.ctx, ql, gqa, a.sliding_window, c16);
       }
-      compute_chunk<NCG, PER_TOKEN>(st, qt, ring + stg * kStageBytes, krow, grp, c16, cp.tb0 + k * kChunk);
+      compute_chunk<NCG, PER_TOKEN>(st, qt, ring + stg * kStageBytes, krow, grp, c16, cur.tb0 + k * kChunk);
     }
     // ---- the piece is complete: output row or partial ----
     const float vfin = PER_TOKEN ? st.vsmax : v_tensor_scale;
@@ -1270,19 +1316,19 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
     if (e < eq) {
       const int qi = e / gqa;
       const int g = e - qi * gqa;
-      const int qh = cp.h * gqa + g;
+      const int qh = cur.h * gqa + g;
       const float sc = L > 0.0f ? vfin / L : 0.0f;
-      if (cp.target < 0) {
-        const int64_t off = (int64_t)(cp.orow + qi) * a.stride_out_tok + (int64_t)qh * a.stride_out_head + 4 * grp;
+      if (cur.target < 0) {
+        const int64_t off = (int64_t)(cur.orow + qi) * a.stride_out_tok + (int64_t)qh * a.stride_out_head + 4 * grp;
 #pragma unroll
         for (int j = 0; j < 8; ++j) store_out4(output, a.output_dtype, off + 16 * j, st.acc[0][j] * sc);
       } else {
         int64_t po, pl;
         if (WORKLIST) {
-          po = (int64_t)(cp.target + qi) * a.stride_po_row + (int64_t)qh * kHead;
-          pl = (int64_t)(cp.target + qi) * a.stride_pl_row + qh;
+          po = (int64_t)(cur.target + qi) * a.stride_po_row + (int64_t)qh * kHead;
+          pl = (int64_t)(cur.target + qi) * a.stride_pl_row + qh;
         } else {
-          pl = (int64_t)cp.target * eq + e;
+          pl = (int64_t)cur.target * eq + e;
           po = pl * kHead;
         }
 #pragma unroll
@@ -1290,9 +1336,15 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
         if (grp == 0) part_lse[pl] = L > 0.0f ? kLn2 * (m + __builtin_amdgcn_logf(L) - 8.0f) : kNegInf;
       }
     }
-    if (!WORKLIST && cp.desc_cnt > 0 && lane == 0)
-      *(i32x2*)(segdesc + 2 * ((int64_t)cp.b * H + cp.h)) = i32x2{cp.target, cp.desc_cnt};
+    if (!WORKLIST && cur.desc_cnt > 0 && lane == 0)
+      *(i32x2*)(segdesc + 2 * ((int64_t)cur.b * a.num_kv_heads + cur.h)) = i32x2{cur.target, cur.desc_cnt};
     st.reset();
+    // ---- move the window ----
+    cur = nxt;
+    has_cur = has_nxt;
+    has_nxt = has_cur && next_piece(nxt);
+    if (iw == 1) iw = 0;
+    if (!iok && has_nxt && nxt.n > 0) issue_enter(nxt, 1);
   }
 }
 
@@ -1330,27 +1382,24 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
   const int grp = lane >> 4;
   const int c16 = lane & 15;
   const int wid = blockIdx.x;
-  const int H = a.num_kv_heads;
   const int ql = a.query_length;
   const int gqa = a.query_group_size;
   const int eq = ql * gqa;
-  const int W = a.sliding_window;
   const int bs = a.block_size;
   const int bs_shift = BS16 ? 4 : __builtin_ctz((unsigned)bs);
   const int nblocks = a.num_blocks;
   const int e = wave * 16 + c16;  // this lane's query column
 
   using Walk = typename std::conditional<WORKLIST, WorklistWalk, BalancedWalk>::type;
-  Walk iwalk;
+  Walk walk;
   if constexpr (WORKLIST) {
     if (wid >= a.num_workers) return;
-    iwalk.idx = ld_uniform(work_indptr, wid);
-    iwalk.end = ld_uniform(work_indptr, wid + 1);
+    walk.idx = ld_uniform(work_indptr, wid);
+    walk.end = ld_uniform(work_indptr, wid + 1);
   } else {
-    if (!balanced_start(iwalk, a, kv_indptr, context_lengths, wid, lane)) return;
+    if (!balanced_start(walk, a, kv_indptr, context_lengths, wid, lane)) return;
   }
-  Walk cwalk = iwalk;
-  auto next_piece = [&](Walk& walk, Piece& p) -> bool {
+  auto next_piece = [&](Piece& p) -> bool {
     if constexpr (WORKLIST)
       return walk.next(p, a, kv_indptr, context_lengths, work_info, partition_indptr);
     else
@@ -1363,18 +1412,50 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
     return p < nblocks ? p : nblocks - 1;
   };
 
-  // ---------------- issue side: this wave's share of every chunk ----------------
-  Piece ip;
-  bool iok = next_piece(iwalk, ip);
-  while (iok && ip.n == 0) iok = next_piece(iwalk, ip);
-  int ic = 0;
-  auto issue_next = [&](int st) {
-    const int tb = ip.tb0 + ic * kChunk;
-    const int lp0 = tb >> bs_shift;
-    const int p0 = clamp_page(ld_uniform(block_tables, ip.bt_off + pa_min(lp0, ip.last_page)));
-    const int p1 = BS16 ? clamp_page(ld_uniform(block_tables, ip.bt_off + pa_min(lp0 + 1, ip.last_page))) : p0;
-    const uint8_t* kbase = (const uint8_t*)a.key_cache + (int64_t)ip.h * a.stride_k_head;
-    const uint8_t* vbase = (const uint8_t*)a.value_cache + (int64_t)ip.h * a.stride_v_head;
+  // ---------------- piece window ----------------
+  // The walk is seen through two pieces: `cur` is being computed, `nxt`
+  // follows.  The issue side runs up to S - 1 chunks ahead of the compute
+  // side but never past `nxt`: once it has issued all of `nxt` it pauses
+  // until the compute side moves on.  One walker serves both sides, which
+  // keeps the scalar state small enough to stay in SGPRs.
+  Piece cur, nxt;
+  bool has_cur = next_piece(cur);
+  if (!has_cur) return;
+  bool has_nxt = next_piece(nxt);
+
+  // Issue cursor: next chunk at token itb of kv head ih, irem chunks left
+  // in its piece, which is nxt when iw (else cur).
+  int itb = 0, ih = 0, ilast = 0, irem = 0, iw = 0;
+  int64_t ibt = 0;
+  bool iok = false;
+  int np0 = 0, np1 = 0;  // page ids of the next chunk (prefetched)
+  auto fetch_pages = [&]() {
+    const int lp0 = itb >> bs_shift;
+    np0 = ld_uniform(block_tables, ibt + pa_min(lp0, ilast));
+    np1 = BS16 ? ld_uniform(block_tables, ibt + pa_min(lp0 + 1, ilast)) : np0;
+  };
+  auto issue_enter = [&](const Piece& p, int which) {
+    itb = p.tb0;
+    ih = p.h;
+    ibt = p.bt_off;
+    ilast = p.last_page;
+    irem = p.n;
+    iw = which;
+    iok = true;
+    fetch_pages();
+  };
+  if (cur.n > 0)
+    issue_enter(cur, 0);
+  else if (has_nxt && nxt.n > 0)
+    issue_enter(nxt, 1);
+
+  // This wave's share of the next chunk, into stage st.
+  auto issue_chunk = [&](int st) {
+    const int tb = itb;
+    const int p0 = clamp_page(np0);
+    const int p1 = BS16 ? clamp_page(np1) : p0;
+    const uint8_t* kbase = (const uint8_t*)a.key_cache + (int64_t)ih * a.stride_k_head;
+    const uint8_t* vbase = (const uint8_t*)a.value_cache + (int64_t)ih * a.stride_v_head;
     LDS_AS unsigned char* sk = (LDS_AS unsigned char*)smem + st * kStageBytes;
     LDS_AS unsigned char* sv = sk + kKBytes;
     // Load i (0..7): i < 4 keys, else values; half hh = (i >> 1) & 1, 1 KiB piece q2 = i & 1.
@@ -1412,16 +1493,17 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
         const int tt = (lane & 7) * 4;
         const int pg2 = BS16 ? (tt >= 16 ? p1 : p0) : p0;
         const int sidx = BS16 ? (tt & 15) : (tb & (bs - 1)) + tt;
-        const float* base = (lane < 8 ? key_scale : value_scale) + (int64_t)ip.h * a.stride_ks_head;
+        const float* base = (lane < 8 ? key_scale : value_scale) + (int64_t)ih * a.stride_ks_head;
         lds_dma16(base + (int64_t)pg2 * a.stride_ks_block + sidx, ss);
       }
     }
-    if (++ic == ip.n) {
-      ic = 0;
-      do {
-        iok = next_piece(iwalk, ip);
-      } while (iok && ip.n == 0);
-    }
+    itb += kChunk;
+    if (--irem > 0)
+      fetch_pages();
+    else if (iw == 0 && has_nxt && nxt.n > 0)
+      issue_enter(nxt, 1);
+    else
+      iok = false;
   };
 
   // ---------------- query rows of a piece (registers) ----------------
@@ -1450,37 +1532,29 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
   st.reset();
   QueryTile<1> qt;
 
-  // Compute side.  A piece's query rows are consumed at its first chunk and
-  // the next non-empty piece's rows are loaded during its last chunk, so a
-  // single register set carries them, in the same in-order load queue as
-  // the chunks.
-  Piece cp;
-  bool cok = next_piece(cwalk, cp);
-  auto next_nonempty = [&](Walk w, Piece p, bool ok, Piece& out) -> bool {
-    while (ok && p.n == 0) ok = next_piece(w, p);
-    out = p;
-    return ok;
-  };
-  {
-    Piece q0;
-    if (next_nonempty(cwalk, cp, cok, q0)) load_query(q0);
-  }
+  // Query rows are loaded during the previous piece's last chunk when the
+  // next piece is known by then (qready), else at the piece's first chunk.
+  bool qready = false;
   int issued = 0;  // chunks this workgroup has issued
+  int gc = 0;      // chunks computed
 #pragma unroll
   for (int k = 0; k < S - 1; ++k)
     if (iok) {
-      issue_next(k);
+      issue_chunk(issued % S);
       ++issued;
     }
 
-  int gc = 0;  // chunks computed
-  while (cok) {
-    Piece np;
-    const bool nok = next_piece(cwalk, np);
-    for (int k = 0; k < cp.n; ++k) {
+  while (has_cur) {
+    for (int k = 0; k < cur.n; ++k) {
+      if (issued == gc) {
+        // The issue side paused past an empty piece: chunk gc goes now
+        // (its stage last held chunk gc - S, which every wave has left).
+        issue_chunk(gc % S);
+        ++issued;
+      }
       // Wait for this wave's loads of chunk gc: newer chunks (up to S - 2)
-      // may stay in flight.  Loads retire in order; query rows or stores
-      // issued in between are only waited for early.
+      // may stay in flight.  Loads retire in order; query rows issued in
+      // between are only waited for early.
       const int newer = issued - gc - 1;
       if (newer >= 2)
         __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * kLoads));
@@ -1489,21 +1563,26 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
       else
         __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
       // Every wave's share of chunk gc is now in LDS and every wave is done
-      // with chunk gc - 1, whose stage the next issue reuses.  A bare
-      // s_barrier: the DMA completion was awaited explicitly above (a fenced
-      // barrier would also wait for the chunks still in flight).
+      // with chunk gc - 1.  A bare s_barrier: the DMA completion was awaited
+      // explicitly above (a fenced barrier would also wait for the chunks
+      // still in flight).
       asm volatile("s_barrier" ::: "memory");
-      if (k == 0) prepare_query<1>(qt, qraw, a.query_dtype, logit_scale, cp.ctx, ql, gqa, W, c16, wave * 16);
-      if (k == cp.n - 1) {
-        Piece q;
-        if (next_nonempty(cwalk, np, nok, q)) load_query(q);
+      if (k == 0) {
+        if (!qready) load_query(cur);
+        prepare_query<1>(qt, qraw, a.query_dtype, logit_scale, cur.ctx, ql, gqa, a.sliding_window, c16, wave * 16);
       }
-      if (iok) {
-        issue_next((gc + S - 1) % S);
+      if (k == cur.n - 1) {
+        qready = has_nxt && nxt.n > 0;
+        if (qready) load_query(nxt);
+      }
+      // Stages of chunks up to gc + S - 1 are free (their previous chunks
+      // are at most gc - 1).
+      while (iok && issued < gc + S) {
+        issue_chunk(issued % S);
         ++issued;
       }
       compute_chunk<1, PER_TOKEN>(st, qt, (const LDS_AS unsigned char*)smem + (gc % S) * kStageBytes, krow, grp, c16,
-                                  cp.tb0 + k * kChunk);
+                                  cur.tb0 + k * kChunk);
       ++gc;
     }
     // ---- the piece is complete: this wave's columns ----
@@ -1513,19 +1592,19 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
     if (e < eq) {
       const int qi = e / gqa;
       const int g = e - qi * gqa;
-      const int qh = cp.h * gqa + g;
+      const int qh = cur.h * gqa + g;
       const float sc = L > 0.0f ? vfin / L : 0.0f;
-      if (cp.target < 0) {
-        const int64_t off = (int64_t)(cp.orow + qi) * a.stride_out_tok + (int64_t)qh * a.stride_out_head + 4 * grp;
+      if (cur.target < 0) {
+        const int64_t off = (int64_t)(cur.orow + qi) * a.stride_out_tok + (int64_t)qh * a.stride_out_head + 4 * grp;
 #pragma unroll
         for (int j = 0; j < 8; ++j) store_out4(output, a.output_dtype, off + 16 * j, st.acc[0][j] * sc);
       } else {
         int64_t po, pl;
         if (WORKLIST) {
-          po = (int64_t)(cp.target + qi) * a.stride_po_row + (int64_t)qh * kHead;
-          pl = (int64_t)(cp.target + qi) * a.stride_pl_row + qh;
+          po = (int64_t)(cur.target + qi) * a.stride_po_row + (int64_t)qh * kHead;
+          pl = (int64_t)(cur.target + qi) * a.stride_pl_row + qh;
         } else {
-          pl = (int64_t)cp.target * eq + e;
+          pl = (int64_t)cur.target * eq + e;
           po = pl * kHead;
         }
 #pragma unroll
@@ -1533,11 +1612,15 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
         if (grp == 0) part_lse[pl] = L > 0.0f ? kLn2 * (m + __builtin_amdgcn_logf(L) - 8.0f) : kNegInf;
       }
     }
-    if (!WORKLIST && cp.desc_cnt > 0 && wave == 0 && lane == 0)
-      *(i32x2*)(segdesc + 2 * ((int64_t)cp.b * H + cp.h)) = i32x2{cp.target, cp.desc_cnt};
+    if (!WORKLIST && cur.desc_cnt > 0 && wave == 0 && lane == 0)
+      *(i32x2*)(segdesc + 2 * ((int64_t)cur.b * a.num_kv_heads + cur.h)) = i32x2{cur.target, cur.desc_cnt};
     st.reset();
-    cp = np;
-    cok = nok;
+    // ---- move the window ----
+    cur = nxt;
+    has_cur = has_nxt;
+    has_nxt = has_cur && next_piece(nxt);
+    if (iw == 1) iw = 0;  // the issue cursor's piece is now cur
+    if (!iok && has_nxt && nxt.n > 0) issue_enter(nxt, 1);
   }
 }
 
