@@ -321,73 +321,80 @@ __device__ __forceinline__ void prepare_query(QueryTile<NCG>& q, const i32x4 (&q
   pa_plan_visible(ctx, ql - 1, ql, W, &q.lo_max, &q.hi_all);
 }
 
-// One 32-token chunk of keys and values, staged in LDS at sk (keys: two
-// 16-token halves [8 dim chunks][16 tokens][16 B], kKHalf apart; values:
-// [2 halves][128 head dims][16 tokens]; per-token K then V scales), folded
-// into the wave's online softmax.  tb is the chunk's first token.
-template <int NCG, bool PER_TOKEN>
-__device__ __forceinline__ void compute_chunk(WaveState<NCG>& s, const QueryTile<NCG>& q,
-                                              const LDS_AS unsigned char* sk, int krow, int grp, int c16, int tb) {
-  const LDS_AS unsigned char* sv = sk + kKBytes;
+// QK^T of one chunk: raw logits of the lane's 8 tokens (two 16-token
+// tiles) for each column block, Q's hi and lo terms accumulated.
+template <int NCG>
+__device__ __forceinline__ void chunk_logits(const QueryTile<NCG>& q, const LDS_AS unsigned char* sk, int krow,
+                                             int grp, f32x4 (&la)[NCG], f32x4 (&lb)[NCG]) {
   const i32x4 ka0 = *(const LDS_AS i32x4*)(sk + krow + grp * 256);
   const i32x4 ka1 = *(const LDS_AS i32x4*)(sk + krow + (grp + 4) * 256);
   const i32x4 kb0 = *(const LDS_AS i32x4*)(sk + krow + 64 + grp * 256);
   const i32x4 kb1 = *(const LDS_AS i32x4*)(sk + krow + 64 + (grp + 4) * 256);
   const i32x8 KA = {ka0[0], ka0[1], ka0[2], ka0[3], ka1[0], ka1[1], ka1[2], ka1[3]};
   const i32x8 KB = {kb0[0], kb0[1], kb0[2], kb0[3], kb1[0], kb1[1], kb1[2], kb1[3]};
-
-  // value operands: head dim 16j + c16, tokens 8*grp .. 8*grp+7
-  long V[8];
+  const f32x4 zz = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int j = 0; j < 8; ++j) V[j] = *(const LDS_AS long*)(sv + (grp >> 1) * 2048 + (16 * j + c16) * 16 + 8 * (grp & 1));
+  for (int cg = 0; cg < NCG; ++cg) {
+    la[cg] = mfma_fp8_k128(KA, q.hi[cg], zz);
+    lb[cg] = mfma_fp8_k128(KB, q.hi[cg], zz);
+    la[cg] = mfma_fp8_k128(KA, q.lo[cg], la[cg]);
+    lb[cg] = mfma_fp8_k128(KB, q.lo[cg], lb[cg]);
+  }
+}
 
-  // This lane's 8 tokens: tb + 8*grp + j.
-  const int tok0 = tb + 8 * grp;
-  const bool interior = tb >= q.lo_max && tb + kChunk <= q.hi_min;
-  const bool edge = tb < q.lo_all || tb + kChunk > q.hi_all;
-
-  float ksc[8], vsc[8];
-  if (PER_TOKEN) {
-    const LDS_AS float* ss = (const LDS_AS float*)(sv + kVBytes);
-    f32x4 k0 = *(const LDS_AS f32x4*)(ss + 8 * grp);
-    f32x4 k1 = *(const LDS_AS f32x4*)(ss + 8 * grp + 4);
-    f32x4 w0 = *(const LDS_AS f32x4*)(ss + 32 + 8 * grp);
-    f32x4 w1 = *(const LDS_AS f32x4*)(ss + 32 + 8 * grp + 4);
+// Softmax and PV of NCH chunks (raw logits la/lb, stages sk, first tokens
+// tb) folded into the online softmax as one step: one running-maximum
+// update, one accumulator rescale and one value-scale update for all of
+// them.  A chunk whose first token lies past every visible range is fully
+// masked (its value bytes are zeroed, so its LDS content does not matter).
+// Per-chunk operands are read from LDS where they are used, which keeps the
+// live registers of several chunks few.
+template <int NCG, bool PER_TOKEN, int NCH>
+__device__ __forceinline__ void chunk_softmax_pv(WaveState<NCG>& s, const QueryTile<NCG>& q,
+                                                 const f32x4 (&la)[NCH][NCG], const f32x4 (&lb)[NCH][NCG],
+                                                 const LDS_AS unsigned char* const (&sk)[NCH], int grp, int c16,
+                                                 const int (&tb)[NCH]) {
+  // Tokens j in [jlo, jhi) of this lane's 8 (tb + 8*grp + j) are visible to
+  // some column; edge chunks zero the value bytes and scales of the others,
+  // since stale page tails must not inject NaN.
+  bool edge[NCH];
+  int jlo[NCH], jhi[NCH];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    edge[ch] = tb[ch] < q.lo_all || tb[ch] + kChunk > q.hi_all;
+    const int tok0 = tb[ch] + 8 * grp;
+    jlo[ch] = pa_min(pa_max(q.lo_all - tok0, 0), 8);
+    jhi[ch] = pa_min(pa_max(q.hi_all - tok0, jlo[ch]), 8);
+  }
+  auto scales = [&](int ch, int off, float (&x)[8]) {
+    const LDS_AS float* ss = (const LDS_AS float*)(sk[ch] + kKBytes + kVBytes) + off + 8 * grp;
+    const f32x4 x0 = *(const LDS_AS f32x4*)ss;
+    const f32x4 x1 = *(const LDS_AS f32x4*)(ss + 4);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      ksc[j] = k0[j];
-      ksc[4 + j] = k1[j];
-      vsc[j] = w0[j];
-      vsc[4 + j] = w1[j];
+      x[j] = x0[j];
+      x[4 + j] = x1[j];
     }
-  }
-  if (__builtin_expect(edge, 0)) {
-    // Tokens j in [jlo, jhi) of this lane are visible to some column.  Zero
-    // the value bytes (and value scales) of the others: stale page tails
-    // must not inject NaN.  One block computes the bounds once, so nothing
-    // of it is evaluated on interior chunks.
-    const int jlo = pa_min(pa_max(q.lo_all - tok0, 0), 8);
-    const int jhi = pa_min(pa_max(q.hi_all - tok0, jlo), 8);
-    const uint64_t below_hi = jhi >= 8 ? ~0ull : (1ull << (8 * jhi)) - 1;
-    const uint64_t below_lo = jlo >= 8 ? ~0ull : (1ull << (8 * jlo)) - 1;
-    const uint64_t keep = below_hi & ~below_lo;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) V[j] = (long)((uint64_t)V[j] & keep);
-    if (PER_TOKEN) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) vsc[j] = (j >= jlo && j < jhi) ? vsc[j] : 0.0f;
-    }
-  }
+  };
 
   // vratio rescales the accumulator when the running maximum of the value
   // scales grows; vmul is that maximum (1 while it is still 0) and vlog its
   // base-2 logarithm, which the exponent subtracts so that the
   // probabilities come out already divided by it.
+  float vsc[NCH][8];
   float vratio = 1.0f, vmul = 1.0f, vlog = 0.0f;
   if (PER_TOKEN) {
     float cmax = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) cmax = fmaxf(cmax, vsc[j]);
+    for (int ch = 0; ch < NCH; ++ch) {
+      scales(ch, 32, vsc[ch]);
+      if (__builtin_expect(edge[ch], 0)) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) vsc[ch][j] = (j >= jlo[ch] && j < jhi[ch]) ? vsc[ch][j] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) cmax = fmaxf(cmax, vsc[ch][j]);
+    }
     cmax = max_over_groups(cmax);
     const float vnew = fmaxf(s.vsmax, cmax);
     // The probabilities and the accumulator are both taken relative to the
@@ -400,78 +407,102 @@ __device__ __forceinline__ void compute_chunk(WaveState<NCG>& s, const QueryTile
 
 #pragma unroll
   for (int cg = 0; cg < NCG; ++cg) {
-    const f32x4 zz = {0.f, 0.f, 0.f, 0.f};
-    f32x4 la = mfma_fp8_k128(KA, q.hi[cg], zz);
-    f32x4 lb = mfma_fp8_k128(KB, q.hi[cg], zz);
-    la = mfma_fp8_k128(KA, q.lo[cg], la);
-    lb = mfma_fp8_k128(KB, q.lo[cg], lb);
     // Base-2 logits l = raw * fac (* per-token key scale).  The column
     // factor is positive unless the softmax or key scale is not: then the
     // maximum is taken on the products without it, which orders them the
     // same way, and the factor goes into the exponent's FMA.
-    float lg[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      lg[i] = la[i];
-      lg[4 + i] = lb[i];
-    }
     const float fac = q.fac[cg];
     const bool prescale = __ballot(!(fac > 0.0f)) != 0;  // wave-uniform
     const float post = prescale ? 1.0f : fac;
-    if (PER_TOKEN) {
+    float lg[NCH][8];
+    float cmax = kNegInf;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) lg[j] *= ksc[j];
-    }
-    if (prescale) {
+    for (int ch = 0; ch < NCH; ++ch) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) lg[j] *= fac;
-    }
-    if (__builtin_expect(!interior, 0)) {
-      const int jl = q.vis_lo[cg] - tok0, jh = q.vis_hi[cg] - tok0;
+      for (int i = 0; i < 4; ++i) {
+        lg[ch][i] = la[ch][cg][i];
+        lg[ch][4 + i] = lb[ch][cg][i];
+      }
+      if (PER_TOKEN) {
+        float ksc[8];
+        scales(ch, 0, ksc);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) lg[j] = (j >= jl && j < jh) ? lg[j] : kNegInf;
+        for (int j = 0; j < 8; ++j) lg[ch][j] *= ksc[j];
+      }
+      if (prescale) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) lg[ch][j] *= fac;
+      }
+      const bool interior = tb[ch] >= q.lo_max && tb[ch] + kChunk <= q.hi_min;
+      if (__builtin_expect(!interior, 0)) {
+        const int tok0 = tb[ch] + 8 * grp;
+        const int jl = q.vis_lo[cg] - tok0, jh = q.vis_hi[cg] - tok0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) lg[ch][j] = (j >= jl && j < jh) ? lg[ch][j] : kNegInf;
+      }
+      cmax = fmaxf(cmax, fmaxf(fmaxf(fmaxf(lg[ch][0], lg[ch][1]), fmaxf(lg[ch][2], lg[ch][3])),
+                               fmaxf(fmaxf(lg[ch][4], lg[ch][5]), fmaxf(lg[ch][6], lg[ch][7]))));
     }
-    float cmax =
-        fmaxf(fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3])), fmaxf(fmaxf(lg[4], lg[5]), fmaxf(lg[6], lg[7])));
     cmax = max_over_groups(cmax) * post;  // post > 0: -inf stays -inf
     const float mnew = fmaxf(s.m2[cg], cmax);
     const float muse = mnew == kNegInf ? 0.0f : mnew;
     const float alpha = __builtin_amdgcn_exp2f(s.m2[cg] - muse);
     s.m2[cg] = mnew;
-    float pr[8];
-    float psum = 0.0f;
-    const float bias = 8.0f - muse;  // 256 * exp(l - m)
-    if (PER_TOKEN) {
-      // ev = 256 * exp(l - m) / vmul; the probability fed to PV is ev * vsc.
-      const float bv = bias - vlog;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(lg[j], post, bv));
-        psum += ev;
-        pr[j] = ev * vsc[j];
-      }
-      s.lsum[cg] = s.lsum[cg] * alpha + psum * vmul;
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        pr[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(lg[j], post, bias));
-        psum += pr[j];
-      }
-      s.lsum[cg] = s.lsum[cg] * alpha + psum;
-    }
-    long phi, plo;
-    split8_fp8(pr, phi, plo);
     const float f = alpha * vratio;
     if (__ballot(f != 1.0f)) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) s.acc[cg][j] *= f;
     }
+    // ev = 256 * exp(l - m) (/ vmul with per-token scales, where the
+    // probability fed to PV is ev * vsc).
+    const float bias = 8.0f - muse - vlog;
+    float psum = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      s.acc[cg][j] = mfma_fp8(V[j], phi, s.acc[cg][j]);
-      s.acc[cg][j] = mfma_fp8(V[j], plo, s.acc[cg][j]);
+    for (int ch = 0; ch < NCH; ++ch) {
+      float pr[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(lg[ch][j], post, bias));
+        psum += ev;
+        pr[j] = PER_TOKEN ? ev * vsc[ch][j] : ev;
+      }
+      long phi, plo;
+      split8_fp8(pr, phi, plo);
+      // value operands: head dim 16j + c16, tokens 8*grp .. 8*grp+7
+      const LDS_AS unsigned char* sv = sk[ch] + kKBytes;
+      long V[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        V[j] = *(const LDS_AS long*)(sv + (grp >> 1) * 2048 + (16 * j + c16) * 16 + 8 * (grp & 1));
+      if (__builtin_expect(edge[ch], 0)) {
+        const uint64_t below_hi = jhi[ch] >= 8 ? ~0ull : (1ull << (8 * jhi[ch])) - 1;
+        const uint64_t below_lo = jlo[ch] >= 8 ? ~0ull : (1ull << (8 * jlo[ch])) - 1;
+        const uint64_t keep = below_hi & ~below_lo;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) V[j] = (long)((uint64_t)V[j] & keep);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        s.acc[cg][j] = mfma_fp8(V[j], phi, s.acc[cg][j]);
+        s.acc[cg][j] = mfma_fp8(V[j], plo, s.acc[cg][j]);
+      }
     }
+    s.lsum[cg] = s.lsum[cg] * alpha + psum * vmul;
   }
+}
+
+// One 32-token chunk of keys and values, staged in LDS at sk (keys: two
+// 16-token halves [8 dim chunks][16 tokens][16 B], kKHalf apart; values:
+// [2 halves][128 head dims][16 tokens]; per-token K then V scales), folded
+// into the wave's online softmax.  tb is the chunk's first token.
+template <int NCG, bool PER_TOKEN>
+__device__ __forceinline__ void compute_chunk(WaveState<NCG>& s, const QueryTile<NCG>& q,
+                                              const LDS_AS unsigned char* sk, int krow, int grp, int c16, int tb) {
+  f32x4 la[1][NCG], lb[1][NCG];
+  chunk_logits<NCG>(q, sk, krow, grp, la[0], lb[0]);
+  const LDS_AS unsigned char* const sks[1] = {sk};
+  const int tbs[1] = {tb};
+  chunk_softmax_pv<NCG, PER_TOKEN, 1>(s, q, la, lb, sks, grp, c16, tbs);
 }
 
 // Workgroup geometry.  A workgroup covers `slots_per_workgroup`
@@ -1359,7 +1390,12 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
 // granularity (one run or one bin per workgroup); every wave writes its own
 // columns of each piece (no merge inside the workgroup).  A piece's query
 // rows are loaded into registers during the previous piece's last chunk.
-constexpr int kCoopStages = 4;
+// A cooperative workgroup moves through its chunks in units of two: one
+// ring stage, one wait and one barrier per unit, and one softmax step for
+// both chunks.  Three unit stages per workgroup (3 x 50 KiB of LDS per CU).
+constexpr int kCoopStages = 3;
+constexpr int kUnit = 2;  // chunks per unit
+constexpr int kFarToken = 1 << 30;  // first token of a unit's missing chunk
 
 template <int NW, bool PER_TOKEN, bool BS16, bool WORKLIST>
 __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
@@ -1371,10 +1407,11 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
     void* __restrict__ output) {
   static_assert(NW == 2 || NW == 4, "two or four waves share a chunk");
   constexpr int S = kCoopStages;
-  constexpr int kStageBytes = kKBytes + kVBytes + (PER_TOKEN ? kScaleBytes : 0);
-  constexpr int kDmaPerWave = 8 / NW;  // of the chunk's 8 one-KiB key/value loads
-  constexpr int kLoads = kDmaPerWave + (PER_TOKEN ? 1 : 0);
-  __shared__ __attribute__((aligned(16))) unsigned char smem[S * kStageBytes];
+  constexpr int kStageBytes = kKBytes + kVBytes + (PER_TOKEN ? kScaleBytes : 0);  // one chunk
+  constexpr int kUnitBytes = kUnit * kStageBytes;
+  constexpr int kDmaPerWave = 8 / NW;  // of a chunk's 8 one-KiB key/value loads
+  constexpr int kLoads = kUnit * (kDmaPerWave + (PER_TOKEN ? 1 : 0));  // per unit
+  __shared__ __attribute__((aligned(16))) unsigned char smem[S * kUnitBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1428,11 +1465,22 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
   int itb = 0, ih = 0, ilast = 0, irem = 0, iw = 0;
   int64_t ibt = 0;
   bool iok = false;
-  int np0 = 0, np1 = 0;  // page ids of the next chunk (prefetched)
+  // Page ids of the next unit (prefetched): its first chunk's (np0, and np1
+  // for the chunk's second 16-token page) and its second chunk's (np2, np3),
+  // which repeat the first's when the unit has one chunk.
+  int np0 = 0, np1 = 0, np2 = 0, np3 = 0;
   auto fetch_pages = [&]() {
     const int lp0 = itb >> bs_shift;
     np0 = ld_uniform(block_tables, ibt + pa_min(lp0, ilast));
-    np1 = BS16 ? ld_uniform(block_tables, ibt + pa_min(lp0 + 1, ilast)) : np0;
+    if (BS16) {
+      np1 = ld_uniform(block_tables, ibt + pa_min(lp0 + 1, ilast));
+      np2 = irem >= 2 ? ld_uniform(block_tables, ibt + pa_min(lp0 + 2, ilast)) : np0;
+      np3 = irem >= 2 ? ld_uniform(block_tables, ibt + pa_min(lp0 + 3, ilast)) : np1;
+    } else {
+      np1 = np0;
+      np2 = irem >= 2 ? ld_uniform(block_tables, ibt + pa_min((itb + kChunk) >> bs_shift, ilast)) : np0;
+      np3 = np2;
+    }
   };
   auto issue_enter = [&](const Piece& p, int which) {
     itb = p.tb0;
@@ -1449,14 +1497,14 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
   else if (has_nxt && nxt.n > 0)
     issue_enter(nxt, 1);
 
-  // This wave's share of the next chunk, into stage st.
-  auto issue_chunk = [&](int st) {
-    const int tb = itb;
-    const int p0 = clamp_page(np0);
-    const int p1 = BS16 ? clamp_page(np1) : p0;
+  // This wave's share of the chunk at token tb of kv head ih (pages q0, q1),
+  // into chunk slot sl of unit stage st.
+  auto issue_chunk = [&](int st, int sl, int tb, int q0, int q1) {
+    const int p0 = clamp_page(q0);
+    const int p1 = BS16 ? clamp_page(q1) : p0;
     const uint8_t* kbase = (const uint8_t*)a.key_cache + (int64_t)ih * a.stride_k_head;
     const uint8_t* vbase = (const uint8_t*)a.value_cache + (int64_t)ih * a.stride_v_head;
-    LDS_AS unsigned char* sk = (LDS_AS unsigned char*)smem + st * kStageBytes;
+    LDS_AS unsigned char* sk = (LDS_AS unsigned char*)smem + st * kUnitBytes + sl * kStageBytes;
     LDS_AS unsigned char* sv = sk + kKBytes;
     // Load i (0..7): i < 4 keys, else values; half hh = (i >> 1) & 1, 1 KiB piece q2 = i & 1.
 #pragma unroll
@@ -1497,8 +1545,17 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
         lds_dma16(base + (int64_t)pg2 * a.stride_ks_block + sidx, ss);
       }
     }
-    itb += kChunk;
-    if (--irem > 0)
+  };
+  // The next unit: the next two chunks of the issue piece, or its last one
+  // loaded twice (the copy keeps the load count per unit fixed; the compute
+  // side masks it).
+  auto issue_unit = [&](int st) {
+    const bool two = irem >= 2;
+    issue_chunk(st, 0, itb, np0, np1);
+    issue_chunk(st, 1, two ? itb + kChunk : itb, np2, np3);
+    itb += two ? 2 * kChunk : kChunk;
+    irem -= two ? 2 : 1;
+    if (irem > 0)
       fetch_pages();
     else if (iw == 0 && has_nxt && nxt.n > 0)
       issue_enter(nxt, 1);
@@ -1532,58 +1589,63 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
   st.reset();
   QueryTile<1> qt;
 
-  // Query rows are loaded during the previous piece's last chunk when the
-  // next piece is known by then (qready), else at the piece's first chunk.
+  // Query rows are loaded during the previous piece's last unit when the
+  // next piece is known by then (qready), else at the piece's first unit.
   bool qready = false;
-  int issued = 0;  // chunks this workgroup has issued
-  int gc = 0;      // chunks computed
+  int issued = 0;  // units this workgroup has issued
+  int gu = 0;      // units computed
 #pragma unroll
   for (int k = 0; k < S - 1; ++k)
     if (iok) {
-      issue_chunk(issued % S);
+      issue_unit(issued % S);
       ++issued;
     }
 
   while (has_cur) {
-    for (int k = 0; k < cur.n; ++k) {
-      if (issued == gc) {
-        // The issue side paused past an empty piece: chunk gc goes now
-        // (its stage last held chunk gc - S, which every wave has left).
-        issue_chunk(gc % S);
+    const int units = (cur.n + kUnit - 1) / kUnit;
+    for (int u = 0; u < units; ++u) {
+      if (issued == gu) {
+        // The issue side paused past an empty piece: unit gu goes now (its
+        // stage last held unit gu - S, which every wave has left).
+        issue_unit(gu % S);
         ++issued;
       }
-      // Wait for this wave's loads of chunk gc: newer chunks (up to S - 2)
+      // Wait for this wave's loads of unit gu: newer units (up to S - 2)
       // may stay in flight.  Loads retire in order; query rows issued in
       // between are only waited for early.
-      const int newer = issued - gc - 1;
-      if (newer >= 2)
-        __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * kLoads));
-      else if (newer == 1)
+      const int newer = issued - gu - 1;
+      if (newer >= 1)
         __builtin_amdgcn_s_waitcnt(vmcnt_only(kLoads));
       else
         __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-      // Every wave's share of chunk gc is now in LDS and every wave is done
-      // with chunk gc - 1.  A bare s_barrier: the DMA completion was awaited
-      // explicitly above (a fenced barrier would also wait for the chunks
+      // Every wave's share of unit gu is now in LDS and every wave is done
+      // with unit gu - 1.  A bare s_barrier: the DMA completion was awaited
+      // explicitly above (a fenced barrier would also wait for the units
       // still in flight).
       asm volatile("s_barrier" ::: "memory");
-      if (k == 0) {
+      if (u == 0) {
         if (!qready) load_query(cur);
         prepare_query<1>(qt, qraw, a.query_dtype, logit_scale, cur.ctx, ql, gqa, a.sliding_window, c16, wave * 16);
       }
-      if (k == cur.n - 1) {
+      if (u == units - 1) {
         qready = has_nxt && nxt.n > 0;
         if (qready) load_query(nxt);
       }
-      // Stages of chunks up to gc + S - 1 are free (their previous chunks
-      // are at most gc - 1).
-      while (iok && issued < gc + S) {
-        issue_chunk(issued % S);
+      // Stages of units up to gu + S - 1 are free (their previous units are
+      // at most gu - 1).
+      while (iok && issued < gu + S) {
+        issue_unit(issued % S);
         ++issued;
       }
-      compute_chunk<1, PER_TOKEN>(st, qt, (const LDS_AS unsigned char*)smem + (gc % S) * kStageBytes, krow, grp, c16,
-                                  cur.tb0 + k * kChunk);
-      ++gc;
+      const LDS_AS unsigned char* sb = (const LDS_AS unsigned char*)smem + (gu % S) * kUnitBytes;
+      const LDS_AS unsigned char* const sks[kUnit] = {sb, sb + kStageBytes};
+      const int tb0 = cur.tb0 + u * (kUnit * kChunk);
+      const int tbs[kUnit] = {tb0, kUnit * u + 1 < cur.n ? tb0 + kChunk : kFarToken};
+      f32x4 la[kUnit][1], lb[kUnit][1];
+#pragma unroll
+      for (int ch = 0; ch < kUnit; ++ch) chunk_logits<1>(qt, sks[ch], krow, grp, la[ch], lb[ch]);
+      chunk_softmax_pv<1, PER_TOKEN, kUnit>(st, qt, la, lb, sks, grp, c16, tbs);
+      ++gu;
     }
     // ---- the piece is complete: this wave's columns ----
     const float vfin = PER_TOKEN ? st.vsmax : v_tensor_scale;
@@ -1957,9 +2019,9 @@ hipError_t dispatch_coop_nw(const pa_fp8_stream_args& a, unsigned grid, hipStrea
 // blocks run on four waves, the fourth computing only masked columns).
 int coop_waves(int eq) { return eq <= 32 ? 2 : 4; }
 
-// Resident cooperative workgroups per CU (LDS: kCoopStages chunk stages
-// per workgroup; registers: three waves per SIMD).
-int coop_per_cu(int nw) { return nw == 2 ? 4 : 3; }
+// Resident cooperative workgroups per CU (LDS: kCoopStages unit stages of
+// up to 17 KiB per workgroup; registers: three waves per SIMD).
+int coop_per_cu(int) { return 3; }
 
 // One launch of the per-wave (<= 16 columns) or cooperative kernel.
 template <bool WL>
