@@ -342,8 +342,8 @@ __device__ __forceinline__ void chunk_logits(const QueryTile<NCG>& q, const LDS_
   }
 }
 
-// Softmax and PV of NCH chunks (raw logits la/lb, stages sk, first tokens
-// tb) folded into the online softmax as one step: one running-maximum
+// Softmax and PV of NCH chunks (raw logits la/lb, stages sk, per-token K
+// scales at ssc and V scales 32 floats later, first tokens tb) folded into the online softmax as one step: one running-maximum
 // update, one accumulator rescale and one value-scale update for all of
 // them.  A chunk whose first token lies past every visible range is fully
 // masked (its value bytes are zeroed, so its LDS content does not matter).
@@ -352,7 +352,8 @@ __device__ __forceinline__ void chunk_logits(const QueryTile<NCG>& q, const LDS_
 template <int NCG, bool PER_TOKEN, int NCH>
 __device__ __forceinline__ void chunk_softmax_pv(WaveState<NCG>& s, const QueryTile<NCG>& q,
                                                  const f32x4 (&la)[NCH][NCG], const f32x4 (&lb)[NCH][NCG],
-                                                 const LDS_AS unsigned char* const (&sk)[NCH], int grp, int c16,
+                                                 const LDS_AS unsigned char* const (&sk)[NCH],
+                                                 const LDS_AS float* const (&ssc)[NCH], int grp, int c16,
                                                  const int (&tb)[NCH]) {
   // Tokens j in [jlo, jhi) of this lane's 8 (tb + 8*grp + j) are visible to
   // some column; edge chunks zero the value bytes and scales of the others,
@@ -367,7 +368,7 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<NCG>& s, const QueryT
     jhi[ch] = pa_min(pa_max(q.hi_all - tok0, jlo[ch]), 8);
   }
   auto scales = [&](int ch, int off, float (&x)[8]) {
-    const LDS_AS float* ss = (const LDS_AS float*)(sk[ch] + kKBytes + kVBytes) + off + 8 * grp;
+    const LDS_AS float* ss = ssc[ch] + off + 8 * grp;
     const f32x4 x0 = *(const LDS_AS f32x4*)ss;
     const f32x4 x1 = *(const LDS_AS f32x4*)(ss + 4);
 #pragma unroll
@@ -501,8 +502,9 @@ __device__ __forceinline__ void compute_chunk(WaveState<NCG>& s, const QueryTile
   f32x4 la[1][NCG], lb[1][NCG];
   chunk_logits<NCG>(q, sk, krow, grp, la[0], lb[0]);
   const LDS_AS unsigned char* const sks[1] = {sk};
+  const LDS_AS float* const sss[1] = {(const LDS_AS float*)(sk + kKBytes + kVBytes)};
   const int tbs[1] = {tb};
-  chunk_softmax_pv<NCG, PER_TOKEN, 1>(s, q, la, lb, sks, grp, c16, tbs);
+  chunk_softmax_pv<NCG, PER_TOKEN, 1>(s, q, la, lb, sks, sss, grp, c16, tbs);
 }
 
 // Workgroup geometry.  A workgroup covers `slots_per_workgroup`
@@ -1407,10 +1409,12 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
     void* __restrict__ output) {
   static_assert(NW == 2 || NW == 4, "two or four waves share a chunk");
   constexpr int S = kCoopStages;
-  constexpr int kStageBytes = kKBytes + kVBytes + (PER_TOKEN ? kScaleBytes : 0);  // one chunk
-  constexpr int kUnitBytes = kUnit * kStageBytes;
+  // Unit stage: [chunk 0 keys, values][chunk 1 keys, values][per-token
+  // scales: chunk 0 K, V, chunk 1 K, V (128 B each)].
+  constexpr int kStageBytes = kKBytes + kVBytes;  // one chunk
+  constexpr int kUnitBytes = kUnit * kStageBytes + (PER_TOKEN ? kUnit * kScaleBytes : 0);
   constexpr int kDmaPerWave = 8 / NW;  // of a chunk's 8 one-KiB key/value loads
-  constexpr int kLoads = kUnit * (kDmaPerWave + (PER_TOKEN ? 1 : 0));  // per unit
+  constexpr int kLoads = kUnit * kDmaPerWave + (PER_TOKEN ? 1 : 0);  // per unit
   __shared__ __attribute__((aligned(16))) unsigned char smem[S * kUnitBytes];
 
   const int tid = threadIdx.x;
@@ -1464,6 +1468,36 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
   // in its piece, which is nxt when iw (else cur).
   int itb = 0, ih = 0, ilast = 0, irem = 0, iw = 0;
   int64_t ibt = 0;
+  // This wave's share of every chunk, fixed for the launch: load i = wave *
+  // kDmaPerWave + j of a chunk's eight 1 KiB loads is keys for i < 4 (else
+  // values), 16-token half hh = (i >> 1) & 1, 1 KiB piece q2 = i & 1.  A
+  // wave's loads are all keys or all values, so each chunk costs it one
+  // address (page base + in-page offset) plus per-lane constants.
+  const bool wk = wave < NW / 2;
+  const uint8_t* const rbase = (const uint8_t*)(wk ? a.key_cache : a.value_cache);
+  const int64_t rstride_head = wk ? a.stride_k_head : a.stride_v_head;
+  const int64_t rstride_block = wk ? a.stride_k_block : a.stride_v_block;
+  // In-page offset of a chunk at page slot s0: (s0 >> sh1) << sh2.
+  const int sh1 = (!wk && a.trans_v) ? 4 : 0;
+  const int sh2 = wk ? 4 : (a.trans_v ? 11 : 0);
+  int loff[kDmaPerWave], ldsoff[kDmaPerWave];
+  bool hsel[kDmaPerWave];
+#pragma unroll
+  for (int j = 0; j < kDmaPerWave; ++j) {
+    const int i = wave * kDmaPerWave + j;
+    const int hh = (i >> 1) & 1, q2 = i & 1;
+    hsel[j] = hh != 0;
+    if (BS16)
+      loff[j] = (wk ? koff_lane : lane * 16) + q2 * 1024;
+    else if (wk)
+      loff[j] = hh * 256 + q2 * (4 * bs * 16) + koff_lane;
+    else if (a.trans_v)
+      loff[j] = hh * 2048 + q2 * 1024 + lane * 16;
+    else
+      loff[j] = hh * 16 + q2 * (64 * bs) + voff_plain;
+    ldsoff[j] = (wk ? hh * kKHalf : kKBytes + hh * 2048) + q2 * 1024;
+  }
+  const uint8_t* ibase = rbase;  // rbase + ih * rstride_head
   bool iok = false;
   // Page ids of the next unit (prefetched): its first chunk's (np0, and np1
   // for the chunk's second 16-token page) and its second chunk's (np2, np3),
@@ -1490,6 +1524,7 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
     irem = p.n;
     iw = which;
     iok = true;
+    ibase = rbase + (int64_t)ih * rstride_head;
     fetch_pages();
   };
   if (cur.n > 0)
@@ -1502,48 +1537,29 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
   auto issue_chunk = [&](int st, int sl, int tb, int q0, int q1) {
     const int p0 = clamp_page(q0);
     const int p1 = BS16 ? clamp_page(q1) : p0;
-    const uint8_t* kbase = (const uint8_t*)a.key_cache + (int64_t)ih * a.stride_k_head;
-    const uint8_t* vbase = (const uint8_t*)a.value_cache + (int64_t)ih * a.stride_v_head;
+    const int64_t inpage = BS16 ? 0 : (int64_t)(((tb & (bs - 1)) >> sh1) << sh2);
     LDS_AS unsigned char* sk = (LDS_AS unsigned char*)smem + st * kUnitBytes + sl * kStageBytes;
-    LDS_AS unsigned char* sv = sk + kKBytes;
-    // Load i (0..7): i < 4 keys, else values; half hh = (i >> 1) & 1, 1 KiB piece q2 = i & 1.
 #pragma unroll
     for (int j = 0; j < kDmaPerWave; ++j) {
-      const int i = wave * kDmaPerWave + j;
-      const bool isk = i < 4;
-      const int hh = (i >> 1) & 1, q2 = i & 1;
-      if (BS16) {
-        const int pg = hh ? p1 : p0;
-        if (isk)
-          lds_dma16(kbase + (int64_t)pg * a.stride_k_block + koff_lane + q2 * 1024, sk + hh * kKHalf + q2 * 1024);
-        else
-          lds_dma16(vbase + (int64_t)pg * a.stride_v_block + lane * 16 + q2 * 1024, sv + hh * 2048 + q2 * 1024);
-      } else {
-        const int s0 = tb & (bs - 1);
-        if (isk) {
-          lds_dma16(kbase + (int64_t)p0 * a.stride_k_block + s0 * 16 + hh * 256 + q2 * (4 * bs * 16) + koff_lane,
-                    sk + hh * kKHalf + q2 * 1024);
-        } else if (a.trans_v) {
-          lds_dma16(vbase + (int64_t)p0 * a.stride_v_block + (s0 >> 4) * (kHead * 16) + hh * 2048 + q2 * 1024 +
-                        lane * 16,
-                    sv + hh * 2048 + q2 * 1024);
-        } else {
-          lds_dma16(vbase + (int64_t)p0 * a.stride_v_block + s0 + hh * 16 + q2 * (64 * bs) + voff_plain,
-                    sv + hh * 2048 + q2 * 1024);
-        }
-      }
+      const int pg = (BS16 && hsel[j]) ? p1 : p0;
+      lds_dma16(ibase + (int64_t)pg * rstride_block + inpage + loff[j], sk + ldsoff[j]);
     }
-    if (PER_TOKEN) {
-      // Every wave writes the same 256 bytes of scales: each wave's own
-      // wait then covers them.
-      LDS_AS unsigned char* ss = sv + kVBytes;
-      if (lane < 16) {
-        const int tt = (lane & 7) * 4;
-        const int pg2 = BS16 ? (tt >= 16 ? p1 : p0) : p0;
-        const int sidx = BS16 ? (tt & 15) : (tb & (bs - 1)) + tt;
-        const float* base = (lane < 8 ? key_scale : value_scale) + (int64_t)ih * a.stride_ks_head;
-        lds_dma16(base + (int64_t)pg2 * a.stride_ks_block + sidx, ss);
-      }
+  };
+  // Per-token scales of a unit's two chunks (at tokens tb0, tb1; pages as
+  // issue_chunk) in one load of 32 lanes: lane l carries 4 tokens' scales,
+  // chunk l / 16, keys or values by bit 3.  Every wave loads them, so each
+  // wave's own wait covers them.
+  auto issue_scales = [&](int st, int tb0, int tb1) {
+    LDS_AS unsigned char* ss = (LDS_AS unsigned char*)smem + st * kUnitBytes + kUnit * kStageBytes;
+    if (lane < 32) {
+      const int c = lane >> 4;
+      const int tt = (lane & 7) * 4;
+      const int tb = c ? tb1 : tb0;
+      const int q0 = c ? np2 : np0, q1 = c ? np3 : np1;
+      const int pg = clamp_page(BS16 ? (tt >= 16 ? q1 : q0) : q0);
+      const int sidx = BS16 ? (tt & 15) : (tb & (bs - 1)) + tt;
+      const float* base = ((lane & 8) ? value_scale : key_scale) + (int64_t)ih * a.stride_ks_head;
+      lds_dma16(base + (int64_t)pg * a.stride_ks_block + sidx, ss);
     }
   };
   // The next unit: the next two chunks of the issue piece, or its last one
@@ -1551,8 +1567,10 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
   // side masks it).
   auto issue_unit = [&](int st) {
     const bool two = irem >= 2;
+    const int tb1 = two ? itb + kChunk : itb;
     issue_chunk(st, 0, itb, np0, np1);
-    issue_chunk(st, 1, two ? itb + kChunk : itb, np2, np3);
+    issue_chunk(st, 1, tb1, np2, np3);
+    if (PER_TOKEN) issue_scales(st, itb, tb1);
     itb += two ? 2 * kChunk : kChunk;
     irem -= two ? 2 : 1;
     if (irem > 0)
@@ -1639,12 +1657,14 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
       }
       const LDS_AS unsigned char* sb = (const LDS_AS unsigned char*)smem + (gu % S) * kUnitBytes;
       const LDS_AS unsigned char* const sks[kUnit] = {sb, sb + kStageBytes};
+      const LDS_AS float* const sss[kUnit] = {(const LDS_AS float*)(sb + kUnit * kStageBytes),
+                                              (const LDS_AS float*)(sb + kUnit * kStageBytes + kScaleBytes)};
       const int tb0 = cur.tb0 + u * (kUnit * kChunk);
       const int tbs[kUnit] = {tb0, kUnit * u + 1 < cur.n ? tb0 + kChunk : kFarToken};
       f32x4 la[kUnit][1], lb[kUnit][1];
 #pragma unroll
       for (int ch = 0; ch < kUnit; ++ch) chunk_logits<1>(qt, sks[ch], krow, grp, la[ch], lb[ch]);
-      chunk_softmax_pv<1, PER_TOKEN, kUnit>(st, qt, la, lb, sks, grp, c16, tbs);
+      chunk_softmax_pv<1, PER_TOKEN, kUnit>(st, qt, la, lb, sks, sss, grp, c16, tbs);
       ++gu;
     }
     // ---- the piece is complete: this wave's columns ----
