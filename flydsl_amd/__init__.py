@@ -4,7 +4,10 @@ Public API (same names and signatures as the reference):
   * kernels/pa_decode_fp8.py: :func:`pa_decode_ps_launch`,
     :func:`get_recommended_splits`, :func:`get_pa_metadata`;
   * kernels/fused_rope_cache_kernel.py: :func:`build_fused_rope_cache_module`
-    (the KV-cache writer that produces the cache the decode reads).
+    (the KV-cache writer that produces the cache the decode reads);
+  * kernels/qk_norm_rope_quant.py: :func:`flydsl_qk_norm_rope_quant`,
+    :func:`compile_flydsl_qk_norm_rope_quant` (fused RMSNorm + GPT-J RoPE +
+    fp8 quant of Q and the KV row).
 Device work runs in the hand-written gfx950 HIP kernels of ``libpa_fp8.so``
 (C ABI: ``include/pa_fp8.h``).
 """
@@ -17,6 +20,7 @@ from .pa_decode import (  # noqa: F401
     pa_decode_ps_launch,
     prepare_pa_decode,
 )
+from .qk_norm_rope import compile_flydsl_qk_norm_rope_quant, flydsl_qk_norm_rope_quant  # noqa: F401
 from .rope_cache import build_fused_rope_cache_module  # noqa: F401
 
 __all__ = [
@@ -27,4 +31,6 @@ __all__ = [
     "PreparedDecode",
     "KV_COMPUTE_BLOCK",
     "build_fused_rope_cache_module",
+    "flydsl_qk_norm_rope_quant",
+    "compile_flydsl_qk_norm_rope_quant",
 ]

@@ -51,6 +51,7 @@ EXPORTED_SYMBOLS = (
     "pa_fp8_worklist_sizes",
     "pa_fp8_plan_worklist",
     "pa_fp8_rope_cache",
+    "pa_fp8_qk_norm_rope_quant",
 )
 
 _i32 = ctypes.c_int32
@@ -265,6 +266,35 @@ class RopeCacheArgs(ctypes.Structure):
 _LIB: Optional[ctypes.CDLL] = None
 
 
+class QkNormRopeArgs(ctypes.Structure):
+    """Mirror of ``pa_qk_norm_rope_args`` (field order matters)."""
+
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("q", _vp),
+        ("kv", _vp),
+        ("q_weight", _vp),
+        ("kv_weight", _vp),
+        ("cos_cache", _vp),
+        ("sin_cache", _vp),
+        ("positions", _vp),
+        ("q_out", _vp),
+        ("kv_out", _vp),
+        ("q_scale", _vp),
+        ("kv_scale", _vp),
+        ("stride_q_tok", _i64),
+        ("stride_kv_tok", _i64),
+        ("num_tokens", ctypes.c_int32),
+        ("num_q_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("rope_head_dim", ctypes.c_int32),
+        ("max_pos", ctypes.c_int32),
+        ("quant", ctypes.c_int32),
+        ("group_size", ctypes.c_int32),
+        ("scale_e8m0", ctypes.c_int32),
+    ]
+
+
 class LibraryNotBuilt(RuntimeError):
     pass
 
@@ -312,6 +342,8 @@ def load(path: Optional[str] = None) -> ctypes.CDLL:
     lib.pa_fp8_plan_worklist.restype = ctypes.c_int
     lib.pa_fp8_rope_cache.argtypes = [ctypes.POINTER(RopeCacheArgs), _vp]
     lib.pa_fp8_rope_cache.restype = ctypes.c_int
+    lib.pa_fp8_qk_norm_rope_quant.argtypes = [ctypes.POINTER(QkNormRopeArgs), _vp]
+    lib.pa_fp8_qk_norm_rope_quant.restype = ctypes.c_int
     if path is None:
         _LIB = lib
     return lib

@@ -11,7 +11,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
-SOURCES = [os.path.join(CSRC, "pa_fp8.hip"), os.path.join(CSRC, "rope_cache.hip")]
+SOURCES = [os.path.join(CSRC, n) for n in ("pa_fp8.hip", "rope_cache.hip", "qk_norm_rope.hip")]
 OUTPUT = os.path.join(HERE, "libpa_fp8.so")
 ARCH = "gfx950"
 

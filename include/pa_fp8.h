@@ -374,6 +374,55 @@ typedef struct {
 
 int pa_fp8_rope_cache(const pa_fp8_rope_cache_args* args, void* hip_stream);
 
+/*
+ * Fused per-token RMSNorm + GPT-J RoPE + optional fp8 quantisation of the
+ * query heads and the single KV row of each token.  Replaces the launcher
+ * compiled by compile_flydsl_qk_norm_rope_quant
+ * (kernels/qk_norm_rope_quant.py:709-736; kernel :259-640, launch :650-686)
+ * as flydsl_qk_norm_rope_quant (:739-955) calls it.
+ *
+ *   q          [T, H, D]  bf16, token stride stride_q_tok, heads dense
+ *   kv         [T, D]     bf16, token stride stride_kv_tok
+ *   q_weight   [D] bf16 or NULL (unweighted Q); kv_weight [D] bf16
+ *   cos_cache, sin_cache [max_pos, RD / 2] bf16, contiguous
+ *   positions  [T] int64, read as their low 32-bit words; outside
+ *              [0, max_pos) the rotation reads zeros
+ *   q_out [T, H, D], kv_out [T, D], dense: bf16, or fp8 e4m3fn when quant
+ *   q_scale [T, H, NG], kv_scale [T, NG], NG = D / group_size: float32, or
+ *              uint8 e8m0 exponents when scale_e8m0 (quant only)
+ * Row statistic rstd = rsqrt(mean(x^2) + 1e-6) over the unweighted row; the
+ * last RD elements are rotated in pairs (2k, 2k + 1) by cos/sin[pos, k].
+ * D in {128, 256, 512}; RD even, a multiple of D / 64, at most D;
+ * group_size a multiple of D / 64 dividing D, D / 64 lanes per group a
+ * power of two.  T * (H + 1) < 2^31.
+ */
+typedef struct {
+  int32_t abi_version; /* = PA_FP8_ABI_VERSION */
+  const void* q;
+  const void* kv;
+  const void* q_weight;
+  const void* kv_weight;
+  const void* cos_cache;
+  const void* sin_cache;
+  const int64_t* positions;
+  void* q_out;
+  void* kv_out;
+  void* q_scale;
+  void* kv_scale;
+  int64_t stride_q_tok;
+  int64_t stride_kv_tok;
+  int32_t num_tokens;
+  int32_t num_q_heads;
+  int32_t head_dim;
+  int32_t rope_head_dim;
+  int32_t max_pos;
+  int32_t quant;
+  int32_t group_size;
+  int32_t scale_e8m0;
+} pa_qk_norm_rope_args;
+
+int pa_fp8_qk_norm_rope_quant(const pa_qk_norm_rope_args* args, void* hip_stream);
+
 /* Library identification and error names. */
 const char* pa_fp8_version(void);
 const char* pa_fp8_error_string(int code);

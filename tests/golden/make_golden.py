@@ -16,6 +16,8 @@ Files:
                 two get_pa_metadata work lists
   rope_cache.npz  three KV-cache writer calls: inputs and the oracle's
                 Q_out / K_out / key and value caches, as raw bits
+  qk_norm_rope.npz  four fused RMSNorm + GPT-J RoPE (+ fp8 quant) calls:
+                inputs as raw bits and the oracle's outputs and scales
 """
 
 from __future__ import annotations
@@ -28,6 +30,7 @@ import numpy as np
 import torch
 
 from oracle import plan, worklist
+from oracle import qk_norm_rope as qnr
 from oracle import rope_cache as rc
 from tests._cases import make_case, torch_oracle
 
@@ -182,11 +185,62 @@ def rope_fixture() -> dict:
     return arrays
 
 
+# name -> (T, H, D, RD, quant, group_size, scale_dtype, q_weighted, max_pos, kv row stride)
+QKNR_CASES = {
+    "v4_bf16": (6, 4, 512, 64, False, None, "fp32", False, 32, 512),
+    "v4_fp8_g128_qw": (5, 3, 512, 64, True, 128, "fp32", True, 32, 640),
+    "d256_fp8_e8m0_g64": (4, 2, 256, 128, True, 64, "e8m0", False, 16, 256),
+    "d128_full_rope_oob": (7, 1, 128, 128, True, 32, "fp32", True, 8, 192),
+}
+
+
+def qknr_inputs(name: str) -> dict:
+    """Seeded inputs of one fused RMSNorm + RoPE call (CPU tensors; kv is a
+    [T, D] view with the case's row stride)."""
+    T, H, D, RD, quant, G, sd, qw, max_pos, kv_stride = QKNR_CASES[name]
+    g = torch.Generator().manual_seed(sum(map(ord, name)))
+    cos, sin = qnr.rope_table(max_pos, RD)
+    kv_wide = torch.randn(T, kv_stride, generator=g).to(torch.bfloat16)
+    pos = torch.randint(0, max_pos, (T,), generator=g, dtype=torch.int64)
+    if name.endswith("oob"):
+        pos[0], pos[1] = -1, max_pos
+    return dict(
+        q=torch.randn(T, H, D, generator=g).to(torch.bfloat16),
+        kv=kv_wide[:, :D],
+        kv_weight=(1.0 + 0.3 * torch.randn(D, generator=g)).to(torch.bfloat16),
+        q_weight=(1.0 + 0.3 * torch.randn(D, generator=g)).to(torch.bfloat16) if qw else None,
+        cos_cache=cos,
+        sin_cache=sin,
+        positions=pos,
+    )
+
+
+def qknr_reference(name: str, inp: dict):
+    T, H, D, RD, quant, G, sd, qw, max_pos, kv_stride = QKNR_CASES[name]
+    return qnr.qk_norm_rope_quant(inp["q"], inp["kv"], inp["kv_weight"], inp["cos_cache"], inp["sin_cache"],
+                                  inp["positions"], num_q_heads=H, head_dim=D, rope_head_dim=RD,
+                                  q_weight=inp["q_weight"], quant=quant, quant_group_size=G, scale_dtype=sd)
+
+
+def qknr_fixture() -> dict:
+    arrays = {}
+    for name in QKNR_CASES:
+        inp = qknr_inputs(name)
+        for key, t in inp.items():
+            if t is not None:
+                arrays[f"{name}/{key}"] = _bits(t) if t.is_floating_point() else t.numpy()
+        for key, a in zip(("q_out", "kv_out", "q_scale", "kv_scale"), qknr_reference(name, inp)):
+            if a is not None:
+                arrays[f"{name}/{key}"] = np.ascontiguousarray(a)
+    return arrays
+
+
 def main() -> None:
     torch.set_num_threads(1)
     np.savez_compressed(os.path.join(HERE, "decode.npz"), **decode_fixture())
     np.savez_compressed(os.path.join(HERE, "planner.npz"), **planner_fixture())
     np.savez_compressed(os.path.join(HERE, "rope_cache.npz"), **rope_fixture())
+    np.savez_compressed(os.path.join(HERE, "qk_norm_rope.npz"), **qknr_fixture())
 
 
 if __name__ == "__main__":

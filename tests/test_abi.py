@@ -64,6 +64,21 @@ def test_null_args_rejected_without_gpu():
     assert lib.pa_fp8_rope_cache(ctypes.byref(ra), None) == -1  # no tensors
     ra.num_tokens = 0
     assert lib.pa_fp8_rope_cache(ctypes.byref(ra), None) == 0  # nothing to do
+    assert lib.pa_fp8_qk_norm_rope_quant(None, None) == -1
+    qa = _lib.QkNormRopeArgs()
+    qa.abi_version = 99
+    assert lib.pa_fp8_qk_norm_rope_quant(ctypes.byref(qa), None) == -8
+    qa.abi_version = _lib.ABI_VERSION
+    qa.head_dim, qa.rope_head_dim, qa.max_pos, qa.num_tokens, qa.num_q_heads = 64, 0, 8, 1, 1
+    assert lib.pa_fp8_qk_norm_rope_quant(ctypes.byref(qa), None) == -2  # one wave per row needs D in {128, 256, 512}
+    qa.head_dim, qa.rope_head_dim = 512, 63
+    assert lib.pa_fp8_qk_norm_rope_quant(ctypes.byref(qa), None) == -6  # odd rotary width
+    qa.rope_head_dim, qa.quant, qa.group_size = 64, 1, 48
+    assert lib.pa_fp8_qk_norm_rope_quant(ctypes.byref(qa), None) == -6  # group does not divide the row
+    qa.group_size = 128
+    assert lib.pa_fp8_qk_norm_rope_quant(ctypes.byref(qa), None) == -1  # no tensors
+    qa.num_tokens = 0
+    assert lib.pa_fp8_qk_norm_rope_quant(ctypes.byref(qa), None) == 0  # nothing to do
 
 
 def test_stream_worker_counts():
@@ -71,8 +86,8 @@ def test_stream_worker_counts():
     assert _lib.stream_workers(256, 1, 4, True) == 2048
     assert _lib.stream_workers(256, 1, 8, False) == 1024
     assert _lib.stream_workers(256, 4, 4, True) == 1024
-    # 17..64 columns: cooperative workgroups (4 per CU for 2-wave, 3 for 4-wave groups)
-    assert _lib.stream_workers(256, 4, 8, True) == 1024
+    # 17..64 columns: cooperative workgroups (3 per CU, by the LDS of their ring)
+    assert _lib.stream_workers(256, 4, 8, True) == 768
     assert _lib.stream_workers(256, 4, 16, True) == 768
     with pytest.raises(RuntimeError):
         _lib.stream_workers(256, 4, 32, True)  # 128 columns: not supported
@@ -84,7 +99,8 @@ def test_stream_worker_counts():
                                           (_lib.ReduceArgs, "pa_fp8_reduce_args"),
                                           (_lib.StreamArgs, "pa_fp8_stream_args"),
                                           (_lib.WorklistReduceArgs, "pa_fp8_worklist_reduce_args"),
-                                          (_lib.RopeCacheArgs, "pa_fp8_rope_cache_args")])
+                                          (_lib.RopeCacheArgs, "pa_fp8_rope_cache_args"),
+                                          (_lib.QkNormRopeArgs, "pa_qk_norm_rope_args")])
 def test_struct_layout_matches_header(tmp_path, struct, cname):
     fields = [f for f, _ in struct._fields_]
     src = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){",

@@ -116,3 +116,19 @@ def test_rope_cache_outputs_reproduce(name):
         assert np.array_equal(have, want), key
     for key, t in zip(("q_out", "k_out", "key_cache_out", "value_cache_out"), mg.rope_reference(name, inp)):
         assert np.array_equal(mg._bits(t), fx[f"{name}/{key}"]), key
+
+
+@pytest.mark.parametrize("name", list(mg.QKNR_CASES))
+def test_qk_norm_rope_outputs_reproduce(name):
+    fx = load("qk_norm_rope.npz")
+    inp = mg.qknr_inputs(name)
+    for key, t in inp.items():
+        if t is not None:
+            want = fx[f"{name}/{key}"]
+            have = mg._bits(t) if t.is_floating_point() else t.numpy()
+            assert (have == want.reshape(have.shape)).all(), f"{name}: input {key}"
+    for key, a in zip(("q_out", "kv_out", "q_scale", "kv_scale"), mg.qknr_reference(name, inp)):
+        if a is None:
+            assert f"{name}/{key}" not in fx
+        else:
+            assert np.array_equal(a, fx[f"{name}/{key}"]), f"{name}: {key}"
