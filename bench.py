@@ -52,7 +52,8 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--config", default="c2_llama8b",
                    help="c1_tiny|c2_llama8b|c3_ragged|c4_window|c5_mtp|all (decode), "
-                        "rope_decode_llama8b|rope_prefill_llama8b (KV-cache writer)")
+                        "rope_decode_llama8b|rope_prefill_llama8b (KV-cache writer), "
+                        "qknr_prefill_v4|qknr_decode_v4 (fused RMSNorm + GPT-J RoPE + fp8 quant)")
     p.add_argument("--seed", type=int, default=7)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
@@ -420,6 +421,134 @@ def run_rope_config(name: str, args) -> dict:
     return line
 
 
+def qknr_cpu_baseline(case_gpu, cfg, budget_s: float) -> dict:
+    """Time the fused RMSNorm + RoPE CPU oracle over growing samples of the
+    workload's tokens until the budget is spent; scaled to GB/s of
+    algorithmic bytes."""
+    import torch
+
+    from flydsl_amd import workloads
+    from oracle import qk_norm_rope as qnr
+
+    per_tok = workloads.qknr_bytes(cfg) / cfg.num_tokens
+    c = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in case_gpu.items()}
+    done, spent, n = 0, 0.0, 8
+    while spent < budget_s and done < cfg.num_tokens:
+        m = min(n, cfg.num_tokens - done)
+        sl = slice(done, done + m)
+        t0 = time.perf_counter()
+        qnr.qk_norm_rope_quant(c["q"][sl], c["kv"][sl], c["kv_weight"], c["cos_cache"], c["sin_cache"],
+                               c["positions"][sl], num_q_heads=cfg.num_q_heads, head_dim=cfg.head_dim,
+                               rope_head_dim=cfg.rope_head_dim, quant=cfg.quant, quant_group_size=cfg.group_size,
+                               scale_dtype=cfg.scale_dtype)
+        spent += time.perf_counter() - t0
+        done += m
+        n *= 2
+    return {
+        "value": round(done * per_tok / spent / 1e9, 4),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{done} of {cfg.num_tokens} tokens of {cfg.name} through the NumPy oracle "
+        f"(oracle/qk_norm_rope.py qk_norm_rope_quant), {spent:.1f} s; "
+        f"host {cpu_model()}, affinity {len(os.sched_getaffinity(0))} cpus, os.cpu_count {os.cpu_count()}",
+    }
+
+
+def run_qknr_config(name: str, args) -> dict:
+    """One fused RMSNorm + RoPE (+ fp8) call per step, prepared as a serving
+    loop makes it; inputs rotate over copies so no step reads what the last
+    one left in the Infinity Cache."""
+    import torch
+
+    from flydsl_amd import workloads
+    from flydsl_amd.qk_norm_rope import FP8_DTYPE, compile_flydsl_qk_norm_rope_quant
+
+    cfg = workloads.QKNR_CONFIGS[name]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    case = workloads.build_qknr_inputs(cfg, device=dev, seed=args.seed)
+    algo = workloads.qknr_bytes(cfg)
+    T, H, D = cfg.num_tokens, cfg.num_q_heads, cfg.head_dim
+    in_bytes = sum(case[k].numel() * case[k].element_size() for k in ("q", "kv"))
+    if args.copies:
+        copies = args.copies
+    elif in_bytes > 64 << 20:
+        copies = max(2, math.ceil(2 * MALL_BYTES / in_bytes) + 1)
+    else:
+        copies = 1
+    ins = [(case["q"], case["kv"])]
+    for _ in range(copies - 1):
+        ins.append(tuple(t.clone() for t in ins[0]))
+    odt = FP8_DTYPE if cfg.quant else torch.bfloat16
+    q_out = torch.empty((T, H, D), dtype=odt, device=dev)
+    kv_out = torch.empty((T, D), dtype=odt, device=dev)
+    ng = D // cfg.group_size
+    sdt = torch.float32 if cfg.scale_dtype == "fp32" else torch.uint8
+    q_scale = torch.empty((T, H, ng), dtype=sdt, device=dev)
+    kv_scale = torch.empty((T, ng), dtype=sdt, device=dev)
+    launcher = compile_flydsl_qk_norm_rope_quant(num_q_heads=H, head_dim=D, rope_head_dim=cfg.rope_head_dim,
+                                                 quant=cfg.quant, group_size=cfg.group_size,
+                                                 scale_dtype=cfg.scale_dtype, q_weighted=False)
+    calls = [launcher.prepare(q.view(T, H, D), kv, case["kv_weight"], case["kv_weight"], case["cos_cache"],
+                              case["sin_cache"], case["positions"], q_out, kv_out, q_scale, kv_scale, kv.stride(0), T)
+             for q, kv in ins]
+    for i in range(max(3, args.warmup)):
+        calls[i % copies].launch()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(args.steps):
+        calls[i % copies].launch()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    value = algo / (ms * 1e-3) / 1e9
+    line = {
+        "metric": "fused RMSNorm + GPT-J RoPE + fp8 quant HBM GB/s (% of peak) + us/call",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_step": round(ms * 1e3, 2),
+        "pct_of_peak": round(100.0 * value / PEAK_HBM_GBPS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 Q/KV, 10000-base GPT-J rotary tables, random positions)",
+        "config": {
+            "workload": name,
+            "num_tokens": T,
+            "num_query_heads": H,
+            "head_dim": D,
+            "rope_head_dim": cfg.rope_head_dim,
+            "quant": f"fp8 e4m3fn, {cfg.scale_dtype} scale per {cfg.group_size}" if cfg.quant else "bf16",
+            "q_weighted": False,
+            "algorithmic_bytes_per_call": algo,
+            "input_copies_rotated": copies,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "pa_qk_norm_rope_kernel",
+            "kernels_per_step": 1,
+            "achieved": round(value, 2),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(value / PEAK_HBM_GBPS, 4),
+            "traffic": load_traffic(name),
+            "kernel_us": round(ms * 1e3, 2),
+            "algorithmic_bytes": algo,
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = qknr_cpu_baseline(case, cfg, args.cpu_seconds)
+    return line
+
+
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -431,7 +560,12 @@ def main():
         return
     names = ["c2_llama8b", "c3_ragged", "c4_window", "c5_mtp"] if args.config == "all" else [args.config]
     for n in names:
-        line = run_rope_config(n, args) if n.startswith("rope_") else run_config(n, args)
+        if n.startswith("rope_"):
+            line = run_rope_config(n, args)
+        elif n.startswith("qknr_"):
+            line = run_qknr_config(n, args)
+        else:
+            line = run_config(n, args)
         print(json.dumps(line), flush=True)
 
 

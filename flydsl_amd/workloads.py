@@ -255,3 +255,58 @@ def rope_bytes(cfg: RopeCacheConfig) -> int:
     read = (qh + 2 * kh) * d * 2 + 2 * (d // 2) * 2 + 2 * 4
     write = (qh + kh) * d * 2 + 2 * kh * d
     return cfg.num_tokens * (read + write)
+
+
+@dataclasses.dataclass(frozen=True)
+class QkNormRopeConfig:
+    name: str
+    num_tokens: int
+    num_q_heads: int
+    head_dim: int
+    rope_head_dim: int
+    quant: bool
+    group_size: int
+    scale_dtype: str
+    max_pos: int = 8192
+
+
+# DeepSeek-V4-shaped rows (the reference kernel's shape: D 512, RD 64), 16
+# query heads per GPU plus the KV row, weightless Q, fp8 out with float32
+# scales per 128 elements:
+#   prefill: 8192 tokens;  decode: 64 tokens (one per sequence)
+QKNR_CONFIGS: Dict[str, QkNormRopeConfig] = {
+    "qknr_prefill_v4": QkNormRopeConfig("qknr_prefill_v4", 8192, 16, 512, 64, True, 128, "fp32"),
+    "qknr_decode_v4": QkNormRopeConfig("qknr_decode_v4", 64, 16, 512, 64, True, 128, "fp32"),
+}
+
+
+def build_qknr_inputs(cfg: QkNormRopeConfig, device="cpu", seed: int = 0) -> dict:
+    """Inputs of one fused RMSNorm + RoPE call: bf16 Q [T, H*D] and KV [T, D]
+    N(0,1), a KV weight around 1, 10000-base GPT-J cos/sin tables [max_pos,
+    RD/2] and random int64 positions."""
+    device = torch.device(device)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    T, H, d, rd = cfg.num_tokens, cfg.num_q_heads, cfg.head_dim, cfg.rope_head_dim
+    inv = 1.0 / (10000.0 ** (torch.arange(0, rd, 2, dtype=torch.float64) / rd))
+    ang = torch.arange(cfg.max_pos, dtype=torch.float64)[:, None] * inv[None, :]
+    return {
+        "config": cfg,
+        "q": torch.randn(T, H * d, generator=gen, device=device).to(torch.bfloat16),
+        "kv": torch.randn(T, d, generator=gen, device=device).to(torch.bfloat16),
+        "kv_weight": (1.0 + 0.1 * torch.randn(d, generator=gen, device=device)).to(torch.bfloat16),
+        "cos_cache": torch.cos(ang).to(torch.bfloat16).to(device),
+        "sin_cache": torch.sin(ang).to(torch.bfloat16).to(device),
+        "positions": torch.randint(0, cfg.max_pos, (T,), generator=gen, device=device, dtype=torch.int64),
+    }
+
+
+def qknr_bytes(cfg: QkNormRopeConfig) -> int:
+    """Algorithmic HBM bytes of one call: every row read (bf16) and written
+    (fp8 or bf16), its scales, and per token one position and one cos and
+    one sin row (the per-channel weight is read once)."""
+    rows = cfg.num_q_heads + 1
+    out_el = 1 if cfg.quant else 2
+    ng = cfg.head_dim // cfg.group_size if cfg.quant else 0
+    scale_el = 4 if cfg.scale_dtype == "fp32" else 1
+    per_tok = rows * (cfg.head_dim * 2 + cfg.head_dim * out_el + ng * scale_el) + 8 + 2 * (cfg.rope_head_dim // 2) * 2
+    return cfg.num_tokens * per_tok + cfg.head_dim * 2
