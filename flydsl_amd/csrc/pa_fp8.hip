@@ -317,8 +317,15 @@ __device__ __forceinline__ void prepare_query(QueryTile<NCG>& q, const i32x4 (&q
     q.vis_hi[cg] = hi;
   }
   // lo and hi grow with qi: the extremes come from the first and last query.
-  pa_plan_visible(ctx, 0, ql, W, &q.lo_all, &q.hi_min);
-  pa_plan_visible(ctx, ql - 1, ql, W, &q.lo_max, &q.hi_all);
+  // They are wave-uniform (readfirstlane states it), so the per-chunk
+  // interior / edge tests are scalar compares and scalar branches.
+  int lo_all, hi_min, lo_max, hi_all;
+  pa_plan_visible(ctx, 0, ql, W, &lo_all, &hi_min);
+  pa_plan_visible(ctx, ql - 1, ql, W, &lo_max, &hi_all);
+  q.lo_all = __builtin_amdgcn_readfirstlane(lo_all);
+  q.hi_min = __builtin_amdgcn_readfirstlane(hi_min);
+  q.lo_max = __builtin_amdgcn_readfirstlane(lo_max);
+  q.hi_all = __builtin_amdgcn_readfirstlane(hi_all);
 }
 
 // QK^T of one chunk: raw logits of the lane's 8 tokens (two 16-token
@@ -441,8 +448,9 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<NCG>& s, const QueryT
 #pragma unroll
         for (int j = 0; j < 8; ++j) lg[ch][j] = (j >= jl && j < jh) ? lg[ch][j] : kNegInf;
       }
-      cmax = fmaxf(cmax, fmaxf(fmaxf(fmaxf(lg[ch][0], lg[ch][1]), fmaxf(lg[ch][2], lg[ch][3])),
-                               fmaxf(fmaxf(lg[ch][4], lg[ch][5]), fmaxf(lg[ch][6], lg[ch][7]))));
+      // a linear chain, which the compiler folds into v_max3_f32
+#pragma unroll
+      for (int j = 0; j < 8; ++j) cmax = fmaxf(cmax, lg[ch][j]);
     }
     cmax = max_over_groups(cmax) * post;  // post > 0: -inf stays -inf
     const float mnew = fmaxf(s.m2[cg], cmax);
