@@ -52,6 +52,10 @@ EXPORTED_SYMBOLS = (
     "pa_fp8_plan_worklist",
     "pa_fp8_rope_cache",
     "pa_fp8_qk_norm_rope_quant",
+    "pa_fp8_mla_decode",
+    "pa_fp8_mla_reduce",
+    "pa_fp8_mla_plan_sizes",
+    "pa_fp8_mla_plan",
 )
 
 _i32 = ctypes.c_int32
@@ -295,6 +299,49 @@ class QkNormRopeArgs(ctypes.Structure):
     ]
 
 
+class MlaDecodeArgs(ctypes.Structure):
+    """Mirror of ``pa_mla_decode_args`` (field order matters)."""
+
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("query", _vp),
+        ("kv_buffer", _vp),
+        ("kv_page_indices", _vp),
+        ("work_indptr", _vp),
+        ("work_info", _vp),
+        ("final_output", _vp),
+        ("split_output", _vp),
+        ("split_lse", _vp),
+        ("num_pages", _i64),
+        ("num_page_indices", ctypes.c_int32),
+        ("num_rows", ctypes.c_int32),
+        ("num_workers", ctypes.c_int32),
+        ("num_works", ctypes.c_int32),
+        ("num_partial", ctypes.c_int32),
+        ("softmax_scale", ctypes.c_float),
+        ("precise_p", ctypes.c_int32),
+    ]
+
+
+class MlaReduceArgs(ctypes.Structure):
+    """Mirror of ``pa_mla_reduce_args`` (field order matters)."""
+
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("split_output", _vp),
+        ("split_lse", _vp),
+        ("reduce_indptr", _vp),
+        ("reduce_final_map", _vp),
+        ("reduce_partial_map", _vp),
+        ("final_output", _vp),
+        ("final_lse", _vp),
+        ("num_groups", ctypes.c_int32),
+        ("num_partial", ctypes.c_int32),
+        ("num_partial_map", ctypes.c_int32),
+        ("num_rows", ctypes.c_int32),
+    ]
+
+
 class LibraryNotBuilt(RuntimeError):
     pass
 
@@ -344,6 +391,15 @@ def load(path: Optional[str] = None) -> ctypes.CDLL:
     lib.pa_fp8_rope_cache.restype = ctypes.c_int
     lib.pa_fp8_qk_norm_rope_quant.argtypes = [ctypes.POINTER(QkNormRopeArgs), _vp]
     lib.pa_fp8_qk_norm_rope_quant.restype = ctypes.c_int
+    lib.pa_fp8_mla_decode.argtypes = [ctypes.POINTER(MlaDecodeArgs), _vp]
+    lib.pa_fp8_mla_decode.restype = ctypes.c_int
+    lib.pa_fp8_mla_reduce.argtypes = [ctypes.POINTER(MlaReduceArgs), _vp]
+    lib.pa_fp8_mla_reduce.restype = ctypes.c_int
+    lib.pa_fp8_mla_plan_sizes.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int),
+                                          ctypes.POINTER(ctypes.c_int)]
+    lib.pa_fp8_mla_plan_sizes.restype = ctypes.c_int
+    lib.pa_fp8_mla_plan.argtypes = [_vp, _vp] + [ctypes.c_int] * 4 + [_vp] * 5 + [ctypes.POINTER(ctypes.c_int)] * 2
+    lib.pa_fp8_mla_plan.restype = ctypes.c_int
     if path is None:
         _LIB = lib
     return lib
@@ -423,3 +479,36 @@ def plan_worklist(context_lengths, num_kv_heads: int, query_group_size: int, que
     if n < 0:
         check(n, "pa_fp8_plan_worklist")
     return n, out
+
+
+def mla_plan_sizes(num_rows: int, num_workers: int):
+    mw, mp = ctypes.c_int(), ctypes.c_int()
+    check(load().pa_fp8_mla_plan_sizes(num_rows, num_workers, mw, mp), "pa_fp8_mla_plan_sizes")
+    return mw.value, mp.value
+
+
+def mla_plan(qo_indptr, kv_indptr, num_workers: int):
+    """Host MLA work list (numpy int32 arrays); returns (num_works, num_groups,
+    num_partials, dict)."""
+    import numpy as np
+
+    qo = np.ascontiguousarray(np.asarray(qo_indptr, dtype=np.int32))
+    kv = np.ascontiguousarray(np.asarray(kv_indptr, dtype=np.int32))
+    B = int(qo.shape[0]) - 1
+    rows = int(qo[-1] - qo[0]) if B >= 0 else 0
+    max_works, max_partials = mla_plan_sizes(rows, num_workers)
+    out = {
+        "work_indptr": np.zeros(num_workers + 1, np.int32),
+        "work_info": np.zeros((max(max_works, 1), 8), np.int32),
+        "reduce_indptr": np.zeros(rows + 1, np.int32),
+        "reduce_final_map": np.zeros((max(rows, 1), 2), np.int32),
+        "reduce_partial_map": np.zeros(max(max_partials, 1), np.int32),
+    }
+    ng, npart = ctypes.c_int(), ctypes.c_int()
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    n = int(load().pa_fp8_mla_plan(ptr(qo), ptr(kv), B, num_workers, max(max_works, 1), max(max_partials, 1),
+                                   ptr(out["work_indptr"]), ptr(out["work_info"]), ptr(out["reduce_indptr"]),
+                                   ptr(out["reduce_final_map"]), ptr(out["reduce_partial_map"]), ng, npart))
+    if n < 0:
+        check(n, "pa_fp8_mla_plan")
+    return n, ng.value, npart.value, out

@@ -1,0 +1,628 @@
+// MLA (multi-head latent attention) fp8 decode for MI355X (gfx950): the
+// persistent decode kernel, its log-sum-exp reduce, the host work-list
+// planner and their C ABI (pa_fp8.h).
+//
+// Shape (kernels/mla_fwd_decode_m16x8_fp8_fp8.py:41-60): 128 query heads
+// share one latent kv head; a token's key is its whole 576-byte fp8 row
+// (512 latent + 64 rope dims) and its value is the first 512 bytes of the
+// same row; page size 1.  Per token the decode does 128 x 1088 x 2 FLOP on
+// 576 bytes, 484 FLOP/B -- just below the fp8 MFMA ridge of MI355X
+// (5.0 PFLOP/s / 8 TB/s = 625 FLOP/B), so both the matrix cores and HBM
+// must run near their peaks.
+//
+// Work decomposition.  One 256-thread workgroup per worker (grid = number
+// of workers, one per CU); it walks its works (work_indptr / work_info) and
+// each work's kv range in 128-token blocks.  The four waves split the heads
+// (wave w: heads 32w .. 32w+31) and share each block through LDS: wave w
+// DMAs tokens 32w .. 32w+31 of the block (gfx950 global_load_lds, 16 B per
+// lane) into one of two 72 KiB stages while the block before is computed.
+//
+// LDS image of a stage: [4 token groups of 32][36 column units of 16 B]
+// [32 tokens][16 B].  Each DMA instruction of a wave fills two column units
+// of its 32 tokens, so every lane keeps one token (one page index) for the
+// whole block, and both the key reads (16 consecutive tokens of one unit)
+// and the transposed value reads cover whole 256-byte runs.
+//
+// Arithmetic, all on v_mfma_scale_f32_16x16x128_f8f6f4 (e4m3fn operands,
+// unit scales):
+//   * S^T = K Q^T per 16-token tile: A = 16 key rows x 128 dims (two 16-byte
+//     LDS reads), B = Q^T of 16 heads, held in registers for the work; 4
+//     latent blocks + 1 rope block (its upper 64 k-slots zero);
+//   * the result lane (c, g) = (l % 16, l / 16) holds tokens 4g .. 4g+3 of
+//     the tile for head c, which is exactly the B-operand slot order the
+//     value product needs: dword T of P^T = the four probabilities of tile T;
+//   * O^T = V^T P^T per 32 value dims: ds_read_b64_tr_b8 (gfx950 LDS
+//     transpose read) gives lane (c, g) four tokens 16T+4g .. 16T+4g+3 of
+//     value dims d0+c (low dword) and d0+16+c (high dword), i.e. the A
+//     operands of two 16-dim row tiles with the same token order as P^T.
+// The O^T accumulators are 32 heads x 512 dims per wave (256 registers).
+// Softmax is base 2 with a lazy rescale: the reference maximum of a head
+// moves only when a block's maximum exceeds it by more than 8, so p <= 256
+// stays inside e4m3fn and the 256-register rescale runs on the first block
+// of a work and rarely after.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mla_plan.h"
+#include "pa_fp8.h"
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+#define LDS_AS __attribute__((address_space(3)))
+
+constexpr int kHeads = 128;
+constexpr int kQkDim = 576;
+constexpr int kVDim = 512;
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kBlock = MLA_PLAN_BLOCK;       // tokens per LDS stage
+constexpr int kUnitBytes = 32 * 16;         // one 16-byte column unit of a 32-token group
+constexpr int kGroupBytes = 32 * kQkDim;     // one wave's 32 tokens
+constexpr int kStageBytes = kBlock * kQkDim; // 73728
+constexpr int kDmaPerWave = kQkDim / 32;     // 18 instructions of 1 KiB
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.69314718055994531f;
+constexpr float kNegInf = -__builtin_inff();
+
+static_assert(kGroupBytes * 4 == kStageBytes, "four 32-token groups per stage");
+static_assert(kUnitBytes * (kQkDim / 16) == kGroupBytes, "36 units per group");
+
+// Value product into accumulators pinned to AGPRs, with e8m0 block scales
+// (sa for the values: unit, sb for the probabilities of the lane's head and
+// 32-token group).  The 256 accumulator registers of a wave fill the AGPR
+// half of the register file; queries, logits and operands stay in VGPRs,
+// which the compiler's own register-class choice for MFMA results does not
+// achieve here.  The accumulate chain (same destination, same opcode back
+// to back) is dependency-checked by the hardware; the only VALU reads of
+// the accumulators (the epilogue) follow agpr_settle().
+template <bool FIRST>
+__device__ __forceinline__ void pv_mfma(f32x4& acc, const i32x8& a, const i32x8& b, int sa, int sb) {
+  if (FIRST)
+    asm volatile("s_nop 1\n\tv_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, 0, %3, %4" : "=&a"(acc) : "v"(a), "v"(b), "v"(sa), "v"(sb));
+  else
+    asm volatile("s_nop 1\n\tv_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4" : "+a"(acc) : "v"(a), "v"(b), "v"(sa), "v"(sb));
+}
+// Key product into logits pinned to VGPRs (first: srcC = 0).  The logits
+// are read by VALU only after logits_settle().
+template <bool FIRST>
+__device__ __forceinline__ void qk_mfma(f32x4& acc, const i32x8& a, const i32x8& b) {
+  if (FIRST)
+    asm volatile("s_nop 1\n\tv_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "v"(b));
+  else
+    asm volatile("s_nop 1\n\tv_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+}
+template <bool DUMMY = false>
+__device__ __forceinline__ void qk_rope_mfma(f32x4& acc, const i32x8& a, const i32x8& b, int sa, int sb) {
+  asm volatile("s_nop 1\n\tv_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4" : "+v"(acc) : "v"(a), "v"(b), "v"(sa), "v"(sb));
+}
+// The compiler does not know that the inline-asm MFMAs are MFMAs, so the
+// hazards it would cover are covered here (s_nop n waits n + 1 states):
+//   * VALU write of an operand -> MFMA read: 2 wait states, the s_nop 1 in
+//     front of every MFMA above;
+//   * MFMA result -> first VALU read: logits_settle() ties the logits to a
+//     24-state wait (as in/out operands, so no read can be scheduled ahead
+//     of it), agpr_settle() does the same before the accumulator reads.
+__device__ __forceinline__ void logits_settle(f32x4 (&s)[4][2]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
+               : "+v"(s[0][0]), "+v"(s[0][1]), "+v"(s[1][0]), "+v"(s[1][1]), "+v"(s[2][0]), "+v"(s[2][1]),
+                 "+v"(s[3][0]), "+v"(s[3][1]));
+}
+// Orders the probability packing before the value product.
+template <bool PRECISE>
+__device__ __forceinline__ void probs_ready(i32x8 (&phi)[2], i32x8 (&plo)[2]) {
+  if (PRECISE)
+    asm volatile("" : "+v"(phi[0]), "+v"(phi[1]), "+v"(plo[0]), "+v"(plo[1]));
+  else
+    asm volatile("" : "+v"(phi[0]), "+v"(phi[1]));
+}
+// Accumulator tile -> VGPRs through explicit v_accvgpr_read (opaque to the
+// compiler, so the epilogue's scaling cannot be hoisted ahead of its
+// stores and keep every tile live at once).
+__device__ __forceinline__ f32x4 read_acc(const f32x4& acc) {
+  f32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(r[i]) : "a"(acc[i]));
+  return r;
+}
+__device__ __forceinline__ void agpr_settle() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
+
+__device__ __forceinline__ void lds_dma16(const void* gsrc, LDS_AS void* ldst) {
+  __builtin_amdgcn_global_load_lds(gsrc, ldst, 16, 0, 2);
+}
+
+constexpr int vmcnt_only(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | (7 << 4) | (15 << 8); }
+
+__device__ __forceinline__ uint32_t pack4_fp8(float a, float b, float c, float d) {
+  int r = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  r = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, r, true);
+  return (uint32_t)r;
+}
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// Reductions over lanes c, c+16, c+32, c+48 (one head across the four
+// 16-lane groups), VALU permlane swaps.
+__device__ __forceinline__ float max_over_groups(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_over_groups(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Max over lanes l and l ^ 16 (lane groups {0,1} and {2,3}).
+__device__ __forceinline__ float max_over_pair(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// Value of lane l ^ 32.
+__device__ __forceinline__ int other_half_wave(int v) { return __shfl_xor(v, 32, 64); }
+
+// One work record, clamped into range; all fields wave-uniform.
+struct Work {
+  int qo;       // query row
+  int pql;      // partial row, or -1: final output
+  int kv0, kv1; // positions in kv_page_indices
+  int nblk;     // 128-token blocks (1 for an empty range)
+};
+
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__device__ __forceinline__ Work load_work(const pa_mla_decode_args& a, int wi) {
+  const int32_t* w = a.work_info + 8 * (int64_t)wi;
+  Work r;
+  r.pql = uni(w[1]);
+  r.qo = uni(w[2]);
+  r.kv0 = uni(w[4]);
+  r.kv1 = uni(w[5]);
+  r.qo = min(max(r.qo, 0), a.num_rows - 1);
+  if (r.pql >= a.num_partial) r.pql = a.num_partial - 1;
+  if (r.pql < 0) r.pql = -1;
+  r.kv0 = min(max(r.kv0, 0), a.num_page_indices);
+  r.kv1 = min(max(r.kv1, r.kv0), a.num_page_indices);
+  const int len = r.kv1 - r.kv0;
+  r.nblk = len > 0 ? (len + kBlock - 1) / kBlock : 1;
+  return r;
+}
+
+// Walks the (work, block) units of one worker.
+struct Cursor {
+  int wi, blk;
+  Work w;
+};
+
+__device__ __forceinline__ bool valid(const Cursor& c, int we) { return c.wi < we; }
+
+__device__ __forceinline__ void advance(const pa_mla_decode_args& a, Cursor& c, int we) {
+  if (c.wi >= we) return;
+  if (++c.blk < c.w.nblk) return;
+  c.blk = 0;
+  if (++c.wi < we) c.w = load_work(a, c.wi);
+}
+
+// Page of this lane's token (32w + l % 32 of the block) for unit c.
+__device__ __forceinline__ int unit_page(const pa_mla_decode_args& a, const Cursor& c, int w, int lane) {
+  if (c.w.kv1 <= c.w.kv0) return 0;
+  int pos = c.w.kv0 + c.blk * kBlock + 32 * w + (lane & 31);
+  pos = min(pos, c.w.kv1 - 1);
+  return a.kv_page_indices[pos];
+}
+
+// DMA of one wave's 32 tokens of a block into stage `st`.
+__device__ __forceinline__ void issue_block(const pa_mla_decode_args& a, LDS_AS unsigned char* stage, int w,
+                                           int lane, int page) {
+  page = min(max(page, 0), (int)(a.num_pages - 1));
+  const unsigned char* src =
+      (const unsigned char*)a.kv_buffer + (int64_t)page * kQkDim + 16 * (lane >> 5);
+  LDS_AS unsigned char* dst = stage + w * kGroupBytes;
+#pragma unroll
+  for (int n = 0; n < kDmaPerWave; ++n) lds_dma16(src + 32 * n, dst + 1024 * n);
+}
+
+// Q^T B operands of the wave's two 16-head tiles for query row qo: slot
+// order per latent block kb: 16 dims at 128kb + 16g, then 16 at
+// 128kb + 64 + 16g; the rope block's 16 dims 512 + 16g sit in both halves
+// of its operand (with the key's rope dims likewise doubled and a B scale
+// of 1/2, which is exact).
+struct QTile {
+  i32x8 b[2][4];  // latent blocks
+  i32x4 r[2];     // rope dims 512 + 16g .. +15
+};
+
+__device__ __forceinline__ void load_query(const pa_mla_decode_args& a, int qo, int w, int c, int g, QTile& q) {
+#pragma unroll
+  for (int ht = 0; ht < 2; ++ht) {
+    const unsigned char* row =
+        (const unsigned char*)a.query + ((int64_t)qo * kHeads + 32 * w + 16 * ht + c) * kQkDim + 16 * g;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const i32x4 lo = *(const i32x4*)(row + 128 * kb);
+      const i32x4 hi = *(const i32x4*)(row + 128 * kb + 64);
+      q.b[ht][kb] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+    q.r[ht] = *(const i32x4*)(row + 512);
+  }
+}
+
+// O^T += V^T P^T over one 128-token block held at stage `sb`: per 32 value
+// dims, eight transpose reads give the A operands of two 16-dim row tiles.
+template <bool FIRST, bool PRECISE>
+__device__ __forceinline__ void pv_block(const LDS_AS unsigned char* sb, f32x4 (&o)[16][2][2], const i32x8 (&phi)[2],
+                                         const i32x8 (&plo)[2], const int (&sbs)[2], const int (&sbl)[2], int sa,
+                                         int vbase) {
+  // Software pipelined by hand (the reads of block db + 1 are issued before
+  // the MFMAs of block db); scheduling barriers keep the compiler from
+  // hoisting further reads, which would cost registers.
+  i32x8 va[2][2];
+  auto load = [&](int db, i32x8(&dst)[2]) {
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const i32x2 r = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (LDS_AS i32x2*)(sb + k * kGroupBytes + (2 * db + rt) * kUnitBytes + vbase));
+        dst[rt][2 * k] = r[0];
+        dst[rt][2 * k + 1] = r[1];
+      }
+  };
+  load(0, va[0]);
+#pragma unroll
+  for (int db = 0; db < 16; ++db) {
+    if (db + 1 < 16) load(db + 1, va[(db + 1) & 1]);
+#pragma unroll
+    for (int ht = 0; ht < 2; ++ht)
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        pv_mfma<FIRST>(o[db][rt][ht], va[db & 1][rt], phi[ht], sa, sbs[ht]);
+        if (PRECISE) pv_mfma<false>(o[db][rt][ht], va[db & 1][rt], plo[ht], sa, sbl[ht]);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <bool PRECISE>
+__global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_mla_decode_args a) {
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[2 * kStageBytes];
+  LDS_AS unsigned char* lds = (LDS_AS unsigned char*)lds_raw;
+
+  const int lane = threadIdx.x & 63;
+  const int w = uni(threadIdx.x >> 6);
+  const int c = lane & 15, g = lane >> 4;
+
+  int ws = uni(a.work_indptr[blockIdx.x]);
+  int we = uni(a.work_indptr[blockIdx.x + 1]);
+  ws = min(max(ws, 0), a.num_works);
+  we = min(max(we, ws), a.num_works);
+  if (ws >= we) return;
+
+  const float scale2 = a.softmax_scale * kLog2e;
+
+  // Unit cursors: cur (computed now), c1 (DMA issued this step), c2 (page
+  // index prefetched this step).
+  Cursor cur;
+  cur.wi = ws;
+  cur.blk = 0;
+  cur.w = load_work(a, ws);
+  Cursor c1 = cur;
+  advance(a, c1, we);
+  Cursor c2 = c1;
+  advance(a, c2, we);
+
+  QTile q;
+  load_query(a, cur.w.qo, w, c, g, q);
+  issue_block(a, lds, w, lane, unit_page(a, cur, w, lane));
+  int pg1 = valid(c1, we) ? unit_page(a, c1, w, lane) : 0;
+
+  // O^T accumulators: [32-dim block][16-dim row tile][head tile].
+  f32x4 o[16][2][2];
+  float m0[2] = {0.f, 0.f};      // reference exponent of each head (set on a work's first block)
+  float lsum[2] = {0.f, 0.f};    // this lane's share of the denominator, in units of 2^m0
+
+  // Lane bases inside a stage.  Keys: token row 16T + c, unit 8kb + g
+  // (+4 for the upper 64 dims).  Values (transpose reads): lanes c < 8
+  // address tile 2k, lanes c >= 8 tile 2k+1, row 4g + (c / 2) % 4 of the
+  // tile, unit 2db + rt, byte 8 (c % 2); the low dword then holds tile 2k
+  // and the high dword tile 2k+1 of value dim 32db + 16rt + c.
+  const int kbase = c * 16 + g * kUnitBytes;
+  const int vbase = (c >> 3) * 256 + (4 * g + ((c >> 1) & 3)) * 16 + (c & 1) * 8;
+  const int unit_scale = 127;  // e8m0 2^0
+  const int half_scale = 126;  // e8m0 2^-1
+
+  int st = 0;
+  while (true) {
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    asm volatile("s_barrier" ::: "memory");
+    if (valid(c1, we)) {
+      issue_block(a, lds + (st ^ 1) * kStageBytes, w, lane, pg1);
+      if (valid(c2, we)) pg1 = unit_page(a, c2, w, lane);
+    }
+    const LDS_AS unsigned char* sb = lds + st * kStageBytes;
+
+    // ---- S^T = K Q^T and softmax, in two halves of four 16-token tiles ----
+    // The probabilities go into the value product with e8m0 block scales.
+    // v_mfma_scale_f32_16x16x128_f8f6f4 scales k-slots in blocks of 32: the
+    // low 16 bytes (tiles 0..3) of lane groups {0,1} form block 0, of {2,3}
+    // block 1, the high 16 bytes (tiles 4..7) blocks 2 and 3, and lane
+    // group j supplies the scale of block j.  So each half of the block has
+    // one exponent per lane pair (g, g^1) and head: e = ceil(pair max), the
+    // probabilities p = 2^(x - e) sit at the top of the fp8 range, and the
+    // MFMA multiplies them back by 2^(e - m0).
+    const bool first = cur.blk == 0;
+    const bool last = cur.blk == cur.w.nblk - 1;
+    const int len = cur.w.kv1 - cur.w.kv0 - cur.blk * kBlock;  // valid tokens from this block on
+    i32x8 phi[2], plo[2];
+    int kexp[2][2];  // [half][head tile]: block exponent - m0
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      f32x4 s[4][2];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int T = 4 * half + t;
+        const LDS_AS unsigned char* kr = sb + (T >> 1) * kGroupBytes + (T & 1) * 256 + kbase;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          const i32x4 lo = *(const LDS_AS i32x4*)(kr + kb * 8 * kUnitBytes);
+          const i32x4 hi = *(const LDS_AS i32x4*)(kr + (kb * 8 + 4) * kUnitBytes);
+          const i32x8 ka = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          if (kb == 0) {
+            qk_mfma<true>(s[t][0], ka, q.b[0][kb]);
+            qk_mfma<true>(s[t][1], ka, q.b[1][kb]);
+          } else {
+            qk_mfma<false>(s[t][0], ka, q.b[0][kb]);
+            qk_mfma<false>(s[t][1], ka, q.b[1][kb]);
+          }
+        }
+        // rope: both operands carry the 16 dims twice; the B scale 2^-1
+        // undoes the doubling exactly
+        const i32x4 kr4 = *(const LDS_AS i32x4*)(kr + 32 * kUnitBytes);
+        const i32x8 ka = {kr4[0], kr4[1], kr4[2], kr4[3], kr4[0], kr4[1], kr4[2], kr4[3]};
+#pragma unroll
+        for (int ht = 0; ht < 2; ++ht) {
+          const i32x8 qb = {q.r[ht][0], q.r[ht][1], q.r[ht][2], q.r[ht][3],
+                            q.r[ht][0], q.r[ht][1], q.r[ht][2], q.r[ht][3]};
+          qk_rope_mfma(s[t][ht], ka, qb, unit_scale, half_scale);
+        }
+      }
+      logits_settle(s);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        s[t][0] *= scale2;
+        s[t][1] *= scale2;
+      }
+      if (len < (half + 1) * (kBlock / 2)) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool keep = 16 * (4 * half + t) + 4 * g + i < len;
+            s[t][0][i] = keep ? s[t][0][i] : kNegInf;
+            s[t][1][i] = keep ? s[t][1][i] : kNegInf;
+          }
+      }
+#pragma unroll
+      for (int ht = 0; ht < 2; ++ht) {
+        float x = kNegInf;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) x = fmaxf(x, fmaxf(fmaxf(s[t][ht][0], s[t][ht][1]), fmaxf(s[t][ht][2], s[t][ht][3])));
+        if (half == 0 && first) {
+          const float hm = max_over_groups(x);
+          m0[ht] = hm == kNegInf ? 0.f : __builtin_ceilf(hm) + 40.f;
+        }
+        const float xp = max_over_pair(x);
+        // exponents beyond m0 +- 127 leave the e8m0 range
+        const float eh = fminf(fmaxf(xp == kNegInf ? m0[ht] : __builtin_ceilf(xp), m0[ht] - 127.f), m0[ht] + 127.f);
+        kexp[half][ht] = (int)(eh - m0[ht]);
+        float acc = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          float pv[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            pv[i] = __builtin_amdgcn_exp2f(s[t][ht][i] - eh);
+            acc += pv[i];
+          }
+          const uint32_t h = pack4_fp8(pv[0], pv[1], pv[2], pv[3]);
+          phi[ht][4 * half + t] = (int)h;
+          if (PRECISE) {
+            const f32x2 b0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, false);
+            const f32x2 b1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, true);
+            // low terms carried x16 (scale 2^-4 in their MFMA), clear of
+            // the e4m3fn subnormal range
+            plo[ht][4 * half + t] = (int)pack4_fp8(16.f * (pv[0] - b0[0]), 16.f * (pv[1] - b0[1]),
+                                                   16.f * (pv[2] - b1[0]), 16.f * (pv[3] - b1[1]));
+          }
+        }
+        lsum[ht] += __builtin_ldexpf(acc, kexp[half][ht]);
+      }
+    }
+    // Scale VGPR of lane group g = exponent of block g: (half 0, pair {0,1}),
+    // (half 0, pair {2,3}), (half 1, pair {0,1}), (half 1, pair {2,3}).
+    int sbv[2][2];  // [hi, lo term][head tile]
+#pragma unroll
+    for (int ht = 0; ht < 2; ++ht) {
+      const int t0 = other_half_wave(kexp[0][ht]);  // group 1 <- group 3
+      const int t1 = other_half_wave(kexp[1][ht]);  // group 2 <- group 0
+      const int k = g == 0 ? kexp[0][ht] : g == 1 ? t0 : g == 2 ? t1 : kexp[1][ht];
+      sbv[0][ht] = k + 127;
+      sbv[1][ht] = max(k + 127 - 4, 0);
+    }
+
+    // The next work's queries load during the value product (the logits
+    // are dead by then, the query registers free since this block's QK).
+    if (last && valid(c1, we)) load_query(a, c1.w.qo, w, c, g, q);
+
+    // ---- O^T += V^T P^T: 16 blocks of 32 value dims ----
+    probs_ready<PRECISE>(phi, plo);
+    if (first)
+      pv_block<true, PRECISE>(sb, o, phi, plo, sbv[0], sbv[1], unit_scale, vbase);
+    else
+      pv_block<false, PRECISE>(sb, o, phi, plo, sbv[0], sbv[1], unit_scale, vbase);
+
+    if (last) {
+      // ---- epilogue: normalise and store the work's rows ----
+      // One accumulator tile at a time (a scheduling barrier per tile): the
+      // scaled tiles would otherwise all be formed before the stores.
+      agpr_settle();
+      const bool direct = cur.w.pql < 0;
+#pragma unroll
+      for (int ht = 0; ht < 2; ++ht) {
+        const float l = sum_over_groups(lsum[ht]);
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        const int head = 32 * w + 16 * ht + c;
+        const int64_t prow = direct ? (int64_t)cur.w.qo * kHeads + head : (int64_t)cur.w.pql * kHeads + head;
+        unsigned char* orow = direct ? (unsigned char*)a.final_output + prow * (kVDim * 2)
+                                     : (unsigned char*)(a.split_output + prow * kVDim);
+#pragma unroll
+        for (int db = 0; db < 16; ++db)
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt) {
+            const f32x4 v = read_acc(o[db][rt][ht]) * inv;
+            const int d = 32 * db + 16 * rt + 4 * g;
+            if (direct) {
+              const uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
+              const uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
+              *(i32x2*)(orow + 2 * d) = i32x2{(int)lo, (int)hi};
+            } else {
+              *(f32x4*)(orow + 4 * d) = v;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        if (!direct && g == 0) a.split_lse[prow] = l > 0.f ? (m0[ht] + __builtin_amdgcn_logf(l)) * kLn2 : kNegInf;
+        lsum[ht] = 0.f;
+      }
+    }
+
+    if (!valid(c1, we)) break;
+    cur = c1;
+    c1 = c2;
+    advance(a, c2, we);
+    st ^= 1;
+  }
+}
+
+// One wave per (group, head): lane l merges value dims 8l .. 8l+7.
+__global__ __launch_bounds__(256) void mla_fp8_reduce_kernel(const pa_mla_reduce_args a) {
+  const int gidx = blockIdx.x;
+  const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  int p0 = a.reduce_indptr[gidx], p1 = a.reduce_indptr[gidx + 1];
+  p0 = min(max(p0, 0), a.num_partial_map);
+  p1 = min(max(p1, p0), a.num_partial_map);
+  if (p0 >= p1) return;
+  const int row0 = min(max(a.reduce_final_map[2 * gidx], 0), a.num_rows);
+  const int row1 = min(max(a.reduce_final_map[2 * gidx + 1], row0), a.num_rows);
+  for (int row = row0; row < row1; ++row) {
+    const int r = row - row0;
+    float mx = kNegInf;
+    for (int i = p0; i < p1; ++i) {
+      const int pr = a.reduce_partial_map[i] + r;
+      if (pr < 0 || pr >= a.num_partial) continue;
+      mx = fmaxf(mx, a.split_lse[(int64_t)pr * kHeads + head]);
+    }
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float wsum = 0.f;
+    if (mx != kNegInf) {
+      for (int i = p0; i < p1; ++i) {
+        const int pr = a.reduce_partial_map[i] + r;
+        if (pr < 0 || pr >= a.num_partial) continue;
+        const int64_t prow = (int64_t)pr * kHeads + head;
+        const float wgt = __expf(a.split_lse[prow] - mx);
+        const f32x4* src = (const f32x4*)(a.split_output + prow * kVDim + 8 * lane);
+        const f32x4 x0 = src[0], x1 = src[1];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          acc[k] += wgt * x0[k];
+          acc[4 + k] += wgt * x1[k];
+        }
+        wsum += wgt;
+      }
+    }
+    const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+    uint32_t packed[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      packed[k] = f32_to_bf16_bits(acc[2 * k] * inv) | (f32_to_bf16_bits(acc[2 * k + 1] * inv) << 16);
+    unsigned char* orow = (unsigned char*)a.final_output + ((int64_t)row * kHeads + head) * (kVDim * 2);
+    *(i32x4*)(orow + 16 * lane) = i32x4{(int)packed[0], (int)packed[1], (int)packed[2], (int)packed[3]};
+    if (a.final_lse && lane == 0)
+      a.final_lse[(int64_t)row * kHeads + head] = wsum > 0.f ? mx + __logf(wsum) : kNegInf;
+  }
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+extern "C" int pa_fp8_mla_decode(const pa_mla_decode_args* a, void* stream) {
+  if (!a) return PA_ERR_NULL_ARG;
+  if (a->abi_version != PA_FP8_ABI_VERSION) return PA_ERR_ABI;
+  if (a->num_workers < 0 || a->num_works < 0 || a->num_rows < 0 || a->num_partial < 0 ||
+      a->num_page_indices < 0 || a->num_pages < 0)
+    return PA_ERR_SHAPE;
+  if (a->num_workers == 0 || a->num_works == 0) return 0;
+  if (a->num_rows == 0 || a->num_pages == 0) return PA_ERR_SHAPE;
+  if (a->num_pages > 0x7fffffffLL) return PA_ERR_SHAPE;
+  if (!a->query || !a->kv_buffer || !a->work_indptr || !a->work_info || !a->final_output) return PA_ERR_NULL_ARG;
+  if (a->num_page_indices > 0 && !a->kv_page_indices) return PA_ERR_NULL_ARG;
+  if (a->num_partial > 0 && (!a->split_output || !a->split_lse)) return PA_ERR_NULL_ARG;
+  if (!aligned16(a->query) || !aligned16(a->kv_buffer) || !aligned16(a->final_output) ||
+      (a->split_output && !aligned16(a->split_output)))
+    return PA_ERR_ALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  if (a->precise_p)
+    hipLaunchKernelGGL(mla_fp8_decode_kernel<true>, dim3(a->num_workers), dim3(kThreads), 0, s, *a);
+  else
+    hipLaunchKernelGGL(mla_fp8_decode_kernel<false>, dim3(a->num_workers), dim3(kThreads), 0, s, *a);
+  return (int)hipGetLastError();
+}
+
+extern "C" int pa_fp8_mla_reduce(const pa_mla_reduce_args* a, void* stream) {
+  if (!a) return PA_ERR_NULL_ARG;
+  if (a->abi_version != PA_FP8_ABI_VERSION) return PA_ERR_ABI;
+  if (a->num_groups < 0 || a->num_partial < 0 || a->num_partial_map < 0 || a->num_rows < 0) return PA_ERR_SHAPE;
+  if (a->num_groups == 0) return 0;
+  if (!a->reduce_indptr || !a->reduce_final_map || !a->final_output) return PA_ERR_NULL_ARG;
+  if (a->num_partial > 0 && (!a->split_output || !a->split_lse || !a->reduce_partial_map)) return PA_ERR_NULL_ARG;
+  if (!aligned16(a->final_output) || (a->split_output && !aligned16(a->split_output))) return PA_ERR_ALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(mla_fp8_reduce_kernel, dim3(a->num_groups, kHeads / 4), dim3(256), 0, s, *a);
+  return (int)hipGetLastError();
+}
+
+extern "C" int pa_fp8_mla_plan_sizes(int num_rows, int num_workers, int* max_works, int* max_partials) {
+  if (num_rows < 0 || num_workers <= 0) return PA_ERR_SHAPE;
+  if (!max_works || !max_partials) return PA_ERR_NULL_ARG;
+  mla_plan_sizes(num_rows, num_workers, max_works, max_partials);
+  return 0;
+}
+
+extern "C" int pa_fp8_mla_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, int num_seqs, int num_workers,
+                               int max_works, int max_partials, int32_t* work_indptr, int32_t* work_info,
+                               int32_t* reduce_indptr, int32_t* reduce_final_map, int32_t* reduce_partial_map,
+                               int* num_groups, int* num_partials) {
+  if (!qo_indptr || !kv_indptr || !work_indptr || !reduce_indptr || !num_groups || !num_partials)
+    return PA_ERR_NULL_ARG;
+  if (num_seqs < 0 || num_workers <= 0 || max_works < 0 || max_partials < 0) return PA_ERR_SHAPE;
+  if (max_works > 0 && !work_info) return PA_ERR_NULL_ARG;
+  const int rows = qo_indptr[num_seqs] - qo_indptr[0];
+  if (rows > 0 && !reduce_final_map) return PA_ERR_NULL_ARG;
+  if (max_partials > 0 && !reduce_partial_map) return PA_ERR_NULL_ARG;
+  const int n = mla_plan(qo_indptr, kv_indptr, num_seqs, num_workers, max_works, max_partials, work_indptr,
+                         work_info, reduce_indptr, reduce_final_map, reduce_partial_map, num_groups, num_partials);
+  return n < 0 ? PA_ERR_SHAPE : n;
+}

@@ -423,6 +423,101 @@ typedef struct {
 
 int pa_fp8_qk_norm_rope_quant(const pa_qk_norm_rope_args* args, void* hip_stream);
 
+/*
+ * MLA (multi-head latent attention, DeepSeek-V3 shape) fp8 decode.
+ * Replaces launch_mla_fwd_decode_m16x8_fp8_fp8
+ * (kernels/mla_fwd_decode_m16x8_fp8_fp8.py:2069-2104; kernel :310-2066) as
+ * flydsl_mla_fwd_decode (kernels/mla_fwd_decode.py:57-167) calls it.
+ *
+ *   query        [num_rows, 128, 576] fp8 e4m3fn, dense (576 = 512 latent
+ *                + 64 rope dims)
+ *   kv_buffer    [num_pages, 576] fp8 e4m3fn, dense: page size 1, one kv
+ *                head; the value of a token is the first 512 bytes of its row
+ *   kv_page_indices [num_page_indices] int32
+ *   work_indptr  [num_workers + 1] int32: works of worker w are
+ *                work_indptr[w] .. work_indptr[w+1]
+ *   work_info    [num_works][8] int32: (batch, partial row or -1, query row,
+ *                query row + 1, first position, end position in
+ *                kv_page_indices, 0, heads)
+ *   final_output [num_rows, 128, 512] bf16, written for partial row -1
+ *   split_output [num_partial, 128, 512] float32 and split_lse
+ *                [num_partial, 128] float32, written for partial rows >= 0:
+ *                the normalised partial output and its log-sum-exp
+ *                (natural log of the scaled logits)
+ * Logits are softmax_scale * q.k over all 576 dims; p is rounded to fp8
+ * for the value product (the reference's arithmetic), or split into two
+ * fp8 terms when precise_p is non-zero.  Work fields and page indices out
+ * of range are clamped into range (memory safety, not a result contract).
+ * A work with an empty range writes zeros (and lse -inf).
+ */
+typedef struct {
+  int32_t abi_version; /* = PA_FP8_ABI_VERSION */
+  const void* query;
+  const void* kv_buffer;
+  const int32_t* kv_page_indices;
+  const int32_t* work_indptr;
+  const int32_t* work_info;
+  void* final_output;
+  float* split_output;
+  float* split_lse;
+  int64_t num_pages;
+  int32_t num_page_indices;
+  int32_t num_rows;
+  int32_t num_workers;
+  int32_t num_works;
+  int32_t num_partial;
+  float softmax_scale;
+  int32_t precise_p;
+} pa_mla_decode_args;
+
+int pa_fp8_mla_decode(const pa_mla_decode_args* args, void* hip_stream);
+
+/*
+ * Log-sum-exp merge of the split MLA outputs (replaces aiter's
+ * mla_reduce_v1, called at tests/kernels/test_mla_decode.py:356-365; not
+ * part of the reference).  Group g (0 <= g < num_groups) merges, for each
+ * query row r of reduce_final_map[g] = (row0, row1), the partial rows
+ * reduce_partial_map[i] + (r - row0), i in reduce_indptr[g] ..
+ * reduce_indptr[g+1]; empty groups are skipped.
+ *   out = sum_i w_i o_i / sum_i w_i, w_i = exp(lse_i - max lse)
+ * into final_output [num_rows, 128, 512] bf16 and, when not NULL,
+ * final_lse [num_rows, 128] float32.  Rows and partial rows out of range
+ * are skipped.
+ */
+typedef struct {
+  int32_t abi_version; /* = PA_FP8_ABI_VERSION */
+  const float* split_output;
+  const float* split_lse;
+  const int32_t* reduce_indptr;
+  const int32_t* reduce_final_map;
+  const int32_t* reduce_partial_map;
+  void* final_output;
+  float* final_lse;
+  int32_t num_groups;
+  int32_t num_partial;
+  int32_t num_partial_map;
+  int32_t num_rows;
+} pa_mla_reduce_args;
+
+int pa_fp8_mla_reduce(const pa_mla_reduce_args* args, void* hip_stream);
+
+/*
+ * Host planner of the MLA work list (our own; aiter's get_mla_metadata_v1,
+ * tests/kernels/test_mla_decode.py:274-295, is not part of the reference):
+ * 128-token blocks of every query row dealt to num_workers workers in
+ * contiguous balanced runs.  qo_indptr, kv_indptr [num_seqs + 1] host int32.
+ * Output buffers sized by pa_fp8_mla_plan_sizes (num_rows =
+ * qo_indptr[num_seqs] - qo_indptr[0]); reduce_indptr [num_rows + 1],
+ * reduce_final_map [num_rows][2].  Returns the number of works or a
+ * PA_ERR_* code; *num_groups / *num_partials receive the reduce group and
+ * partial row counts.
+ */
+int pa_fp8_mla_plan_sizes(int num_rows, int num_workers, int* max_works, int* max_partials);
+int pa_fp8_mla_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, int num_seqs, int num_workers,
+                    int max_works, int max_partials, int32_t* work_indptr, int32_t* work_info,
+                    int32_t* reduce_indptr, int32_t* reduce_final_map, int32_t* reduce_partial_map,
+                    int* num_groups, int* num_partials);
+
 /* Library identification and error names. */
 const char* pa_fp8_version(void);
 const char* pa_fp8_error_string(int code);

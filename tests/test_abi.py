@@ -79,6 +79,22 @@ def test_null_args_rejected_without_gpu():
     assert lib.pa_fp8_qk_norm_rope_quant(ctypes.byref(qa), None) == -1  # no tensors
     qa.num_tokens = 0
     assert lib.pa_fp8_qk_norm_rope_quant(ctypes.byref(qa), None) == 0  # nothing to do
+    assert lib.pa_fp8_mla_decode(None, None) == -1
+    assert lib.pa_fp8_mla_reduce(None, None) == -1
+    ma = _lib.MlaDecodeArgs()
+    ma.abi_version = 99
+    assert lib.pa_fp8_mla_decode(ctypes.byref(ma), None) == -8
+    ma.abi_version = _lib.ABI_VERSION
+    assert lib.pa_fp8_mla_decode(ctypes.byref(ma), None) == 0  # no workers: nothing to do
+    ma.num_workers, ma.num_works, ma.num_rows, ma.num_pages = 4, 4, 1, 0
+    assert lib.pa_fp8_mla_decode(ctypes.byref(ma), None) == -6  # no pages to read
+    ma.num_pages = 8
+    assert lib.pa_fp8_mla_decode(ctypes.byref(ma), None) == -1  # no tensors
+    mr = _lib.MlaReduceArgs()
+    mr.abi_version = _lib.ABI_VERSION
+    assert lib.pa_fp8_mla_reduce(ctypes.byref(mr), None) == 0
+    mr.num_groups = 3
+    assert lib.pa_fp8_mla_reduce(ctypes.byref(mr), None) == -1
 
 
 def test_stream_worker_counts():
@@ -100,7 +116,9 @@ def test_stream_worker_counts():
                                           (_lib.StreamArgs, "pa_fp8_stream_args"),
                                           (_lib.WorklistReduceArgs, "pa_fp8_worklist_reduce_args"),
                                           (_lib.RopeCacheArgs, "pa_fp8_rope_cache_args"),
-                                          (_lib.QkNormRopeArgs, "pa_qk_norm_rope_args")])
+                                          (_lib.QkNormRopeArgs, "pa_qk_norm_rope_args"),
+                                          (_lib.MlaDecodeArgs, "pa_mla_decode_args"),
+                                          (_lib.MlaReduceArgs, "pa_mla_reduce_args")])
 def test_struct_layout_matches_header(tmp_path, struct, cname):
     fields = [f for f, _ in struct._fields_]
     src = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){",

@@ -1,0 +1,159 @@
+"""MLA fp8 decode on the GPU against the oracle (oracle/mla.py).
+
+Mirrors tests/kernels/test_mla_decode.py: fp8 query [rows, 128, 576] and
+fp8 KV buffer [pages, 1, 1, 576] from standard normals, pages in random
+order, softmax scale 1/sqrt(576); work list from get_mla_metadata_v1, the
+decode, then mla_reduce_v1.  Each case checks
+  * every work's split output and lse (or, for uncut rows, the final
+    output) against the oracle's per-work attention, and
+  * the final bf16 output and the reduced lse against the oracle's
+    unsplit attention.
+Bar (floating point): the logits are exact (fp8 x fp8 products summed in
+float32), so the error comes from the probabilities carried in fp8 for the
+value product.  With one fp8 term per probability (the reference's
+arithmetic) each p has relative error <= 2^-4, so
+    |out - ref| <= 2^-4 * wabs + 2^-8 * |ref| + 1e-5
+per element, wabs = the softmax-weighted mean of |v| (2^-8 |ref| covers the
+bf16 output); with precise_p (two fp8 terms) 2^-7 * wabs instead of
+2^-4 * wabs (the low term's own rounding is 2^-8 relative, plus the flush of
+low terms below the e4m3fn subnormal range, 2^-9 of the block maximum).  lse within 2e-5 + 1e-5 |lse|.  The reference test's own bar is
+a cosine difference < 3e-2; the tests also assert that, and a much tighter
+cosine difference.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from flydsl_amd.mla_decode import (
+    QK_HEAD_DIM,
+    V_HEAD_DIM,
+    flydsl_mla_fwd_decode,
+    get_mla_metadata_info_v1,
+    get_mla_metadata_v1,
+    mla_reduce_v1,
+)
+from oracle import mla as om
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+FP8 = torch.float8_e4m3fn
+
+
+def make_case(lens, seed, extra_pages=7):
+    g = torch.Generator().manual_seed(seed)
+    B = len(lens)
+    kv_indptr = torch.zeros(B + 1, dtype=torch.int32)
+    kv_indptr[1:] = torch.cumsum(torch.tensor(lens, dtype=torch.int32), 0)
+    total = int(kv_indptr[-1])
+    num_pages = total + extra_pages
+    kv_indices = torch.randperm(num_pages, generator=g)[:total].to(torch.int32)
+    kv = torch.randn(num_pages, 1, 1, QK_HEAD_DIM, generator=g).to(torch.bfloat16).to(FP8)
+    q = torch.randn(B, 128, QK_HEAD_DIM, generator=g).to(torch.bfloat16).to(FP8)
+    qo_indptr = torch.arange(B + 1, dtype=torch.int32)
+    last = torch.ones(B, dtype=torch.int32)
+    return q, kv, qo_indptr, kv_indptr, kv_indices, last
+
+
+def run(lens, seed=0, num_cu=None, precise=False):
+    q, kv, qo_indptr, kv_indptr, kv_indices, last = make_case(lens, seed)
+    B = len(lens)
+    sizes = get_mla_metadata_info_v1(B, 1, 128, FP8, FP8, num_cu=num_cu)
+    bufs = [torch.empty(s, dtype=t, device=DEV) for s, t in sizes]
+    meta, work_indptr, work_info, reduce_indptr, reduce_final_map, reduce_partial_map = bufs
+    get_mla_metadata_v1(qo_indptr.to(DEV), kv_indptr.to(DEV), last.to(DEV), 128, 1, False, meta, work_info,
+                        work_indptr, reduce_indptr, reduce_final_map, reduce_partial_map, kv_granularity=16,
+                        max_seqlen_qo=1, uni_seqlen_qo=1)
+    npart = reduce_partial_map.size(0)
+    out = torch.full((B, 128, V_HEAD_DIM), -1.0, dtype=torch.bfloat16, device=DEV)
+    split_o = torch.full((npart, 1, 128, V_HEAD_DIM), float("nan"), dtype=torch.float32, device=DEV)
+    split_l = torch.full((npart, 1, 128, 1), float("nan"), dtype=torch.float32, device=DEV)
+    final_lse = torch.full((B, 128), float("nan"), dtype=torch.float32, device=DEV)
+    sm = 1.0 / QK_HEAD_DIM ** 0.5
+    qd, kvd, kid = q.to(DEV), kv.to(DEV), kv_indices.to(DEV)
+    print(f"mla case lens={lens[:4]}{'...' if len(lens) > 4 else ''} B={B} seed={seed} num_cu={num_cu} "
+          f"precise={precise}", flush=True)
+    flydsl_mla_fwd_decode(qd, kvd, kid, work_indptr, work_info, out, split_o, split_l, sm, precise_p=precise)
+    torch.cuda.synchronize()
+    split_snapshot = (split_o.clone(), split_l.clone(), out.clone())
+    mla_reduce_v1(split_o, split_l, reduce_indptr, reduce_final_map, reduce_partial_map, 1, out, final_lse)
+    torch.cuda.synchronize()
+    meta_h = meta.cpu().numpy()
+    return dict(q=om.fp8_to_f64(q), kv=om.fp8_to_f64(kv.view(-1, QK_HEAD_DIM)), qo=qo_indptr.numpy(),
+                kvp=kv_indptr.numpy(), kvi=kv_indices.numpy(), sm=sm, out=out.float().cpu().numpy(),
+                lse=final_lse.cpu().numpy(), split=[t.cpu() for t in split_snapshot],
+                work_info=work_info.cpu().numpy(), n=int(meta_h[0]), ng=int(meta_h[1]), npart=int(meta_h[2]))
+
+
+def tolerance(wabs, ref, precise):
+    return (2.0 ** -7 if precise else 2.0 ** -4) * wabs + 2.0 ** -8 * np.abs(ref) + 1e-5
+
+
+def check(r, precise=False):
+    want, want_lse, wabs = om.mla_decode_ref(r["q"], r["kv"], r["qo"], r["kvp"], r["kvi"], r["sm"])
+    tol = tolerance(wabs, want, precise)
+    err = np.abs(r["out"] - want)
+    assert np.all(err <= tol), f"final output: worst excess {np.max(err - tol):.3g} at {np.unravel_index(np.argmax(err - tol), err.shape)}"
+    cos = 1 - 2 * float((r["out"] * want).sum()) / max(float((r["out"] ** 2 + want ** 2).sum()), 1e-12)
+    assert cos < 3e-2  # the reference test's bar
+    assert cos < (1e-5 if precise else 2e-3)
+    # per work: split rows (float32, normalised) or direct rows
+    so, sl, direct_out = r["split"]
+    so = so.numpy()[:, 0]
+    sl = sl.numpy()[:, 0, :, 0]
+    for row, pql, o, l, wa in om.mla_split_ref(r["q"], r["kv"], r["kvi"], r["work_info"], r["n"], r["sm"]):
+        if pql < 0:
+            got = direct_out[row].float().numpy()
+            assert np.all(np.abs(got - o) <= tolerance(wa, o, precise)), f"direct row {row}"
+        else:
+            e = np.abs(so[pql] - o) - tolerance(wa, o, precise)
+            assert np.all(e <= 0), f"split row {pql}: worst excess {e.max():.3g}"
+            fin = np.isfinite(l)
+            assert np.array_equal(fin, np.isfinite(sl[pql]))
+            assert np.all(np.abs(sl[pql][fin] - l[fin]) <= 2e-5 + 1e-5 * np.abs(l[fin])), f"split lse {pql}"
+    # reduced lse for the cut rows
+    cut = sorted({int(w[2]) for w in r["work_info"][: r["n"]] if w[1] >= 0})
+    for row in cut:
+        assert np.all(np.abs(r["lse"][row] - want_lse[row]) <= 2e-5 + 1e-5 * np.abs(want_lse[row])), f"lse row {row}"
+
+
+# the reference test's configurations (tests/kernels/test_mla_decode.py:60-68)
+@pytest.mark.parametrize("batch,ctx", [(1, 63), (1, 64), (1, 128), (4, 2048), (33, 2333), (32, 8192)])
+def test_reference_configs(batch, ctx):
+    check(run([ctx] * batch, seed=batch * 1000003 + ctx))
+
+
+@pytest.mark.parametrize("batch,ctx", [(1, 128), (4, 2048), (33, 2333)])
+def test_precise_probabilities(batch, ctx):
+    check(run([ctx] * batch, seed=7 + ctx, precise=True), precise=True)
+
+
+def test_ragged_with_few_workers():
+    # several works per worker (cross-work prefetch), cut and uncut rows,
+    # partial last blocks of every length class
+    check(run([1, 127, 128, 129, 255, 5000, 77, 640, 2], seed=11, num_cu=3))
+
+
+def test_one_worker_no_splits():
+    check(run([300, 10, 4096, 1], seed=12, num_cu=1))
+
+
+def test_many_small_pieces():
+    # more workers than blocks: every block its own piece, long merges
+    check(run([1100, 40], seed=13, num_cu=64))
+
+
+def test_empty_sequence_writes_zeros():
+    r = run([0, 200, 0], seed=14, num_cu=2)
+    assert np.all(r["out"][0] == 0) and np.all(r["out"][2] == 0)
+    want, _, wabs = om.mla_decode_ref(r["q"], r["kv"], r["qo"], r["kvp"], r["kvi"], r["sm"])
+    assert np.all(np.abs(r["out"][1] - want[1]) <= tolerance(wabs[1], want[1], False))
+
+
+def test_rerun_is_deterministic():
+    a = run([3000, 900], seed=15, num_cu=16)
+    b = run([3000, 900], seed=15, num_cu=16)
+    assert np.array_equal(a["out"], b["out"])
