@@ -53,7 +53,8 @@ def parse_args():
     p.add_argument("--config", default="c2_llama8b",
                    help="c1_tiny|c2_llama8b|c3_ragged|c4_window|c5_mtp|all (decode), "
                         "rope_decode_llama8b|rope_prefill_llama8b (KV-cache writer), "
-                        "qknr_prefill_v4|qknr_decode_v4 (fused RMSNorm + GPT-J RoPE + fp8 quant)")
+                        "qknr_prefill_v4|qknr_decode_v4 (fused RMSNorm + GPT-J RoPE + fp8 quant), "
+                        "mla_b32_c8192|mla_b128_c8192 (MLA fp8 decode)")
     p.add_argument("--seed", type=int, default=7)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
@@ -549,6 +550,142 @@ def run_qknr_config(name: str, args) -> dict:
     return line
 
 
+def mla_cpu_baseline(case_gpu, cfg, budget_s: float) -> dict:
+    """Time the MLA CPU oracle (float64 NumPy attention) over growing samples
+    of the workload's sequences until the budget is spent; GB/s of
+    algorithmic bytes."""
+    import torch
+
+    from flydsl_amd import workloads
+    from oracle import mla as om
+
+    per_seq = workloads.mla_bytes(cfg) / cfg.batch
+    q = om.fp8_to_f64(case_gpu["q"])
+    idx = case_gpu["kv_indices"].cpu().numpy()
+    done, spent = 0, 0.0
+    while spent < budget_s and done < cfg.batch:
+        rows = idx[done * cfg.context:(done + 1) * cfg.context]
+        kv = om.fp8_to_f64(case_gpu["kvs"][0][torch.from_numpy(rows).long().to(case_gpu["q"].device)].view(-1, 576))
+        t0 = time.perf_counter()
+        om.attend(q[done:done + 1], kv, 1.0 / 24.0)
+        spent += time.perf_counter() - t0
+        done += 1
+    return {
+        "value": round(done * per_seq / spent / 1e9, 4),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{done} of {cfg.batch} sequences of {cfg.name} through the float64 NumPy oracle "
+        f"(oracle/mla.py attend), {spent:.1f} s; host {cpu_model()}, "
+        f"affinity {len(os.sched_getaffinity(0))} cpus, os.cpu_count {os.cpu_count()}",
+    }
+
+
+def run_mla_config(name: str, args) -> dict:
+    """One MLA decode step = the decode launch + the log-sum-exp reduce of the
+    rows it cut, on a work list planned once (as a serving loop plans it per
+    batch shape).  KV buffers rotate over copies so no step reads what the
+    last one left in the Infinity Cache."""
+    import torch
+
+    from flydsl_amd import workloads
+    from flydsl_amd.mla_decode import (flydsl_mla_fwd_decode, get_mla_metadata_info_v1, get_mla_metadata_v1,
+                                       mla_reduce_v1)
+
+    cfg = workloads.MLA_CONFIGS[name]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    kv_bytes = cfg.batch * cfg.context * 576
+    copies = args.copies or (max(2, math.ceil(2 * MALL_BYTES / kv_bytes) + 1) if kv_bytes > 64 << 20 else 1)
+    case = workloads.build_mla_inputs(cfg, dev, seed=args.seed, copies=copies)
+    fp8 = torch.float8_e4m3fn
+    sizes = get_mla_metadata_info_v1(cfg.batch, 1, 128, fp8, fp8)
+    meta, wp, wi, ri, rf, rp = [torch.empty(sz, dtype=t, device=dev) for sz, t in sizes]
+    get_mla_metadata_v1(case["qo_indptr"].to(dev), case["kv_indptr"].to(dev), case["kv_last_page_lens"].to(dev),
+                        128, 1, False, meta, wi, wp, ri, rf, rp)
+    out = torch.empty(cfg.batch, 128, 512, dtype=torch.bfloat16, device=dev)
+    so = torch.empty(rp.size(0), 1, 128, 512, dtype=torch.float32, device=dev)
+    sl = torch.empty(rp.size(0), 1, 128, 1, dtype=torch.float32, device=dev)
+    sm = 1.0 / math.sqrt(576.0)
+
+    def decode(i):
+        flydsl_mla_fwd_decode(case["q"], case["kvs"][i % copies], case["kv_indices"], wp, wi, out, so, sl, sm)
+
+    def step(i):
+        decode(i)
+        mla_reduce_v1(so, sl, ri, rf, rp, 1, out)
+
+    for i in range(max(3, args.warmup)):
+        step(i)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    # the decode kernel alone, same stream, same rotation
+    e0.record(stream)
+    for i in range(args.steps):
+        decode(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    kms = e0.elapsed_time(e1) / args.steps
+    algo = workloads.mla_bytes(cfg)
+    flops = workloads.mla_flops(cfg)
+    value = algo / (ms * 1e-3) / 1e9
+    kval = algo / (kms * 1e-3) / 1e9
+    mh = meta.cpu().tolist()
+    line = {
+        "metric": "MLA fp8 decode HBM GB/s (KV + Q + out bytes per step) + us/step",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_step": round(ms * 1e3, 2),
+        "pct_of_peak": round(100.0 * value / PEAK_HBM_GBPS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8 e4m3fn (q, kv), f32 accumulate, bf16 out",
+        "data": "synthetic (seeded N(0,1) q and latent KV rows cast to fp8, pages in random order)",
+        "config": {
+            "workload": name,
+            "batch": cfg.batch,
+            "context": cfg.context,
+            "num_heads": 128,
+            "qk_head_dim": 576,
+            "v_head_dim": 512,
+            "page_size": 1,
+            "works": mh[0], "cut_rows": mh[1], "partial_rows": mh[2], "workers": mh[3],
+            "algorithmic_bytes_per_step": algo,
+            "algorithmic_flops_per_step": flops,
+            "decode_tflops": round(flops / (kms * 1e-3) / 1e12, 1),
+            "kv_copies_rotated": copies,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "mla_fp8_decode_kernel",
+            "kernels_per_step": 2,
+            "achieved": round(kval, 2),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(kval / PEAK_HBM_GBPS, 4),
+            "traffic": load_traffic(name),
+            "kernel_us": round(kms * 1e3, 2),
+            "algorithmic_bytes": algo,
+            "mfma_frac_fp8": round(flops / (kms * 1e-3) / 5.0e15, 4),
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = mla_cpu_baseline(case, cfg, args.cpu_seconds)
+    return line
+
+
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -564,6 +701,8 @@ def main():
             line = run_rope_config(n, args)
         elif n.startswith("qknr_"):
             line = run_qknr_config(n, args)
+        elif n.startswith("mla_"):
+            line = run_mla_config(n, args)
         else:
             line = run_config(n, args)
         print(json.dumps(line), flush=True)

@@ -310,3 +310,50 @@ def qknr_bytes(cfg: QkNormRopeConfig) -> int:
     scale_el = 4 if cfg.scale_dtype == "fp32" else 1
     per_tok = rows * (cfg.head_dim * 2 + cfg.head_dim * out_el + ng * scale_el) + 8 + 2 * (cfg.rope_head_dim // 2) * 2
     return cfg.num_tokens * per_tok + cfg.head_dim * 2
+
+
+@dataclasses.dataclass(frozen=True)
+class MlaConfig:
+    """MLA decode workload (tests/kernels/test_mla_decode.py:60-68 shapes:
+    128 query heads, one 576-dim latent kv head, page size 1, one query row
+    per sequence)."""
+
+    name: str
+    batch: int
+    context: int
+
+
+MLA_CONFIGS: Dict[str, MlaConfig] = {
+    # the reference test's largest configuration
+    "mla_b32_c8192": MlaConfig("mla_b32_c8192", 32, 8192),
+    # a full serving batch at the same context
+    "mla_b128_c8192": MlaConfig("mla_b128_c8192", 128, 8192),
+}
+
+
+def mla_bytes(cfg: MlaConfig) -> int:
+    """Algorithmic HBM bytes of one decode: every key/value row once (576 B
+    fp8), the fp8 query rows and the bf16 output rows."""
+    return cfg.batch * cfg.context * 576 + cfg.batch * 128 * 576 + cfg.batch * 128 * 512 * 2
+
+
+def mla_flops(cfg: MlaConfig) -> int:
+    """Algorithmic FLOPs: 128 heads x (576 + 512) multiply-adds per token."""
+    return cfg.batch * cfg.context * 128 * (576 + 512) * 2
+
+
+def build_mla_inputs(cfg: MlaConfig, device, seed: int = 7, copies: int = 1):
+    """fp8 query [B, 128, 576] and `copies` fp8 KV buffers [pages, 1, 1, 576]
+    from seeded normals; pages of each sequence in random order."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    total = cfg.batch * cfg.context
+    kv_indptr = torch.arange(cfg.batch + 1, dtype=torch.int32) * cfg.context
+    kv_indices = torch.randperm(total, generator=g).to(torch.int32)
+    q = torch.randn(cfg.batch, 128, 576, generator=g).to(torch.bfloat16).to(torch.float8_e4m3fn)
+    kv = torch.randn(total, 1, 1, 576, generator=g).to(torch.bfloat16).to(torch.float8_e4m3fn).to(device)
+    kvs = [kv] + [kv.clone() for _ in range(copies - 1)]
+    return {"q": q.to(device), "kvs": kvs, "kv_indptr": kv_indptr, "kv_indices": kv_indices.to(device),
+            "qo_indptr": torch.arange(cfg.batch + 1, dtype=torch.int32),
+            "kv_last_page_lens": torch.ones(cfg.batch, dtype=torch.int32)}
