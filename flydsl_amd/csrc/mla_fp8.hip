@@ -43,6 +43,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 #include "mla_plan.h"
 #include "pa_fp8.h"
 
@@ -183,6 +186,24 @@ struct Work {
 
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+// f(integral_constant<int, i>) for i = 0 .. N-1, each i a compile-time constant.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Lane index, recomputed where it is needed (volatile, so it is not hoisted
+// into a register that lives through the whole loop and gets spilled).
+__device__ __forceinline__ int lane_id() {
+  int r;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(r));
+  return r;
+}
+
 __device__ __forceinline__ Work load_work(const pa_mla_decode_args& a, int wi) {
   const int32_t* w = a.work_info + 8 * (int64_t)wi;
   Work r;
@@ -216,19 +237,19 @@ __device__ __forceinline__ void advance(const pa_mla_decode_args& a, Cursor& c, 
 }
 
 // Page of this lane's token (32w + l % 32 of the block) for unit c.
-__device__ __forceinline__ int unit_page(const pa_mla_decode_args& a, const Cursor& c, int w, int lane) {
+__device__ __forceinline__ int unit_page(const pa_mla_decode_args& a, const Cursor& c, int w) {
   if (c.w.kv1 <= c.w.kv0) return 0;
-  int pos = c.w.kv0 + c.blk * kBlock + 32 * w + (lane & 31);
+  int pos = c.w.kv0 + c.blk * kBlock + 32 * w + (lane_id() & 31);
   pos = min(pos, c.w.kv1 - 1);
   return a.kv_page_indices[pos];
 }
 
 // DMA of one wave's 32 tokens of a block into stage `st`.
 __device__ __forceinline__ void issue_block(const pa_mla_decode_args& a, LDS_AS unsigned char* stage, int w,
-                                           int lane, int page) {
+                                           int page) {
   page = min(max(page, 0), (int)(a.num_pages - 1));
   const unsigned char* src =
-      (const unsigned char*)a.kv_buffer + (int64_t)page * kQkDim + 16 * (lane >> 5);
+      (const unsigned char*)a.kv_buffer + (int64_t)page * kQkDim + 16 * (lane_id() >> 5);
   LDS_AS unsigned char* dst = stage + w * kGroupBytes;
 #pragma unroll
   for (int n = 0; n < kDmaPerWave; ++n) lds_dma16(src + 32 * n, dst + 1024 * n);
@@ -259,31 +280,57 @@ __device__ __forceinline__ void load_query(const pa_mla_decode_args& a, int qo, 
   }
 }
 
+// ds_read_b64_tr_b8 as inline assembly: the compiler's own intrinsic makes it
+// wait for every outstanding DMA (vmcnt(0)) before the read, which would
+// serialise the next block's DMA with this block's value product.  The
+// reads target the stage the DMA is not writing; their completion is
+// awaited explicitly with lgkmcnt.
+template <int OFF>
+__device__ __forceinline__ i32x2 lds_read_tr8(unsigned addr) {
+  i32x2 r;
+  asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
+  return r;
+}
+
+// A operand of one 16-dim row tile: tiles 2k (low dword) and 2k+1 (high) of
+// each 32-token group k.
+template <int OFF>
+__device__ __forceinline__ i32x8 read_tr_operand(const unsigned (&base)[4]) {
+  const i32x2 r0 = lds_read_tr8<OFF>(base[0]);
+  const i32x2 r1 = lds_read_tr8<OFF>(base[1]);
+  const i32x2 r2 = lds_read_tr8<OFF>(base[2]);
+  const i32x2 r3 = lds_read_tr8<OFF>(base[3]);
+  return i32x8{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+}
+
+
 // O^T += V^T P^T over one 128-token block held at stage `sb`: per 32 value
 // dims, eight transpose reads give the A operands of two 16-dim row tiles.
+// Software pipelined by hand: the reads of block db + 1 are issued before
+// the MFMAs of block db, which wait only for their own eight reads.
 template <bool FIRST, bool PRECISE>
 __device__ __forceinline__ void pv_block(const LDS_AS unsigned char* sb, f32x4 (&o)[16][2][2], const i32x8 (&phi)[2],
                                          const i32x8 (&plo)[2], const int (&sbs)[2], const int (&sbl)[2], int sa,
                                          int vbase) {
-  // Software pipelined by hand (the reads of block db + 1 are issued before
-  // the MFMAs of block db); scheduling barriers keep the compiler from
-  // hoisting further reads, which would cost registers.
+  unsigned base[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) base[k] = (unsigned)(uintptr_t)(sb + k * kGroupBytes + vbase);
   i32x8 va[2][2];
-  auto load = [&](int db, i32x8(&dst)[2]) {
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const i32x2 r = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-            (LDS_AS i32x2*)(sb + k * kGroupBytes + (2 * db + rt) * kUnitBytes + vbase));
-        dst[rt][2 * k] = r[0];
-        dst[rt][2 * k + 1] = r[1];
-      }
+  auto load = [&](auto dbc, i32x8(&dst)[2]) {
+    constexpr int db = decltype(dbc)::value;
+    dst[0] = read_tr_operand<(2 * db) * kUnitBytes>(base);
+    dst[1] = read_tr_operand<(2 * db + 1) * kUnitBytes>(base);
   };
-  load(0, va[0]);
-#pragma unroll
-  for (int db = 0; db < 16; ++db) {
-    if (db + 1 < 16) load(db + 1, va[(db + 1) & 1]);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  load(std::integral_constant<int, 0>{}, va[0]);
+  static_for<16>([&](auto dbc) {
+    constexpr int db = decltype(dbc)::value;
+    if constexpr (db + 1 < 16) {
+      load(std::integral_constant<int, db + 1>{}, va[(db + 1) & 1]);
+      asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
 #pragma unroll
     for (int ht = 0; ht < 2; ++ht)
 #pragma unroll
@@ -291,8 +338,7 @@ __device__ __forceinline__ void pv_block(const LDS_AS unsigned char* sb, f32x4 (
         pv_mfma<FIRST>(o[db][rt][ht], va[db & 1][rt], phi[ht], sa, sbs[ht]);
         if (PRECISE) pv_mfma<false>(o[db][rt][ht], va[db & 1][rt], plo[ht], sa, sbl[ht]);
       }
-    __builtin_amdgcn_sched_barrier(0);
-  }
+  });
 }
 
 template <bool PRECISE>
@@ -325,8 +371,8 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
 
   QTile q;
   load_query(a, cur.w.qo, w, c, g, q);
-  issue_block(a, lds, w, lane, unit_page(a, cur, w, lane));
-  int pg1 = valid(c1, we) ? unit_page(a, c1, w, lane) : 0;
+  issue_block(a, lds, w, unit_page(a, cur, w));
+  int pg1 = valid(c1, we) ? unit_page(a, c1, w) : 0;
 
   // O^T accumulators: [32-dim block][16-dim row tile][head tile].
   f32x4 o[16][2][2];
@@ -348,8 +394,8 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
     __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
     asm volatile("s_barrier" ::: "memory");
     if (valid(c1, we)) {
-      issue_block(a, lds + (st ^ 1) * kStageBytes, w, lane, pg1);
-      if (valid(c2, we)) pg1 = unit_page(a, c2, w, lane);
+      issue_block(a, lds + (st ^ 1) * kStageBytes, w, pg1);
+      if (valid(c2, we)) pg1 = unit_page(a, c2, w);
     }
     const LDS_AS unsigned char* sb = lds + st * kStageBytes;
 
@@ -462,9 +508,6 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
       sbv[1][ht] = max(k + 127 - 4, 0);
     }
 
-    // The next work's queries load during the value product (the logits
-    // are dead by then, the query registers free since this block's QK).
-    if (last && valid(c1, we)) load_query(a, c1.w.qo, w, c, g, q);
 
     // ---- O^T += V^T P^T: 16 blocks of 32 value dims ----
     probs_ready<PRECISE>(phi, plo);
@@ -508,6 +551,12 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
     }
 
     if (!valid(c1, we)) break;
+    // The queries of the next block's work are reloaded (from L2) after
+    // every block rather than held in registers through the softmax and the
+    // value product: that keeps the VGPRs within budget (no scratch spills,
+    // whose reloads would wait on the in-flight DMA through vmcnt).  They
+    // arrive with the next block's DMA, which the loop top waits for.
+    load_query(a, c1.w.qo, w, c, g, q);
     cur = c1;
     c1 = c2;
     advance(a, c2, we);
