@@ -65,7 +65,7 @@ constexpr int kVDim = 512;
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBlock = MLA_PLAN_BLOCK;       // tokens per LDS stage
-constexpr int kUnitBytes = 32 * 16;         // one 16-byte column unit of a 32-token group
+constexpr int kQuadBytes = 32 * 64;         // four column units of a 32-token group
 constexpr int kGroupBytes = 32 * kQkDim;     // one wave's 32 tokens
 constexpr int kStageBytes = kBlock * kQkDim; // 73728
 constexpr int kDmaPerWave = kQkDim / 32;     // 18 instructions of 1 KiB
@@ -74,7 +74,7 @@ constexpr float kLn2 = 0.69314718055994531f;
 constexpr float kNegInf = -__builtin_inff();
 
 static_assert(kGroupBytes * 4 == kStageBytes, "four 32-token groups per stage");
-static_assert(kUnitBytes * (kQkDim / 16) == kGroupBytes, "36 units per group");
+static_assert(kQuadBytes * (kQkDim / 64) == kGroupBytes, "9 quads per group");
 
 // Value product into accumulators pinned to AGPRs, with e8m0 block scales
 // (sa for the values: unit, sb for the probabilities of the lane's head and
@@ -236,23 +236,31 @@ __device__ __forceinline__ void advance(const pa_mla_decode_args& a, Cursor& c, 
   if (++c.wi < we) c.w = load_work(a, c.wi);
 }
 
-// Page of this lane's token (32w + l % 32 of the block) for unit c.
-__device__ __forceinline__ int unit_page(const pa_mla_decode_args& a, const Cursor& c, int w) {
-  if (c.w.kv1 <= c.w.kv0) return 0;
-  int pos = c.w.kv0 + c.blk * kBlock + 32 * w + (lane_id() & 31);
-  pos = min(pos, c.w.kv1 - 1);
-  return a.kv_page_indices[pos];
+// Pages of this lane's two tokens of the wave's 32 (l / 4 and 16 + l / 4)
+// for unit c.
+__device__ __forceinline__ i32x2 unit_pages(const pa_mla_decode_args& a, const Cursor& c, int w) {
+  if (c.w.kv1 <= c.w.kv0) return i32x2{0, 0};
+  const int pos = c.w.kv0 + c.blk * kBlock + 32 * w + (lane_id() >> 2);
+  return i32x2{a.kv_page_indices[min(pos, c.w.kv1 - 1)], a.kv_page_indices[min(pos + 16, c.w.kv1 - 1)]};
 }
 
-// DMA of one wave's 32 tokens of a block into stage `st`.
+// DMA of one wave's 32 tokens of a block into a stage.  Group layout:
+// [9 quads of 4 column units][32 tokens][4 slots of 16 B]; slot s of token t
+// holds unit 4q + (s ^ ((t >> 2) & 3)) (an XOR swizzle that keeps the key
+// reads conflict-free).  Instruction n fills quad n / 2 for tokens
+// 16 (n % 2) .. +15: each lane reads 16 B and four lanes read 64
+// consecutive bytes of one row.
 __device__ __forceinline__ void issue_block(const pa_mla_decode_args& a, LDS_AS unsigned char* stage, int w,
-                                           int page) {
-  page = min(max(page, 0), (int)(a.num_pages - 1));
-  const unsigned char* src =
-      (const unsigned char*)a.kv_buffer + (int64_t)page * kQkDim + 16 * (lane_id() >> 5);
+                                           i32x2 pages) {
+  const int np = (int)(a.num_pages - 1);
+  const int l = lane_id();
+  const int sx = (l & 3) ^ ((l >> 4) & 3);
+  const unsigned char* kvb = (const unsigned char*)a.kv_buffer;
+  const unsigned char* src0 = kvb + (int64_t)min(max(pages[0], 0), np) * kQkDim + 16 * sx;
+  const unsigned char* src1 = kvb + (int64_t)min(max(pages[1], 0), np) * kQkDim + 16 * sx;
   LDS_AS unsigned char* dst = stage + w * kGroupBytes;
 #pragma unroll
-  for (int n = 0; n < kDmaPerWave; ++n) lds_dma16(src + 32 * n, dst + 1024 * n);
+  for (int n = 0; n < kDmaPerWave; ++n) lds_dma16(((n & 1) ? src1 : src0) + 64 * (n >> 1), dst + 1024 * n);
 }
 
 // Q^T B operands of the wave's two 16-head tiles for query row qo: slot
@@ -312,14 +320,18 @@ template <bool FIRST, bool PRECISE>
 __device__ __forceinline__ void pv_block(const LDS_AS unsigned char* sb, f32x4 (&o)[16][2][2], const i32x8 (&phi)[2],
                                          const i32x8 (&plo)[2], const int (&sbs)[2], const int (&sbl)[2], int sa,
                                          int vbase) {
-  unsigned base[4];
+  // unit u = 2db + rt sits in quad u / 4, slot (u % 4) ^ g of the lane's rows
+  const int g = (int)(lane_id() >> 4);
+  unsigned base[4][4];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) base[k] = (unsigned)(uintptr_t)(sb + k * kGroupBytes + vbase);
+  for (int sl = 0; sl < 4; ++sl)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) base[sl][k] = (unsigned)(uintptr_t)(sb + k * kGroupBytes + vbase + 16 * (sl ^ g));
   i32x8 va[2][2];
   auto load = [&](auto dbc, i32x8(&dst)[2]) {
     constexpr int db = decltype(dbc)::value;
-    dst[0] = read_tr_operand<(2 * db) * kUnitBytes>(base);
-    dst[1] = read_tr_operand<(2 * db + 1) * kUnitBytes>(base);
+    dst[0] = read_tr_operand<((2 * db) >> 2) * kQuadBytes>(base[(2 * db) & 3]);
+    dst[1] = read_tr_operand<((2 * db + 1) >> 2) * kQuadBytes>(base[(2 * db + 1) & 3]);
   };
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   load(std::integral_constant<int, 0>{}, va[0]);
@@ -371,8 +383,8 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
 
   QTile q;
   load_query(a, cur.w.qo, w, c, g, q);
-  issue_block(a, lds, w, unit_page(a, cur, w));
-  int pg1 = valid(c1, we) ? unit_page(a, c1, w) : 0;
+  issue_block(a, lds, w, unit_pages(a, cur, w));
+  i32x2 pg1 = valid(c1, we) ? unit_pages(a, c1, w) : i32x2{0, 0};
 
   // O^T accumulators: [32-dim block][16-dim row tile][head tile].
   f32x4 o[16][2][2];
@@ -384,8 +396,8 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
   // address tile 2k, lanes c >= 8 tile 2k+1, row 4g + (c / 2) % 4 of the
   // tile, unit 2db + rt, byte 8 (c % 2); the low dword then holds tile 2k
   // and the high dword tile 2k+1 of value dim 32db + 16rt + c.
-  const int kbase = c * 16 + g * kUnitBytes;
-  const int vbase = (c >> 3) * 256 + (4 * g + ((c >> 1) & 3)) * 16 + (c & 1) * 8;
+  const int kbase = c * 64 + 16 * (g ^ ((c >> 2) & 3));
+  const int vbase = (16 * (c >> 3) + 4 * g + ((c >> 1) & 3)) * 64 + (c & 1) * 8;
   const int unit_scale = 127;  // e8m0 2^0
   const int half_scale = 126;  // e8m0 2^-1
 
@@ -395,7 +407,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
     asm volatile("s_barrier" ::: "memory");
     if (valid(c1, we)) {
       issue_block(a, lds + (st ^ 1) * kStageBytes, w, pg1);
-      if (valid(c2, we)) pg1 = unit_page(a, c2, w);
+      if (valid(c2, we)) pg1 = unit_pages(a, c2, w);
     }
     const LDS_AS unsigned char* sb = lds + st * kStageBytes;
 
@@ -419,11 +431,11 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int T = 4 * half + t;
-        const LDS_AS unsigned char* kr = sb + (T >> 1) * kGroupBytes + (T & 1) * 256 + kbase;
+        const LDS_AS unsigned char* kr = sb + (T >> 1) * kGroupBytes + (T & 1) * 1024 + kbase;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-          const i32x4 lo = *(const LDS_AS i32x4*)(kr + kb * 8 * kUnitBytes);
-          const i32x4 hi = *(const LDS_AS i32x4*)(kr + (kb * 8 + 4) * kUnitBytes);
+          const i32x4 lo = *(const LDS_AS i32x4*)(kr + 2 * kb * kQuadBytes);
+          const i32x4 hi = *(const LDS_AS i32x4*)(kr + (2 * kb + 1) * kQuadBytes);
           const i32x8 ka = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
           if (kb == 0) {
             qk_mfma<true>(s[t][0], ka, q.b[0][kb]);
@@ -435,7 +447,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
         }
         // rope: both operands carry the 16 dims twice; the B scale 2^-1
         // undoes the doubling exactly
-        const i32x4 kr4 = *(const LDS_AS i32x4*)(kr + 32 * kUnitBytes);
+        const i32x4 kr4 = *(const LDS_AS i32x4*)(kr + 8 * kQuadBytes);
         const i32x8 ka = {kr4[0], kr4[1], kr4[2], kr4[3], kr4[0], kr4[1], kr4[2], kr4[3]};
 #pragma unroll
         for (int ht = 0; ht < 2; ++ht) {
