@@ -246,18 +246,20 @@ __device__ __forceinline__ i32x2 unit_pages(const pa_mla_decode_args& a, const C
 
 // DMA of one wave's 32 tokens of a block into a stage.  Group layout:
 // [9 quads of 4 column units][32 tokens][4 slots of 16 B]; slot s of token t
-// holds unit 4q + (s ^ ((t >> 2) & 3)) (an XOR swizzle that keeps the key
-// reads conflict-free).  Instruction n fills quad n / 2 for tokens
+// holds unit 4q + (s ^ swz(t)), swz(t) = ((t >> 2) ^ (t >> 3 & 2)) & 3: an
+// XOR swizzle that spreads the 16 rows of a key read and the 8 rows (two
+// tiles) of a transpose read over distinct bank groups.  Instruction n fills quad n / 2 for tokens
 // 16 (n % 2) .. +15: each lane reads 16 B and four lanes read 64
 // consecutive bytes of one row.
 __device__ __forceinline__ void issue_block(const pa_mla_decode_args& a, LDS_AS unsigned char* stage, int w,
                                            i32x2 pages) {
   const int np = (int)(a.num_pages - 1);
   const int l = lane_id();
-  const int sx = (l & 3) ^ ((l >> 4) & 3);
+  const int sx0 = (l & 3) ^ ((l >> 4) & 3);  // tokens l / 4:      swz = (l >> 4) & 3
+  const int sx1 = sx0 ^ 2;                   // tokens 16 + l / 4: swz ^ 2
   const unsigned char* kvb = (const unsigned char*)a.kv_buffer;
-  const unsigned char* src0 = kvb + (int64_t)min(max(pages[0], 0), np) * kQkDim + 16 * sx;
-  const unsigned char* src1 = kvb + (int64_t)min(max(pages[1], 0), np) * kQkDim + 16 * sx;
+  const unsigned char* src0 = kvb + (int64_t)min(max(pages[0], 0), np) * kQkDim + 16 * sx0;
+  const unsigned char* src1 = kvb + (int64_t)min(max(pages[1], 0), np) * kQkDim + 16 * sx1;
   LDS_AS unsigned char* dst = stage + w * kGroupBytes;
 #pragma unroll
   for (int n = 0; n < kDmaPerWave; ++n) lds_dma16(((n & 1) ? src1 : src0) + 64 * (n >> 1), dst + 1024 * n);
@@ -320,8 +322,10 @@ template <bool FIRST, bool PRECISE>
 __device__ __forceinline__ void pv_block(const LDS_AS unsigned char* sb, f32x4 (&o)[16][2][2], const i32x8 (&phi)[2],
                                          const i32x8 (&plo)[2], const int (&sbs)[2], const int (&sbl)[2], int sa,
                                          int vbase) {
-  // unit u = 2db + rt sits in quad u / 4, slot (u % 4) ^ g of the lane's rows
-  const int g = (int)(lane_id() >> 4);
+  // unit u = 2db + rt sits in quad u / 4, slot (u % 4) ^ swz of the lane's
+  // rows 16(c / 8) + 4g + ..: swz = g ^ 2(c / 8)
+  const int l = lane_id();
+  const int g = (l >> 4) ^ (((l >> 3) & 1) << 1);
   unsigned base[4][4];
 #pragma unroll
   for (int sl = 0; sl < 4; ++sl)
@@ -396,7 +400,9 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
   // address tile 2k, lanes c >= 8 tile 2k+1, row 4g + (c / 2) % 4 of the
   // tile, unit 2db + rt, byte 8 (c % 2); the low dword then holds tile 2k
   // and the high dword tile 2k+1 of value dim 32db + 16rt + c.
-  const int kbase = c * 64 + 16 * (g ^ ((c >> 2) & 3));
+  // key rows 16(T % 2) + c: swz = (c / 4) ^ 2(T % 2)
+  const int kbase0 = c * 64 + 16 * (g ^ ((c >> 2) & 3));
+  const int kbase1 = c * 64 + 16 * (g ^ ((c >> 2) & 3) ^ 2);
   const int vbase = (16 * (c >> 3) + 4 * g + ((c >> 1) & 3)) * 64 + (c & 1) * 8;
   const int unit_scale = 127;  // e8m0 2^0
   const int half_scale = 126;  // e8m0 2^-1
@@ -431,7 +437,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int T = 4 * half + t;
-        const LDS_AS unsigned char* kr = sb + (T >> 1) * kGroupBytes + (T & 1) * 1024 + kbase;
+        const LDS_AS unsigned char* kr = sb + (T >> 1) * kGroupBytes + (T & 1) * 1024 + ((T & 1) ? kbase1 : kbase0);
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
           const i32x4 lo = *(const LDS_AS i32x4*)(kr + 2 * kb * kQuadBytes);
