@@ -51,7 +51,8 @@ def parse_args():
     p.add_argument("--steps", type=int, default=100)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--config", default="c2_llama8b",
-                   help="c1_tiny|c2_llama8b|c3_ragged|c4_window|c5_mtp|all (decode), "
+                   help="c1_tiny|c2_llama8b|c3_ragged|c4_window|c5_mtp|all (decode), c3_ragged_p1024 "
+                        "(work-list route), "
                         "rope_decode_llama8b|rope_prefill_llama8b (KV-cache writer), "
                         "qknr_prefill_v4|qknr_decode_v4 (fused RMSNorm + GPT-J RoPE + fp8 quant), "
                         "mla_b32_c8192|mla_b128_c8192 (MLA fp8 decode)")
@@ -60,6 +61,9 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     p.add_argument("--copies", type=int, default=0, help="KV-cache copies to rotate (0 = auto)")
     p.add_argument("--partitions", type=int, default=0, help="override max_context_partition_num (0 = heuristic)")
+    p.add_argument("--no-metadata", action="store_true",
+                   help="flat-page workloads: call pa_decode_ps_launch without the get_pa_metadata work list "
+                        "(the launcher's balanced split)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="instead of decoding, run a plain device copy of MIB MiB (--steps times): the "
                         "reference point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
@@ -89,9 +93,40 @@ def cpu_model() -> str:
     return platform.processor()
 
 
+def median_of_runs(items, run, budget_s: float, repeats: int = 3):
+    """CPU baseline timing (median of ``repeats`` runs after one warm-up).
+
+    The warm-up pass runs ``run(item)`` over ``items`` in order until a
+    quarter of the budget is spent; the items it reached are the sample,
+    which is then timed ``repeats`` more times.  Returns (sample, median
+    seconds, every timed run's seconds)."""
+    import statistics
+
+    sample, spent = [], 0.0
+    for it in items:
+        t0 = time.perf_counter()
+        run(it)
+        spent += time.perf_counter() - t0
+        sample.append(it)
+        if spent >= budget_s / (repeats + 1):
+            break
+    runs = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        for it in sample:
+            run(it)
+        runs.append(time.perf_counter() - t0)
+    return sample, statistics.median(runs), runs
+
+
+def host_desc() -> str:
+    return (f"host {cpu_model()}, affinity {len(os.sched_getaffinity(0))} cpus, "
+            f"os.cpu_count {os.cpu_count()}")
+
+
 def cpu_baseline(case_gpu, cfg, budget_s: float) -> dict:
-    """Time the CPU oracle on sequences of the same workload until the budget
-    is spent; scaled to KV GB/s over the sequences it finished."""
+    """Time the CPU oracle on a bounded sample of the same workload's
+    sequences (median of 3 runs after a warm-up); KV GB/s of the sample."""
     import torch
 
     from flydsl_amd import workloads
@@ -104,14 +139,11 @@ def cpu_baseline(case_gpu, cfg, budget_s: float) -> dict:
     kc = case_gpu["key_cache"]
     vc = case_gpu["value_cache"]
     per_token = case_gpu["key_scale"].dim() > 1
-    done_bytes = 0
-    done_seqs = 0
-    spent = 0.0
-    order = list(range(cfg.batch))
-    for b in order:
+
+    def prepare(b):
+        # compact copy of this sequence's pages (the oracle's input), not timed
         n = math.ceil(ctx_all[b] / bs)
         pages = case_gpu["block_tables"][b, :n].long()
-        # compact copy of this sequence's pages (the oracle's input), not timed
         k = kc.index_select(0, pages).cpu()
         v = vc.index_select(0, pages).cpu()
         nbp = k.shape[0]
@@ -125,22 +157,22 @@ def cpu_baseline(case_gpu, cfg, budget_s: float) -> dict:
         bt = torch.arange(nbp, dtype=torch.int32).reshape(1, -1)
         cl = torch.tensor([ctx_all[b]], dtype=torch.int32)
         ind = torch.tensor([0, ql], dtype=torch.int32)
-        t0 = time.perf_counter()
-        torch_ref.torch_mha_extend(q, k, v, bt, cl, ind, ks, vs, sliding_window=cfg.sliding_window,
+        return b, (q, k, v, bt, cl, ind, ks, vs)
+
+    def run(item):
+        torch_ref.torch_mha_extend(*item[1], sliding_window=cfg.sliding_window,
                                    softmax_scale=case_gpu["softmax_scale"])
-        spent += time.perf_counter() - t0
-        done_bytes += workloads.kv_bytes(cfg, [ctx_all[b]])
-        done_seqs += 1
-        if spent >= budget_s:
-            break
+
+    sample, med, runs = median_of_runs((prepare(b) for b in range(cfg.batch)), run, budget_s)
+    done_bytes = workloads.kv_bytes(cfg, [ctx_all[b] for b, _ in sample])
     return {
-        "value": round(done_bytes / spent / 1e9, 4),
+        "value": round(done_bytes / med / 1e9, 4),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"{done_seqs} of {cfg.batch} sequences of {cfg.name} through the float32 torch oracle "
-        f"(oracle/torch_ref.py torch_mha_extend), {spent:.1f} s; host {cpu_model()}, "
-        f"affinity {len(os.sched_getaffinity(0))} cpus, os.cpu_count {os.cpu_count()}",
+        "sample": f"{len(sample)} of {cfg.batch} sequences of {cfg.name} through the float32 torch oracle "
+        f"(oracle/torch_ref.py torch_mha_extend): median of {len(runs)} runs after a warm-up, "
+        f"{med:.2f} s (runs {', '.join(f'{r:.2f}' for r in runs)}); {host_desc()}",
     }
 
 
@@ -158,14 +190,26 @@ def load_traffic(name: str):
 KERNEL_OF_ENTRY = {
     "pa_fp8_decode_partition": "pa_fp8_partition_kernel",
     "pa_fp8_decode_balanced": "pa_fp8_stream_kernel (balanced split)",
-    "pa_fp8_decode_worklist": "pa_fp8_stream_kernel (work list)",
+    "pa_fp8_decode_worklist": "pa_fp8_bin_kernel (work list, one workgroup per bin)",
 }
+
+
+def flat_page_list(block_tables, ctx, block_size):
+    """kv_page_indices / kv_indptr of the flat-page routes from a block
+    table (each sequence's first ceil(ctx / bs) pages)."""
+    import torch
+
+    rows = [block_tables[b, : math.ceil(c / block_size)] for b, c in enumerate(ctx)]
+    pages = torch.cat(rows).to(torch.int32).contiguous()
+    counts = torch.tensor([0] + [r.numel() for r in rows], dtype=torch.int64)
+    indptr = torch.cumsum(counts, 0).to(torch.int32).to(block_tables.device)
+    return pages, indptr
 
 
 def run_config(name: str, args) -> dict:
     import torch
 
-    from flydsl_amd import get_recommended_splits, pa_decode_ps_launch, prepare_pa_decode, workloads
+    from flydsl_amd import get_pa_metadata, get_recommended_splits, pa_decode_ps_launch, prepare_pa_decode, workloads
 
     cfg = workloads.CONFIGS[name]
     dev = torch.device("cuda:0")
@@ -197,12 +241,25 @@ def run_config(name: str, args) -> dict:
     # (tests/kernels/test_pa.py:849-900): recommended split count, no
     # caller-side scratch (the window route preallocates its partials).
     sw_scratch = dict(exp_sums=es, max_logits=ml, temporary_output=tmp) if cfg.sliding_window else {}
+    # Pages other than 16 / 64 tokens: the persistent route, with the work
+    # list planned once for the batch (get_pa_metadata, as the harness calls
+    # it before the timed launches, tests/kernels/test_pa.py:834-843).
+    flat = cfg.block_size not in (16, 64)
+    page_idx = indptr = None
+    md = None
+    if flat:
+        page_idx, indptr = flat_page_list(case["block_tables"], ctx, cfg.block_size)
+        if not args.no_metadata:
+            md = get_pa_metadata(case["query"], case["key_cache"], case["context_lengths"], indptr,
+                                 cfg.num_query_heads, hkv)
+            sw_scratch = dict(metadata=md)
+    bt_arg = None if flat else case["block_tables"]
 
     def step(i):
         k, v, ks, vs = caches[i % copies]
-        return pa_decode_ps_launch(out, case["query"], k, v, case["context_lengths"], None, None,
+        return pa_decode_ps_launch(out, case["query"], k, v, case["context_lengths"], page_idx, indptr,
                                    case["softmax_scale"], ks, vs, sliding_window=cfg.sliding_window,
-                                   block_tables=case["block_tables"], max_context_partition_num=P, **sw_scratch)
+                                   block_tables=bt_arg, max_context_partition_num=P, **sw_scratch)
 
     route = None
     for i in range(args.warmup):
@@ -223,10 +280,9 @@ def run_config(name: str, args) -> dict:
     # entry point with pre-marshalled arguments on this same stream.
     calls = []
     for k, v, ks, vs in caches:
-        calls.append(prepare_pa_decode(out, case["query"], k, v, case["context_lengths"], None, None,
+        calls.append(prepare_pa_decode(out, case["query"], k, v, case["context_lengths"], page_idx, indptr,
                                        case["softmax_scale"], ks, vs, sliding_window=cfg.sliding_window,
-                                       block_tables=case["block_tables"], max_context_partition_num=P,
-                                       **sw_scratch))
+                                       block_tables=bt_arg, max_context_partition_num=P, **sw_scratch))
     kernel_name, _ = calls[0].kernels()[0]
     decode = [c.kernels()[0][1] for c in calls]
     for i in range(max(3, args.warmup)):
@@ -274,6 +330,7 @@ def run_config(name: str, args) -> dict:
             "sum_context": int(sum(ctx)),
             "num_partitions": P,
             "route": route,
+            "work_list_bins": md["num_sm"] if md is not None else None,
             "kv_bytes_per_step": kv,
             "kv_plus_scale_bytes_per_step": kv_sc,
             "kv_copies_rotated": copies,
@@ -300,8 +357,9 @@ def run_config(name: str, args) -> dict:
 
 
 def rope_cpu_baseline(case_gpu, cfg, budget_s: float) -> dict:
-    """Time the writer's CPU oracle over growing samples of the workload's
-    tokens until the budget is spent; scaled to GB/s of algorithmic bytes."""
+    """Time the writer's CPU oracle on a bounded sample of the workload's
+    tokens (slices of growing size; median of 3 runs after a warm-up); GB/s
+    of algorithmic bytes."""
     import torch
 
     from flydsl_amd import workloads
@@ -311,26 +369,31 @@ def rope_cpu_baseline(case_gpu, cfg, budget_s: float) -> dict:
     c = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in case_gpu.items()}
     kc = c["key_cache"].view(torch.uint8)
     vc = c["value_cache"].view(torch.uint8)
-    done, spent, n = 0, 0.0, 8
-    while spent < budget_s and done < cfg.num_tokens:
-        m = min(n, cfg.num_tokens - done)
-        sl = slice(done, done + m)
-        t0 = time.perf_counter()
+
+    def slices():
+        done, n = 0, 8
+        while done < cfg.num_tokens:
+            m = min(n, cfg.num_tokens - done)
+            yield slice(done, done + m)
+            done += m
+            n *= 2
+
+    def run(sl):
         rc.rope_cache_ref(c["q"][sl], c["k"][sl], c["v"][sl], c["positions"][sl], c["cos"], c["sin"],
                           c["slot_mapping"][sl], kc, vc, block_size=cfg.block_size, layout=rc.ATOM_TRANS_V,
                           apply_scale=True, k_scale=float(c["k_scale"][0]), v_scale=float(c["v_scale"][0]),
                           inplace=True)
-        spent += time.perf_counter() - t0
-        done += m
-        n *= 2
+
+    sample, med, runs = median_of_runs(slices(), run, budget_s)
+    done = sum(sl.stop - sl.start for sl in sample)
     return {
-        "value": round(done * per_tok / spent / 1e9, 4),
+        "value": round(done * per_tok / med / 1e9, 4),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": f"{done} of {cfg.num_tokens} tokens of {cfg.name} through the torch oracle "
-        f"(oracle/rope_cache.py rope_cache_ref, caches written in place), {spent:.1f} s; "
-        f"host {cpu_model()}, affinity {len(os.sched_getaffinity(0))} cpus, os.cpu_count {os.cpu_count()}",
+        f"(oracle/rope_cache.py rope_cache_ref, caches written in place): median of {len(runs)} runs after a "
+        f"warm-up, {med:.2f} s (runs {', '.join(f'{r:.2f}' for r in runs)}); {host_desc()}",
     }
 
 
@@ -423,9 +486,9 @@ def run_rope_config(name: str, args) -> dict:
 
 
 def qknr_cpu_baseline(case_gpu, cfg, budget_s: float) -> dict:
-    """Time the fused RMSNorm + RoPE CPU oracle over growing samples of the
-    workload's tokens until the budget is spent; scaled to GB/s of
-    algorithmic bytes."""
+    """Time the fused RMSNorm + RoPE CPU oracle on a bounded sample of the
+    workload's tokens (slices of growing size; median of 3 runs after a
+    warm-up); GB/s of algorithmic bytes."""
     import torch
 
     from flydsl_amd import workloads
@@ -433,26 +496,31 @@ def qknr_cpu_baseline(case_gpu, cfg, budget_s: float) -> dict:
 
     per_tok = workloads.qknr_bytes(cfg) / cfg.num_tokens
     c = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in case_gpu.items()}
-    done, spent, n = 0, 0.0, 8
-    while spent < budget_s and done < cfg.num_tokens:
-        m = min(n, cfg.num_tokens - done)
-        sl = slice(done, done + m)
-        t0 = time.perf_counter()
+
+    def slices():
+        done, n = 0, 8
+        while done < cfg.num_tokens:
+            m = min(n, cfg.num_tokens - done)
+            yield slice(done, done + m)
+            done += m
+            n *= 2
+
+    def run(sl):
         qnr.qk_norm_rope_quant(c["q"][sl], c["kv"][sl], c["kv_weight"], c["cos_cache"], c["sin_cache"],
                                c["positions"][sl], num_q_heads=cfg.num_q_heads, head_dim=cfg.head_dim,
                                rope_head_dim=cfg.rope_head_dim, quant=cfg.quant, quant_group_size=cfg.group_size,
                                scale_dtype=cfg.scale_dtype)
-        spent += time.perf_counter() - t0
-        done += m
-        n *= 2
+
+    sample, med, runs = median_of_runs(slices(), run, budget_s)
+    done = sum(sl.stop - sl.start for sl in sample)
     return {
-        "value": round(done * per_tok / spent / 1e9, 4),
+        "value": round(done * per_tok / med / 1e9, 4),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": f"{done} of {cfg.num_tokens} tokens of {cfg.name} through the NumPy oracle "
-        f"(oracle/qk_norm_rope.py qk_norm_rope_quant), {spent:.1f} s; "
-        f"host {cpu_model()}, affinity {len(os.sched_getaffinity(0))} cpus, os.cpu_count {os.cpu_count()}",
+        f"(oracle/qk_norm_rope.py qk_norm_rope_quant): median of {len(runs)} runs after a warm-up, "
+        f"{med:.2f} s (runs {', '.join(f'{r:.2f}' for r in runs)}); {host_desc()}",
     }
 
 
@@ -551,8 +619,8 @@ def run_qknr_config(name: str, args) -> dict:
 
 
 def mla_cpu_baseline(case_gpu, cfg, budget_s: float) -> dict:
-    """Time the MLA CPU oracle (float64 NumPy attention) over growing samples
-    of the workload's sequences until the budget is spent; GB/s of
+    """Time the MLA CPU oracle (float64 NumPy attention) on a bounded sample
+    of the workload's sequences (median of 3 runs after a warm-up); GB/s of
     algorithmic bytes."""
     import torch
 
@@ -562,22 +630,25 @@ def mla_cpu_baseline(case_gpu, cfg, budget_s: float) -> dict:
     per_seq = workloads.mla_bytes(cfg) / cfg.batch
     q = om.fp8_to_f64(case_gpu["q"])
     idx = case_gpu["kv_indices"].cpu().numpy()
-    done, spent = 0, 0.0
-    while spent < budget_s and done < cfg.batch:
-        rows = idx[done * cfg.context:(done + 1) * cfg.context]
+
+    def prepare(s):
+        rows = idx[s * cfg.context:(s + 1) * cfg.context]
         kv = om.fp8_to_f64(case_gpu["kvs"][0][torch.from_numpy(rows).long().to(case_gpu["q"].device)].view(-1, 576))
-        t0 = time.perf_counter()
-        om.attend(q[done:done + 1], kv, 1.0 / 24.0)
-        spent += time.perf_counter() - t0
-        done += 1
+        return s, kv
+
+    def run(item):
+        s, kv = item
+        om.attend(q[s:s + 1], kv, 1.0 / 24.0)
+
+    sample, med, runs = median_of_runs((prepare(s) for s in range(cfg.batch)), run, budget_s)
     return {
-        "value": round(done * per_seq / spent / 1e9, 4),
+        "value": round(len(sample) * per_seq / med / 1e9, 4),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"{done} of {cfg.batch} sequences of {cfg.name} through the float64 NumPy oracle "
-        f"(oracle/mla.py attend), {spent:.1f} s; host {cpu_model()}, "
-        f"affinity {len(os.sched_getaffinity(0))} cpus, os.cpu_count {os.cpu_count()}",
+        "sample": f"{len(sample)} of {cfg.batch} sequences of {cfg.name} through the float64 NumPy oracle "
+        f"(oracle/mla.py attend): median of {len(runs)} runs after a warm-up, {med:.2f} s "
+        f"(runs {', '.join(f'{r:.2f}' for r in runs)}); {host_desc()}",
     }
 
 

@@ -917,6 +917,8 @@ struct Piece {
   int desc_cnt;   // balanced: pieces of the pair, when this piece starts it
   int last_page;  // last page index of the sequence's page list
   int64_t bt_off; // offset of the sequence's page list in block_tables
+  int cut;        // bin walk: bit 0 the work began before the piece, bit 1 it goes on after it
+  int wstart;     // bin walk: position of the work's first chunk in the bin
 };
 
 // Wave-uniform read of read-only kernel input through the constant address
@@ -987,7 +989,25 @@ struct BalancedWalk {
   }
 };
 
-// Work-list walk: works [idx, end) of this wave's bin.
+// Chunks [tb0, tb0 + 32 n) of a work over partitions [kv0, kv1) (cumulative,
+// pb = the sequence's first) of a sequence with context ctx, visible keys
+// [lo_all, hi_all) and last page last_page (< 0: no pages, nothing visible).
+// Works of one sequence meet at partition boundaries, which are chunk
+// boundaries, so their chunk ranges tile the sequence's.
+__device__ __forceinline__ void work_chunks(int ctx, int lo_all, int hi_all, int last_page, int pb, int kv0, int kv1,
+                                            int& tb0, int& n) {
+  const int a0 = pa_max((kv0 - pb) * PA_PARTITION_TOKENS, lo_all);
+  const int a1 = pa_min(pa_min((kv1 - pb) * PA_PARTITION_TOKENS, ctx), last_page < 0 ? lo_all : hi_all);
+  if (a1 > a0) {
+    tb0 = a0 & ~(kChunk - 1);
+    n = pa_cdiv(a1 - tb0, kChunk);
+  } else {
+    tb0 = 0;
+    n = 0;
+  }
+}
+
+// Work-list walk: works [idx, end) of a bin.
 struct WorklistWalk {
   int idx, end;
   __device__ __forceinline__ bool next(Piece& p, const pa_fp8_stream_args& a, const int32_t* kv_indptr,
@@ -1002,16 +1022,10 @@ struct WorklistWalk {
     piece_sequence(p, a, kv_indptr, context_lengths, b);
     p.h = qh0 / a.query_group_size;
     const int pb = ld_uniform(partition_indptr, b);
-    const int a0 = pa_max((kv0 - pb) * PA_PARTITION_TOKENS, p.lo_all);
-    const int a1 = pa_min(pa_min((kv1 - pb) * PA_PARTITION_TOKENS, p.ctx), p.hi_all);
-    if (a1 > a0) {
-      p.tb0 = a0 & ~(kChunk - 1);
-      p.n = pa_cdiv(a1 - p.tb0, kChunk);
-    } else {
-      p.tb0 = 0;
-      p.n = 0;
-    }
+    work_chunks(p.ctx, p.lo_all, p.hi_all, p.last_page, pb, kv0, kv1, p.tb0, p.n);
     p.target = ploc < 0 ? -1 : ploc + a.query_length;
+    p.cut = 0;
+    p.wstart = 0;
     p.orow = qo0;
     p.desc_cnt = 0;
     return true;
@@ -1114,6 +1128,104 @@ __device__ __forceinline__ void store_out4(void* out, int dtype, int64_t off, f3
   }
 }
 
+// Direct-to-LDS loads of one 32-token chunk of kv head ih (first token tb;
+// page p0, and for 16-token pages p1 for tokens tb + 16 ..) into the stage
+// at sk: keys (two 16-token halves kKHalf apart), values, and with
+// per-token scales the chunk's 32 K then 32 V scales.  8 (+1) load
+// instructions, each reading one page: a wave-uniform page base plus a
+// per-lane offset.
+template <bool PER_TOKEN, bool BS16>
+__device__ __forceinline__ void dma_chunk(const pa_fp8_stream_args& a, const float* __restrict__ key_scale,
+                                          const float* __restrict__ value_scale, LDS_AS unsigned char* sk, int ih,
+                                          int tb, int p0, int p1, int lane) {
+  const int bs = a.block_size;
+  const int koff_lane = BS16 ? lane * 16 : (lane >> 4) * (bs * 16) + (lane & 15) * 16;
+  const uint8_t* kbase = (const uint8_t*)a.key_cache + (int64_t)ih * a.stride_k_head;
+  const uint8_t* vbase = (const uint8_t*)a.value_cache + (int64_t)ih * a.stride_v_head;
+  LDS_AS unsigned char* sv = sk + kKBytes;
+  if (BS16) {
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const uint8_t* kp = kbase + (int64_t)(hh ? p1 : p0) * a.stride_k_block;
+      const uint8_t* vp = vbase + (int64_t)(hh ? p1 : p0) * a.stride_v_block;
+#pragma unroll
+      for (int q2 = 0; q2 < 2; ++q2) lds_dma16(kp + koff_lane + q2 * 1024, sk + hh * kKHalf + q2 * 1024);
+#pragma unroll
+      for (int q2 = 0; q2 < 2; ++q2) lds_dma16(vp + lane * 16 + q2 * 1024, sv + hh * 2048 + q2 * 1024);
+    }
+  } else {
+    const int s0 = tb & (bs - 1);
+    const uint8_t* kp = kbase + (int64_t)p0 * a.stride_k_block + s0 * 16;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int q2 = 0; q2 < 2; ++q2)
+        lds_dma16(kp + hh * 256 + q2 * (4 * bs * 16) + koff_lane, sk + hh * kKHalf + q2 * 1024);
+    if (a.trans_v) {
+      const uint8_t* vp = vbase + (int64_t)p0 * a.stride_v_block + (s0 >> 4) * (kHead * 16);
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int q2 = 0; q2 < 2; ++q2)
+          lds_dma16(vp + hh * 2048 + q2 * 1024 + lane * 16, sv + hh * 2048 + q2 * 1024);
+    } else {
+      const uint8_t* vp = vbase + (int64_t)p0 * a.stride_v_block + s0;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int q2 = 0; q2 < 2; ++q2)
+          lds_dma16(vp + hh * 16 + q2 * (64 * bs) + lane * bs, sv + hh * 2048 + q2 * 1024);
+    }
+  }
+  if (PER_TOKEN) {
+    LDS_AS unsigned char* ss = sv + kVBytes;
+    if (lane < 16) {
+      const int tt = (lane & 7) * 4;
+      const int pg2 = BS16 ? (tt >= 16 ? p1 : p0) : p0;
+      const int sidx = BS16 ? (tt & 15) : (tb & (bs - 1)) + tt;
+      const float* base = (lane < 8 ? key_scale : value_scale) + (int64_t)ih * a.stride_ks_head;
+      lds_dma16(base + (int64_t)pg2 * a.stride_ks_block + sidx, ss);
+    }
+  }
+}
+
+// A finished piece's result for query column e (lane (grp, e % 16) holds
+// head dims 16 j + 4 grp .. + 3 in acc[j]): the output rows when the piece
+// is a whole (sequence, kv head), else a float32 partial row and its
+// natural-log lse (work list: rows target + qi; balanced split: partial id
+// target).  m is the column's base-2 maximum, L its sum of 256 * 2^(l - m),
+// and acc * vfin / L the normalised output.
+template <bool WORKLIST>
+__device__ __forceinline__ void store_piece(const pa_fp8_stream_args& a, void* __restrict__ output,
+                                            float* __restrict__ part_out, float* __restrict__ part_lse,
+                                            const Piece& p, const f32x4 (&acc)[8], float L, float m, float vfin,
+                                            int e, int grp) {
+  const int gqa = a.query_group_size;
+  const int eq = a.query_length * gqa;
+  if (e >= eq) return;
+  const int qi = e / gqa;
+  const int g = e - qi * gqa;
+  const int qh = p.h * gqa + g;
+  const float sc = L > 0.0f ? vfin / L : 0.0f;
+  if (p.target < 0) {
+    const int64_t off = (int64_t)(p.orow + qi) * a.stride_out_tok + (int64_t)qh * a.stride_out_head + 4 * grp;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) store_out4(output, a.output_dtype, off + 16 * j, acc[j] * sc);
+  } else {
+    int64_t po, pl;
+    if (WORKLIST) {
+      po = (int64_t)(p.target + qi) * a.stride_po_row + (int64_t)qh * kHead;
+      pl = (int64_t)(p.target + qi) * a.stride_pl_row + qh;
+    } else {
+      pl = (int64_t)p.target * eq + e;
+      po = pl * kHead;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) *(f32x4*)(part_out + po + 16 * j + 4 * grp) = acc[j] * sc;
+    if (grp == 0) part_lse[pl] = L > 0.0f ? kLn2 * (m + __builtin_amdgcn_logf(L) - 8.0f) : kNegInf;
+  }
+}
+
 // Each wave walks its pieces through a private LDS ring (2 stages of one
 // 32-token chunk each) plus two query images (the current piece's and the
 // next one's: a piece's query rows are loaded by direct-to-LDS DMA just
@@ -1169,8 +1281,6 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
 
   LDS_AS unsigned char* ring = (LDS_AS unsigned char*)smem + wave * kWaveBytes;
   LDS_AS unsigned char* qimg = ring + kStages * kStageBytes;
-  const int koff_lane = BS16 ? lane * 16 : (lane >> 4) * (bs * 16) + (lane & 15) * 16;
-  const int voff_plain = lane * bs;
   auto clamp_page = [&](int p) -> int {
     p = p < 0 ? 0 : p;
     return p < nblocks ? p : nblocks - 1;
@@ -1235,57 +1345,9 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
       iq ^= 1;
       ifirst = false;
     }
-    const int tb = itb;
     const int p0 = clamp_page(np0);
     const int p1 = BS16 ? clamp_page(np1) : p0;
-    const uint8_t* kbase = (const uint8_t*)a.key_cache + (int64_t)ih * a.stride_k_head;
-    const uint8_t* vbase = (const uint8_t*)a.value_cache + (int64_t)ih * a.stride_v_head;
-    LDS_AS unsigned char* sk = ring + st * kStageBytes;
-    LDS_AS unsigned char* sv = sk + kKBytes;
-    if (BS16) {
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const uint8_t* kp = kbase + (int64_t)(hh ? p1 : p0) * a.stride_k_block;
-        const uint8_t* vp = vbase + (int64_t)(hh ? p1 : p0) * a.stride_v_block;
-#pragma unroll
-        for (int q2 = 0; q2 < 2; ++q2) lds_dma16(kp + koff_lane + q2 * 1024, sk + hh * kKHalf + q2 * 1024);
-#pragma unroll
-        for (int q2 = 0; q2 < 2; ++q2) lds_dma16(vp + lane * 16 + q2 * 1024, sv + hh * 2048 + q2 * 1024);
-      }
-    } else {
-      const int s0 = tb & (bs - 1);
-      const uint8_t* kp = kbase + (int64_t)p0 * a.stride_k_block + s0 * 16;
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-        for (int q2 = 0; q2 < 2; ++q2)
-          lds_dma16(kp + hh * 256 + q2 * (4 * bs * 16) + koff_lane, sk + hh * kKHalf + q2 * 1024);
-      if (a.trans_v) {
-        const uint8_t* vp = vbase + (int64_t)p0 * a.stride_v_block + (s0 >> 4) * (kHead * 16);
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-          for (int q2 = 0; q2 < 2; ++q2)
-            lds_dma16(vp + hh * 2048 + q2 * 1024 + lane * 16, sv + hh * 2048 + q2 * 1024);
-      } else {
-        const uint8_t* vp = vbase + (int64_t)p0 * a.stride_v_block + s0;
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-          for (int q2 = 0; q2 < 2; ++q2)
-            lds_dma16(vp + hh * 16 + q2 * (64 * bs) + voff_plain, sv + hh * 2048 + q2 * 1024);
-      }
-    }
-    if (PER_TOKEN) {
-      LDS_AS unsigned char* ss = sv + kVBytes;
-      if (lane < 16) {
-        const int tt = (lane & 7) * 4;
-        const int pg2 = BS16 ? (tt >= 16 ? p1 : p0) : p0;
-        const int sidx = BS16 ? (tt & 15) : (tb & (bs - 1)) + tt;
-        const float* base = (lane < 8 ? key_scale : value_scale) + (int64_t)ih * a.stride_ks_head;
-        lds_dma16(base + (int64_t)pg2 * a.stride_ks_block + sidx, ss);
-      }
-    }
+    dma_chunk<PER_TOKEN, BS16>(a, key_scale, value_scale, ring + st * kStageBytes, ih, itb, p0, p1, lane);
     itb += kChunk;
     if (--irem > 0)
       fetch_pages();
@@ -1351,32 +1413,8 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
     }
     // ---- the piece is complete: output row or partial ----
     const float vfin = PER_TOKEN ? st.vsmax : v_tensor_scale;
-    const float L = sum_over_groups(st.lsum[0]);
-    const float m = st.m2[0];
-    const int e = c16;
-    if (e < eq) {
-      const int qi = e / gqa;
-      const int g = e - qi * gqa;
-      const int qh = cur.h * gqa + g;
-      const float sc = L > 0.0f ? vfin / L : 0.0f;
-      if (cur.target < 0) {
-        const int64_t off = (int64_t)(cur.orow + qi) * a.stride_out_tok + (int64_t)qh * a.stride_out_head + 4 * grp;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) store_out4(output, a.output_dtype, off + 16 * j, st.acc[0][j] * sc);
-      } else {
-        int64_t po, pl;
-        if (WORKLIST) {
-          po = (int64_t)(cur.target + qi) * a.stride_po_row + (int64_t)qh * kHead;
-          pl = (int64_t)(cur.target + qi) * a.stride_pl_row + qh;
-        } else {
-          pl = (int64_t)cur.target * eq + e;
-          po = pl * kHead;
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) *(f32x4*)(part_out + po + 16 * j + 4 * grp) = st.acc[0][j] * sc;
-        if (grp == 0) part_lse[pl] = L > 0.0f ? kLn2 * (m + __builtin_amdgcn_logf(L) - 8.0f) : kNegInf;
-      }
-    }
+    store_piece<WORKLIST>(a, output, part_out, part_lse, cur, st.acc[0], sum_over_groups(st.lsum[0]), st.m2[0],
+                          vfin, c16, grp);
     if (!WORKLIST && cur.desc_cnt > 0 && lane == 0)
       *(i32x2*)(segdesc + 2 * ((int64_t)cur.b * a.num_kv_heads + cur.h)) = i32x2{cur.target, cur.desc_cnt};
     st.reset();
@@ -1386,6 +1424,360 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
     has_nxt = has_cur && next_piece(nxt);
     if (iw == 1) iw = 0;
     if (!iok && has_nxt && nxt.n > 0) issue_enter(nxt, 1);
+  }
+}
+
+// ============================================================================
+// Work-list decode: workgroups over consecutive bins
+// ============================================================================
+//
+// The reference plans its persistent route over CU * 3 bins and launches one
+// workgroup per bin (kernels/pa_decode_fp8.py:1766-1771, 3144-3184).  Here a
+// workgroup of W waves takes a run of consecutive bins -- one per CU: every
+// CU's three bins, whose works are contiguous in the work list -- and
+// treats their works, laid end to end, as one sequence of N chunks: wave r
+// takes chunks [rN/W, (r+1)N/W).  A work cut between waves is merged inside
+// the workgroup once every wave is done: each wave leaves the state of its
+// first piece (when cut) and of its last piece (when cut) in its LDS ring,
+// and the wave that holds a cut work's last chunk folds the others' states
+// into it and writes the work's result.  Eight waves of two 8.3 KiB stages
+// each (17 KiB with per-token scales) fill one CU: two waves per SIMD, the
+// same occupancy as the balanced split.
+#ifndef PA_FP8_BIN_WAVES
+#define PA_FP8_BIN_WAVES 8
+#endif
+constexpr int kBinWaves = PA_FP8_BIN_WAVES;
+
+// Walk of this wave's run [r0, r1) of its workgroup's chunk sequence: the
+// works of the workgroup's bins in order, each clipped to the run.  A work
+// with no chunk belongs to the wave whose (non-empty) run contains its
+// position, or the last wave when it sits at the end.
+struct BinWalk {
+  WorklistWalk w;
+  int pos, r0, r1;
+  bool last;
+  __device__ __forceinline__ bool next(Piece& p, const pa_fp8_stream_args& a, const int32_t* kv_indptr,
+                                       const int32_t* context_lengths, const int32_t* work_info,
+                                       const int32_t* partition_indptr) {
+    while (w.next(p, a, kv_indptr, context_lengths, work_info, partition_indptr)) {
+      const int s = pos, e = pos + p.n;
+      pos = e;
+      if (s > r1) {
+        w.idx = w.end;
+        return false;
+      }
+      if (p.n == 0) {
+        if ((s >= r0 && s < r1) || (last && s == r1)) return true;
+        continue;
+      }
+      const int c0 = pa_max(s, r0), c1 = pa_min(e, r1);
+      if (c1 <= c0) continue;
+      p.tb0 += (c0 - s) * kChunk;
+      p.n = c1 - c0;
+      p.cut = (c0 > s ? 1 : 0) | (c1 < e ? 2 : 0);
+      p.wstart = s;
+      return true;
+    }
+    return false;
+  }
+};
+
+// Merge slot of a cut piece in LDS: value-unit accumulators [128 head dims]
+// [16 columns], then the columns' base-2 maxima and sums.
+constexpr int kSlotAcc = kHead * 16 * 4;
+constexpr int kSlotBytes = kSlotAcc + 2 * 16 * 4;
+
+__device__ __forceinline__ void slot_write(LDS_AS unsigned char* slot, const f32x4 (&acc)[8], float m, float L,
+                                           int grp, int c16) {
+  LDS_AS float* f = (LDS_AS float*)slot;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[(16 * j + 4 * grp + i) * 16 + c16] = acc[j][i];
+  if (grp == 0) {
+    f[kSlotAcc / 4 + c16] = m;
+    f[kSlotAcc / 4 + 16 + c16] = L;
+  }
+}
+
+template <bool PER_TOKEN, bool BS16>
+__global__ __launch_bounds__(64 * kBinWaves) void pa_fp8_bin_kernel(
+    const pa_fp8_stream_args a, const int32_t* __restrict__ block_tables, const int32_t* __restrict__ kv_indptr,
+    const int32_t* __restrict__ context_lengths, const float* __restrict__ key_scale,
+    const float* __restrict__ value_scale, const int32_t* __restrict__ work_indptr,
+    const int32_t* __restrict__ work_info, const int32_t* __restrict__ partition_indptr,
+    float* __restrict__ part_out, float* __restrict__ part_lse, void* __restrict__ output) {
+  constexpr int W = kBinWaves;
+  constexpr int kStageBytes = kKBytes + kVBytes + (PER_TOKEN ? kScaleBytes : 0);
+  constexpr int kWaveBytes = 2 * kStageBytes;
+  constexpr int kLoadsPerChunk = 8 + (PER_TOKEN ? 1 : 0);
+  constexpr int kQLoads = 4;  // query row loads per lane
+  static_assert(2 * kSlotBytes <= kWaveBytes, "a wave's two merge slots fit in its ring");
+  __shared__ __attribute__((aligned(16))) unsigned char smem[W * kWaveBytes];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = lane >> 4;
+  const int c16 = lane & 15;
+  // This workgroup's bins [bin0, bin1): an equal share of the plan's.
+  const int bin0 = (int)((int64_t)blockIdx.x * a.num_workers / gridDim.x);
+  const int bin1 = (int)((int64_t)(blockIdx.x + 1) * a.num_workers / gridDim.x);
+  const int ql = a.query_length;
+  const int gqa = a.query_group_size;
+  const int eq = ql * gqa;
+  const int bs = a.block_size;
+  const int bs_shift = BS16 ? 4 : __builtin_ctz((unsigned)bs);
+  const int nblocks = a.num_blocks;
+  const int w0 = ld_uniform(work_indptr, bin0), w1 = ld_uniform(work_indptr, bin1);
+
+  // ---------------- the bins' chunk count and this wave's run ----------------
+  // One work per lane: its chunk count (vector loads of the work, the
+  // sequence's length and first partition), 64 works per pass.
+  auto chunks_of = [&](int wk) -> int {
+    if (wk >= w1) return 0;
+    const int b = work_info[8 * (int64_t)wk];
+    const int kv0 = work_info[8 * (int64_t)wk + 4], kv1 = work_info[8 * (int64_t)wk + 5];
+    const int ctx = context_lengths[b];
+    const int pb = partition_indptr[b];
+    int lo_all, hi_all, u;
+    pa_plan_visible(ctx, 0, ql, a.sliding_window, &lo_all, &u);
+    pa_plan_visible(ctx, ql - 1, ql, a.sliding_window, &u, &hi_all);
+    const int row_len = kv_indptr ? kv_indptr[b + 1] - kv_indptr[b] : a.max_blocks_per_seq;
+    const int last_page = pa_min(pa_cdiv(ctx, bs) - 1, row_len - 1);
+    int tb0, n;
+    work_chunks(ctx, lo_all, hi_all, last_page, pb, kv0, kv1, tb0, n);
+    return n;
+  };
+  auto wave_incl_scan = [&](int v) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(v, o, 64);
+      if (lane >= o) v += t;
+    }
+    return v;
+  };
+  const int n_first = chunks_of(w0 + lane);
+  int N = __builtin_amdgcn_readlane(wave_incl_scan(n_first), 63);
+  for (int base = w0 + 64; base < w1; base += 64) N += __builtin_amdgcn_readlane(wave_incl_scan(chunks_of(base + lane)), 63);
+  const int R0 = (int)((int64_t)wave * N / W), R1 = (int)((int64_t)(wave + 1) * N / W);
+  // First work of the run: the first that ends past R0, or an empty one at
+  // R0 or later.
+  int wstart_idx = w1, spos = N;
+  {
+    int pos = 0;
+    for (int base = w0; base < w1; base += 64) {
+      const int n = base == w0 ? n_first : chunks_of(base + lane);
+      const int incl = wave_incl_scan(n);
+      const int s = pos + incl - n, e = pos + incl;
+      const uint64_t hit = __ballot(base + lane < w1 && (e > R0 || (n == 0 && s >= R0)));
+      if (hit) {
+        const int l = __builtin_amdgcn_readfirstlane((int)__builtin_ctzll(hit));
+        wstart_idx = base + l;
+        spos = __builtin_amdgcn_readlane(s, l);
+        break;
+      }
+      pos += __builtin_amdgcn_readlane(incl, 63);
+    }
+  }
+  BinWalk walk;
+  walk.w.idx = wstart_idx;
+  walk.w.end = w1;
+  walk.pos = spos;
+  walk.r0 = R0;
+  walk.r1 = R1;
+  walk.last = wave == W - 1;
+  auto next_piece = [&](Piece& p) -> bool {
+    return walk.next(p, a, kv_indptr, context_lengths, work_info, partition_indptr);
+  };
+
+  LDS_AS unsigned char* ring = (LDS_AS unsigned char*)smem + wave * kWaveBytes;
+  auto clamp_page = [&](int p) -> int {
+    p = p < 0 ? 0 : p;
+    return p < nblocks ? p : nblocks - 1;
+  };
+
+  // ---------------- piece window and issue cursor (as the stream kernel) ----------------
+  Piece cur, nxt;
+  bool has_cur = next_piece(cur);
+  bool has_nxt = has_cur && next_piece(nxt);
+  int itb = 0, ih = 0, ilast = 0, irem = 0, iw = 0, iorow = 0;
+  int64_t ibt = 0;
+  bool iok = false, ifirst = false;
+  int np0 = 0, np1 = 0;
+  auto fetch_pages = [&]() {
+    const int lp0 = itb >> bs_shift;
+    np0 = ld_uniform(block_tables, ibt + pa_min(lp0, ilast));
+    np1 = BS16 ? ld_uniform(block_tables, ibt + pa_min(lp0 + 1, ilast)) : np0;
+  };
+  auto issue_enter = [&](const Piece& p, int which) {
+    itb = p.tb0;
+    ih = p.h;
+    ibt = p.bt_off;
+    ilast = p.last_page;
+    irem = p.n;
+    iorow = p.orow;
+    iw = which;
+    iok = true;
+    ifirst = true;
+    fetch_pages();
+  };
+  if (has_cur && cur.n > 0)
+    issue_enter(cur, 0);
+  else if (has_nxt && nxt.n > 0)
+    issue_enter(nxt, 1);
+
+  // Query rows of the next piece (lane (grp, c16): column c16's head dims
+  // 16 grp .. +15 and 16 (grp + 4) .. +15), loaded into registers just
+  // before the piece's first chunk, so they retire before it.
+  i32x4 qn[4];
+  auto issue_chunk = [&](int st) -> bool {
+    const bool q = ifirst;
+    if (ifirst) {
+      const int e = pa_min(c16, eq - 1);
+      const int qi = e / gqa;
+      const int g = e - qi * gqa;
+      const uint16_t* qp = (const uint16_t*)a.query + (int64_t)(iorow + qi) * a.stride_q_tok +
+                           (int64_t)(ih * gqa + g) * a.stride_q_head;
+      qn[0] = *(const i32x4*)(qp + 16 * grp);
+      qn[1] = *(const i32x4*)(qp + 16 * grp + 8);
+      qn[2] = *(const i32x4*)(qp + 16 * (grp + 4));
+      qn[3] = *(const i32x4*)(qp + 16 * (grp + 4) + 8);
+      ifirst = false;
+    }
+    dma_chunk<PER_TOKEN, BS16>(a, key_scale, value_scale, ring + st * kStageBytes, ih, itb, clamp_page(np0),
+                               BS16 ? clamp_page(np1) : 0, lane);
+    itb += kChunk;
+    if (--irem > 0)
+      fetch_pages();
+    else if (iw == 0 && has_nxt && nxt.n > 0)
+      issue_enter(nxt, 1);
+    else
+      iok = false;
+    return q;
+  };
+
+  // ---------------- compute side ----------------
+  const float k_tensor_scale = PER_TOKEN ? 1.0f : key_scale[0];
+  const float v_tensor_scale = PER_TOKEN ? 1.0f : value_scale[0];
+  const float logit_scale = a.softmax_scale * kLog2e * k_tensor_scale;
+  const int krow = (c16 >> 3) * kKHalf + (8 * ((c16 >> 2) & 1) + (c16 & 3)) * 16;
+  WaveState<1> st;
+  st.reset();
+  QueryTile<1> qt;
+  // The wave's first piece with chunks, when cut: its state waits in
+  // registers until the ring is free (value units).
+  f32x4 accA[8];
+  float mA = kNegInf, LA = 0.0f;
+  bool hasA = false, hasB = false;
+  Piece pA;
+  pA.cut = 0;
+  pA.wstart = 0;
+  bool first_piece = true;
+  int gc = 0, issued = 0;
+  if (iok) {
+    issue_chunk(0);
+    issued = 1;
+  }
+  while (has_cur) {
+    for (int k = 0; k < cur.n; ++k) {
+      const int stg = gc & 1;
+      if (issued == gc) {
+        issue_chunk(stg);
+        ++issued;
+      }
+      if (k == 0) {
+        // [query rows][chunk gc] are the newest loads: wait for the rows
+        // and turn them into operands before the next issue reuses qn.
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(kLoadsPerChunk));
+        i32x4 qraw[1][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qraw[0][i] = c16 < eq ? qn[i] : i32x4{0, 0, 0, 0};
+        prepare_query<1>(qt, qraw, a.query_dtype, logit_scale, cur.ctx, ql, gqa, a.sliding_window, c16);
+      }
+      if (iok) {
+        ++issued;
+        if (issue_chunk(stg ^ 1))
+          __builtin_amdgcn_s_waitcnt(vmcnt_only(kLoadsPerChunk + kQLoads));
+        else
+          __builtin_amdgcn_s_waitcnt(vmcnt_only(kLoadsPerChunk));
+      } else {
+        __builtin_amdgcn_s_waitcnt(0);
+      }
+      ++gc;
+      compute_chunk<1, PER_TOKEN>(st, qt, ring + stg * kStageBytes, krow, grp, c16, cur.tb0 + k * kChunk);
+    }
+    // ---- the piece is complete ----
+    const float vfin = PER_TOKEN ? st.vsmax : v_tensor_scale;
+    const float L = sum_over_groups(st.lsum[0]);
+    if (cur.cut == 0) {
+      store_piece<true>(a, output, part_out, part_lse, cur, st.acc[0], L, st.m2[0], vfin, c16, grp);
+    } else if (first_piece) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) accA[j] = st.acc[0][j] * vfin;
+      mA = st.m2[0];
+      LA = L;
+      pA = cur;
+      hasA = true;
+    } else {
+      // A cut piece that is not the wave's first ends its run: nothing is
+      // in flight any more, so its state goes to the ring's second slot.
+      f32x4 acc[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = st.acc[0][j] * vfin;
+      slot_write(ring + kSlotBytes, acc, st.m2[0], L, grp, c16);
+      hasB = true;
+    }
+    // An empty work (no chunk) is never cut and does not count as the
+    // wave's first piece: a cut piece right after it starts the run.
+    if (cur.n > 0) first_piece = false;
+    st.reset();
+    cur = nxt;
+    has_cur = has_nxt;
+    has_nxt = has_cur && next_piece(nxt);
+    if (iw == 1) iw = 0;
+    if (!iok && has_nxt && nxt.n > 0) issue_enter(nxt, 1);
+  }
+  (void)hasB;
+
+  // ---------------- cut works: merge across the waves ----------------
+  // Every load of this wave has retired (its last chunk waited for all).
+  if (hasA) slot_write(ring, accA, mA, LA, grp, c16);
+  __syncthreads();
+  // The wave holding a cut work's last chunk (its first piece, cut at the
+  // start, not at the end) merges the work: wave r's piece of it sits in
+  // r's first slot when r's run starts inside the work, else (the work's
+  // first wave) in r's second slot.
+  if (hasA && pA.cut == 1) {
+    const int s = pA.wstart;
+    float M = kNegInf;
+#pragma unroll
+    for (int r = 0; r < W; ++r) {
+      const int Rr = (int)((int64_t)r * N / W), Rn = (int)((int64_t)(r + 1) * N / W);
+      if (r > wave || Rn <= s || Rn <= Rr) continue;
+      const LDS_AS float* f = (const LDS_AS float*)((LDS_AS unsigned char*)smem + r * kWaveBytes +
+                                                     (Rr >= s ? 0 : kSlotBytes));
+      M = fmaxf(M, f[kSlotAcc / 4 + c16]);
+    }
+    const float Mu = M == kNegInf ? 0.0f : M;
+    float L = 0.0f;
+    f32x4 acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < W; ++r) {
+      const int Rr = (int)((int64_t)r * N / W), Rn = (int)((int64_t)(r + 1) * N / W);
+      if (r > wave || Rn <= s || Rn <= Rr) continue;
+      const LDS_AS float* f = (const LDS_AS float*)((LDS_AS unsigned char*)smem + r * kWaveBytes +
+                                                     (Rr >= s ? 0 : kSlotBytes));
+      const float fr = __builtin_amdgcn_exp2f(f[kSlotAcc / 4 + c16] - Mu);
+      L += f[kSlotAcc / 4 + 16 + c16] * fr;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[j][i] += f[(16 * j + 4 * grp + i) * 16 + c16] * fr;
+    }
+    store_piece<true>(a, output, part_out, part_lse, pA, acc, L, M, 1.0f, c16, grp);
   }
 }
 
@@ -1677,31 +2069,8 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
     }
     // ---- the piece is complete: this wave's columns ----
     const float vfin = PER_TOKEN ? st.vsmax : v_tensor_scale;
-    const float L = sum_over_groups(st.lsum[0]);
-    const float m = st.m2[0];
-    if (e < eq) {
-      const int qi = e / gqa;
-      const int g = e - qi * gqa;
-      const int qh = cur.h * gqa + g;
-      const float sc = L > 0.0f ? vfin / L : 0.0f;
-      if (cur.target < 0) {
-        const int64_t off = (int64_t)(cur.orow + qi) * a.stride_out_tok + (int64_t)qh * a.stride_out_head + 4 * grp;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) store_out4(output, a.output_dtype, off + 16 * j, st.acc[0][j] * sc);
-      } else {
-        int64_t po, pl;
-        if (WORKLIST) {
-          po = (int64_t)(cur.target + qi) * a.stride_po_row + (int64_t)qh * kHead;
-          pl = (int64_t)(cur.target + qi) * a.stride_pl_row + qh;
-        } else {
-          pl = (int64_t)cur.target * eq + e;
-          po = pl * kHead;
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) *(f32x4*)(part_out + po + 16 * j + 4 * grp) = st.acc[0][j] * sc;
-        if (grp == 0) part_lse[pl] = L > 0.0f ? kLn2 * (m + __builtin_amdgcn_logf(L) - 8.0f) : kNegInf;
-      }
-    }
+    store_piece<WORKLIST>(a, output, part_out, part_lse, cur, st.acc[0], sum_over_groups(st.lsum[0]), st.m2[0],
+                          vfin, e, grp);
     if (!WORKLIST && cur.desc_cnt > 0 && wave == 0 && lane == 0)
       *(i32x2*)(segdesc + 2 * ((int64_t)cur.b * a.num_kv_heads + cur.h)) = i32x2{cur.target, cur.desc_cnt};
     st.reset();
@@ -2051,13 +2420,44 @@ int coop_waves(int eq) { return eq <= 32 ? 2 : 4; }
 // up to 17 KiB per workgroup; registers: three waves per SIMD).
 int coop_per_cu(int) { return 3; }
 
-// One launch of the per-wave (<= 16 columns) or cooperative kernel.
-template <bool WL>
-hipError_t dispatch_streaming(const pa_fp8_stream_args& a, hipStream_t s, int32_t* desc, float* po, float* pl) {
+// Workgroups of a work-list launch: as many as fit on the GPU at once (one
+// per CU for eight waves, three for three), at most one per bin.
+unsigned bin_workgroups(int bins) {
+  const int cus = device_cu_count();
+  const int per_cu = kBinWaves >= 8 ? 1 : (kBinWaves >= 4 ? 2 : 3);
+  const int fit = cus > 0 ? cus * per_cu : bins;
+  return (unsigned)(bins < fit ? bins : fit);
+}
+
+template <bool PT, bool BS16>
+hipError_t launch_bin(const pa_fp8_stream_args& a, hipStream_t s) {
+  hipLaunchKernelGGL((pa_fp8_bin_kernel<PT, BS16>), dim3(bin_workgroups(a.num_workers)), dim3(64 * kBinWaves), 0, s, a,
+                     a.block_tables, a.kv_indptr, a.context_lengths, a.key_scale, a.value_scale, a.work_indptr,
+                     a.work_info, a.partition_indptr, a.partial_output, a.partial_lse, a.output);
+  return hipGetLastError();
+}
+
+// One launch of the balanced split: per-wave runs (<= 16 columns) or
+// cooperative workgroup runs.
+hipError_t dispatch_balanced(const pa_fp8_stream_args& a, hipStream_t s, int32_t* desc, float* po, float* pl) {
   const int eq = a.query_length * a.query_group_size;
-  if (eq <= 16) return dispatch_stream<WL>(a, (unsigned)pa_cdiv(a.num_workers, kWaves), s, desc, po, pl);
-  return coop_waves(eq) == 2 ? dispatch_coop_nw<2, WL>(a, (unsigned)a.num_workers, s, desc, po, pl)
-                             : dispatch_coop_nw<4, WL>(a, (unsigned)a.num_workers, s, desc, po, pl);
+  if (eq <= 16) return dispatch_stream<false>(a, (unsigned)pa_cdiv(a.num_workers, kWaves), s, desc, po, pl);
+  return coop_waves(eq) == 2 ? dispatch_coop_nw<2, false>(a, (unsigned)a.num_workers, s, desc, po, pl)
+                             : dispatch_coop_nw<4, false>(a, (unsigned)a.num_workers, s, desc, po, pl);
+}
+
+// One launch of the work-list decode, one workgroup per bin: the bin
+// kernel (<= 16 columns) or the cooperative kernel.
+hipError_t dispatch_worklist(const pa_fp8_stream_args& a, hipStream_t s) {
+  const int eq = a.query_length * a.query_group_size;
+  if (eq <= 16) {
+    const bool pt = a.per_token_kv != 0, bs16 = a.block_size == 16;
+    if (pt) return bs16 ? launch_bin<true, true>(a, s) : launch_bin<true, false>(a, s);
+    return bs16 ? launch_bin<false, true>(a, s) : launch_bin<false, false>(a, s);
+  }
+  return coop_waves(eq) == 2
+             ? dispatch_coop_nw<2, true>(a, (unsigned)a.num_workers, s, nullptr, a.partial_output, a.partial_lse)
+             : dispatch_coop_nw<4, true>(a, (unsigned)a.num_workers, s, nullptr, a.partial_output, a.partial_lse);
 }
 
 // Checks shared by both streaming entry points.
@@ -2232,7 +2632,7 @@ int pa_fp8_decode_balanced(const pa_fp8_stream_args* a, void* workspace, int64_t
   int32_t* desc = (int32_t*)(ws + l.desc);
   float* pl = (float*)(ws + l.lse);
   float* po = (float*)(ws + l.out);
-  hipError_t err = dispatch_streaming<false>(*a, (hipStream_t)stream, desc, po, pl);
+  hipError_t err = dispatch_balanced(*a, (hipStream_t)stream, desc, po, pl);
   return err == hipSuccess ? PA_OK : (int)err;
 }
 
@@ -2270,7 +2670,7 @@ int pa_fp8_decode_worklist(const pa_fp8_stream_args* a, void* stream) {
     return PA_ERR_NULL_ARG;
   if (!aligned16(a->partial_output) || (a->stride_po_row % 4)) return PA_ERR_ALIGN;
   if (a->num_seqs == 0) return PA_OK;
-  hipError_t err = dispatch_streaming<true>(*a, (hipStream_t)stream, nullptr, a->partial_output, a->partial_lse);
+  hipError_t err = dispatch_worklist(*a, (hipStream_t)stream);
   return err == hipSuccess ? PA_OK : (int)err;
 }
 

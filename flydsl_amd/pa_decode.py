@@ -693,6 +693,20 @@ def _prepare_worklist(md, output, query, key_cache, value_cache, context_lengths
     return PreparedDecode("ps_split_reduce", s, keep, stream_args=sa, worklist_reduce_args=wr)
 
 
+# Bins of the persistent route per CU (kernels/pa_decode_fp8.py:40, the
+# reference's _PA_METADATA_GRID_OVERSUB): the work-list decode runs one
+# workgroup per bin, and three of its workgroups fit in a CU.
+PA_METADATA_GRID_OVERSUB = 3
+
+
+def metadata_bins(num_cu: int, num_kv_heads: int) -> int:
+    """Bins of :func:`get_pa_metadata`: ``num_cu * 3`` rounded down to a
+    multiple of ``num_kv_heads`` (kernels/pa_decode_fp8.py:1766-1771); at
+    least ``num_kv_heads``."""
+    n = num_cu * PA_METADATA_GRID_OVERSUB
+    return max(num_kv_heads, (n // num_kv_heads) * num_kv_heads)
+
+
 def get_pa_metadata(
     query: torch.Tensor,
     key_cache: torch.Tensor,
@@ -701,27 +715,32 @@ def get_pa_metadata(
     num_query_heads: int,
     num_kv_heads: int,
     partition_size: int = KV_COMPUTE_BLOCK,
+    *,
+    num_cu: Optional[int] = None,
 ):
     """Work list of the persistent route (kernels/pa_decode_fp8.py:1729-1859).
 
     The scheduler of kernels/pa_metadata.py:145-420 runs on the host
     (``pa_fp8_plan_worklist``; the context lengths are copied to the host,
-    the synchronisation the reference makes with ``.item()``).  Bins are the
-    waves the work-list decode keeps resident (``num_sm``), rounded down to a
-    multiple of ``num_kv_heads``.  Returns the reference's keys: work list,
-    reduce maps, ``partition_indptr`` and the float32 partial buffers
-    ``partial_output`` [(n + 1) * ql, 1, Hq, D] / ``partial_lse``
-    [(n + 1) * ql, 1, Hq, 1] with their strides; plus ``partition_size``.
+    the synchronisation the reference makes with ``.item()``) over the
+    reference's bins, ``(num_cu * 3 // num_kv_heads) * num_kv_heads``
+    (:func:`metadata_bins`; 768 on MI355X for 4 or 8 kv heads), so the work
+    list, reduce maps and partition base are the reference's on the same
+    inputs.  ``num_cu`` defaults to the query device's CU count; pass it to
+    plan on the host.  Returns the reference's keys: work list, reduce maps,
+    ``partition_indptr`` and the float32 partial buffers ``partial_output``
+    [(n + 1) * ql, 1, Hq, D] / ``partial_lse`` [(n + 1) * ql, 1, Hq, 1] with
+    their strides; plus ``partition_size``.  All tensors live on the query's
+    device.
     """
     dev = query.device
     batch_size = int(context_lengths.shape[0])
     query_length = query.shape[0] // max(batch_size, 1)
     head_size = int(query.shape[-1])
     gqa = num_query_heads // num_kv_heads
-    eqgs = query_length * gqa
-    num_cu = _cu_count(dev)
-    workers = _lib.stream_workers(num_cu, query_length, gqa, True)
-    num_sm = max(num_kv_heads, (workers // num_kv_heads) * num_kv_heads)
+    if num_cu is None:
+        num_cu = _cu_count(dev)
+    num_sm = metadata_bins(int(num_cu), num_kv_heads)
     ctx_host = context_lengths.detach().to("cpu", torch.int32)
     n_works, plan = _lib.plan_worklist(ctx_host.numpy(), num_kv_heads, gqa, query_length, num_sm, partition_size)
     parts = (ctx_host + (partition_size - 1)) // partition_size

@@ -175,7 +175,10 @@ int pa_fp8_decode_reduce(const pa_fp8_reduce_args* args, void* hip_stream);
  * workgroup walks the pieces (num_workers then counts workgroups).
  *
  * pa_fp8_decode_worklist: pieces come from the work list of
- * pa_fp8_plan_worklist (one bin per wave: num_workers = bins).  Replaces
+ * pa_fp8_plan_worklist, one workgroup per bin (num_workers = bins, the
+ * reference's CU * 3): up to 16 columns its three waves split the bin's
+ * chunks into equal runs and merge works cut between them in LDS; 17..64
+ * columns the cooperative workgroup walks the bin's works.  Replaces
  * compile_pa_decode_metadata(...)["launch"] (kernels/pa_decode_fp8.py:
  * 1030-1721, launched at :3144-3184): a work with partial_qo_loc < 0 writes
  * output rows qo_start + qi; otherwise partial rows ploc + query_length + qi
@@ -233,7 +236,7 @@ typedef struct pa_fp8_stream_args {
   int32_t trans_v;
   int32_t query_dtype;
   int32_t output_dtype;
-  int32_t num_workers; /* runs or bins: waves (<= 16 columns) or workgroups */
+  int32_t num_workers; /* balanced: runs (waves <= 16 columns, else workgroups); work list: bins */
   float softmax_scale;
 } pa_fp8_stream_args;
 

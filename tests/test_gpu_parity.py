@@ -331,25 +331,38 @@ def _subcase(case, seqs):
     return sub
 
 
+# Share of each full-size configuration's sequences checked against the
+# oracle: every sequence of C2 and C4, a quarter of C3 and C5 (whose CPU
+# oracle is several times slower per sequence).
+FULL_SIZE_SHARE = {"c2_llama8b": 1.0, "c3_ragged": 0.25, "c4_window": 1.0, "c5_mtp": 0.25}
+
+
 @pytest.mark.parametrize("name", ["c2_llama8b", "c3_ragged", "c4_window", "c5_mtp"])
 def test_benchmark_config_full_size(name):
-    """Full BASELINE shapes on the GPU; oracle on a sample of sequences
-    (first, last, longest, shortest and a seeded random few)."""
+    """Full BASELINE shapes on the GPU; the oracle checks FULL_SIZE_SHARE of
+    the sequences (always the first, last, longest and shortest, the rest
+    seeded at random), 16 sequences per oracle call."""
     cfg = workloads.CONFIGS[name]
     print(f"[full-size] {name}: building inputs", flush=True)
     case = workloads.build_inputs(cfg, device=DEV, seed=7)
     out, route, _ = launch(case)
     assert not torch.isnan(out).any()
     ctx = case["context_lengths"].cpu()
-    g = torch.Generator().manual_seed(0)
+    want = math.ceil(FULL_SIZE_SHARE[name] * cfg.batch)
     pick = {0, cfg.batch - 1, int(ctx.argmax()), int(ctx.argmin())}
-    pick |= set(torch.randint(0, cfg.batch, (6,), generator=g).tolist())
+    order = torch.randperm(cfg.batch, generator=torch.Generator().manual_seed(0)).tolist()
+    for b in order:
+        if len(pick) >= want:
+            break
+        pick.add(b)
     seqs = sorted(pick)
-    sub = _subcase(case, seqs)
-    ref = torch_oracle(sub, float_out=False)
     ql = cfg.query_length
-    got = torch.cat([out[b * ql : (b + 1) * ql].cpu() for b in seqs])
-    assert_parity(got, ref, f"{name} seqs={seqs}")
+    for i in range(0, len(seqs), 16):
+        part = seqs[i : i + 16]
+        ref = torch_oracle(_subcase(case, part), float_out=False)
+        got = torch.cat([out[b * ql : (b + 1) * ql].cpu() for b in part])
+        assert_parity(got, ref, f"{name} seqs={part}")
+    print(f"[full-size] {name}: route {route}, {len(seqs)} of {cfg.batch} sequences checked", flush=True)
 
 
 @pytest.mark.parametrize("P", [4, 6, 9])

@@ -285,3 +285,52 @@ def test_worklist_graph_capture_replays():
         with torch.cuda.stream(s):
             call()
         torch.cuda.synchronize()
+
+
+# The reference's own case set for this route (tests/kernels/test_pa.py:
+# 1182-1207, normal_accuracy): 1024-token pages, context 1027 (or lengths
+# drawn in [ql, 1027]), (8, 1) and (16, 1) heads, query lengths 1-4, both
+# quantisation modes, batches 3 and 81; pages drawn with replacement
+# (:713-716) and uniform(-1, 1) queries (:700).
+REF_MATRIX = [(h, ql, q, b, v) for h in ((8, 1), (16, 1)) for ql in (1, 2, 3, 4) for q in ("per_token", "per_tensor")
+              for b in (3, 81) for v in (False, True)]
+
+
+@pytest.mark.parametrize("heads,ql,quant,batch,varlen", REF_MATRIX)
+def test_reference_matrix_metadata_route(heads, ql, quant, batch, varlen):
+    import random
+
+    hq, hkv = heads
+    rnd = random.Random(123 + ql * 7 + batch)
+    ctx = [rnd.randint(ql, 1027) for _ in range(batch)] if varlen else [1027] * batch
+    case = make_case(batch=batch, query_length=ql, num_query_heads=hq, num_kv_heads=hkv, block_size=1024, ctx=ctx,
+                     per_token=quant == "per_token", seed=11 * ql + batch, dist="uniform",
+                     extra_pages=3 * sum(math.ceil(c / 1024) for c in ctx))
+    nb = case["key_cache"].shape[0]
+    bt = case["block_tables"]
+    case["block_tables"] = torch.tensor([[rnd.randrange(nb) for _ in range(bt.shape[1])] for _ in range(batch)],
+                                        dtype=torch.int32)
+    print(f"[ref-matrix] heads={heads} ql={ql} {quant} B={batch} varlen={varlen}", flush=True)
+    ref = torch_oracle(case, float_out=False)
+    d = to_dev(case)
+    pages = flat_pages(case)
+    md = pd.get_pa_metadata(d["query"], d["key_cache"], d["context_lengths"], pages[1], hq, hkv)
+    assert md["num_sm"] == pd.metadata_bins(torch.cuda.get_device_properties(0).multi_processor_count, hkv)
+    out, route = run(d, flat=True, metadata=md, pages=pages)
+    assert route == "ps_split_reduce"
+    assert_parity(out, ref, f"ref-matrix heads={heads} ql={ql} {quant} B={batch} varlen={varlen}")
+
+
+def test_worklist_bins_with_many_works():
+    """Three bins of ~70 works each (200 short sequences, one kv head): the
+    bin kernel's pre-pass takes its works 64 at a time."""
+    case = make_case(batch=200, num_query_heads=8, num_kv_heads=1, block_size=1024, ctx_range=(1, 600),
+                     per_token=True, seed=171)
+    ref = torch_oracle(case, float_out=False)
+    d = to_dev(case)
+    pages = flat_pages(case)
+    md = pd.get_pa_metadata(d["query"], d["key_cache"], d["context_lengths"], pages[1], 8, 1, num_cu=1)
+    assert md["num_sm"] == 3
+    assert int(torch.diff(md["work_indptr"].cpu()).max()) > 64
+    out, route = run(d, flat=True, metadata=md, pages=pages)
+    assert_parity(out, ref, "worklist many works per bin")

@@ -58,6 +58,8 @@ def test_recommended_splits_for_benchmark_configs():
     """Values the reference heuristic gives on a 256-CU MI355X."""
     got = {}
     for name, c in CONFIGS.items():
+        if c.block_size not in (16, 64):
+            continue  # the persistent route plans a work list instead
         if c.sliding_window:
             got[name] = plan.get_recommended_splits(c.batch, c.num_kv_heads, sliding_window=c.sliding_window,
                                                     query_length=c.query_length)

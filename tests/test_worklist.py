@@ -181,17 +181,16 @@ def test_planner_rejects_bad_arguments():
     assert lib.pa_fp8_plan_worklist(None, 1, 1, 4, 1, 8, 256, ptr, ptr, ptr, ptr, ptr) == -1
 
 
-def test_get_pa_metadata_keys_and_buffers(monkeypatch):
+def test_get_pa_metadata_keys_and_buffers():
     """get_pa_metadata on CPU tensors: the reference's keys, buffers sized
-    from the plan, bins = resident waves rounded to the kv heads."""
-    monkeypatch.setattr(pd, "_cu_count", lambda device=None: 256)
+    from the plan, the reference's CU * 3 bins rounded to the kv heads."""
     case = make_case(batch=4, block_size=1024, ctx=[100, 3000, 5000, 700], seed=95)
-    md = pd.get_pa_metadata(case["query"], case["key_cache"], case["context_lengths"], None, 8, 2)
+    md = pd.get_pa_metadata(case["query"], case["key_cache"], case["context_lengths"], None, 8, 2, num_cu=256)
     for k in ("work_indptr", "work_info_flat", "partition_indptr", "reduce_indptr", "reduce_final_map",
               "reduce_partial_map", "num_sm", "partial_output", "partial_lse", "stride_po_partial",
               "stride_pl_partial", "stride_po_ql", "stride_pl_ql", "query_length"):
         assert k in md, k
-    assert md["num_sm"] == _lib.stream_workers(256, 1, 4, True) == 2048
+    assert md["num_sm"] == 768
     assert md["partition_indptr"].tolist() == [0, 1, 13, 33, 36]
     ref = worklist.pa_metadata_v1(case["context_lengths"].tolist(), 2, 4, 1, md["num_sm"], 256)
     n = ref["num_works"]
@@ -200,3 +199,153 @@ def test_get_pa_metadata_keys_and_buffers(monkeypatch):
     assert tuple(md["partial_output"].shape) == ((npart + 1) * 1, 1, 8, 128)
     assert tuple(md["partial_lse"].shape) == ((npart + 1) * 1, 1, 8, 1)
     assert md["stride_po_ql"] == 8 * 128 and md["stride_pl_ql"] == 8
+
+
+def test_metadata_bins_are_the_references():
+    """(CU * 3 // Hkv) * Hkv (kernels/pa_decode_fp8.py:1766-1771): 768 on a
+    256-CU MI355X for 1, 2, 3, 4, 8 kv heads; 765 for 5."""
+    for h, want in [(1, 768), (2, 768), (3, 768), (4, 768), (5, 765), (8, 768), (7, 763)]:
+        assert pd.metadata_bins(256, h) == want
+    assert pd.metadata_bins(304, 8) == 912  # MI300X
+    assert pd.metadata_bins(1, 8) == 8
+
+
+@pytest.mark.parametrize("H,ql,kind", [(8, 1, "ragged"), (4, 4, "uniform"), (1, 2, "zeros"), (2, 1, "aligned")])
+def test_get_pa_metadata_bits_at_reference_bins(H, ql, kind):
+    """Every buffer get_pa_metadata returns equals the restatement planned
+    over 768 bins, bit for bit (valid prefixes), on a ragged 1024-page
+    batch."""
+    rng = np.random.default_rng(H * 31 + ql)
+    B = 97
+    ctx = [max(c, ql) for c in _ctxs(rng, B, kind)] if kind != "zeros" else _ctxs(rng, B, kind)
+    q = torch.zeros(B * ql, H * 4, 128, dtype=torch.bfloat16)
+    kc = torch.zeros(1, H, 8, 1024, 16, dtype=torch.uint8)
+    cl = torch.tensor(ctx, dtype=torch.int32)
+    md = pd.get_pa_metadata(q, kc, cl, None, H * 4, H, num_cu=256)
+    ref = worklist.pa_metadata_v1(ctx, H, 4, ql, 768, 256)
+    n = ref["num_works"]
+    assert md["num_sm"] == 768
+    assert torch.equal(md["work_indptr"], torch.from_numpy(ref["work_indptr"]))
+    assert int(md["work_indptr"][-1]) == n
+    assert torch.equal(md["work_info_flat"][: 8 * n], torch.from_numpy(ref["work_info"][:n].reshape(-1)))
+    assert torch.equal(md["reduce_indptr"], torch.from_numpy(ref["reduce_indptr"]))
+    g = ref["num_groups"]
+    assert torch.equal(md["reduce_final_map"][:g], torch.from_numpy(ref["reduce_final_map"][:g]))
+    used = int(ref["reduce_indptr"][-1])
+    assert torch.equal(md["reduce_partial_map"][:used], torch.from_numpy(ref["reduce_partial_map"][:used]))
+    parts = [-(-c // 256) for c in ctx]
+    assert md["partition_indptr"].tolist() == [0] + np.cumsum(parts).tolist()
+    assert capacity_violations(ref, ctx, H, 768, 256) == []
+
+
+# ---------------------------------------------------------------------------
+# Exact capacities.  kernels/pa_metadata.py:196-221 gives bin c the capacity
+# average + (c % nspk < reminder) partitions (nspk = bins per kv head); the
+# loop at :228-398 fills bins in order, each kv head's partitions laid end
+# to end, closing a bin when its capacity is spent (a finished sequence
+# leaves the rest of the capacity to the next one, :300-318), and starts the
+# next kv head at the bin after its last (:411-417).  So every bin holds
+# exactly min(capacity, partitions still unplaced) of one kv head, in order,
+# and only a sequence with no partition yields an empty work.
+# ---------------------------------------------------------------------------
+
+
+def capacity_violations(plan, ctx, H, num_cu, gran):
+    parts = [-(-max(c, 0) // gran) for c in ctx]
+    pbase = np.concatenate([[0], np.cumsum(parts)]).astype(int)
+    S = int(sum(parts))
+    nspk = num_cu // H
+    avg, rem = divmod(S, nspk)
+    cap = lambda c: avg + (1 if c % nspk < rem else 0)
+    n = plan["num_works"]
+    wi, info = plan["work_indptr"], plan["work_info"][:n]
+    out = []
+    # expected: (kv head, load) per bin
+    want = [(None, 0)] * num_cu
+    c = 0
+    for kh in range(H):
+        left = S
+        while left > 0 and c < num_cu:
+            take = min(cap(c), left)
+            want[c] = (kh, take)
+            left -= take
+            if left > 0:
+                c += 1
+        c += 1
+    pos = [0] * H  # next cumulative partition expected, per kv head
+    for c in range(num_cu):
+        ws = range(int(wi[c]), int(wi[c + 1]))
+        load = sum(int(info[w, 5] - info[w, 4]) for w in ws)
+        if load != want[c][1]:
+            out.append(("load", c, load, want[c][1]))
+        for w in ws:
+            b, kv0, kv1 = int(info[w, 0]), int(info[w, 4]), int(info[w, 5])
+            kh = (int(info[w, 7]) & 0xFFFF) // 4
+            if kv1 <= kv0:
+                if parts[b] != 0:
+                    out.append(("empty work", c, w, b))
+                continue
+            if kh != want[c][0]:
+                out.append(("head", c, w, kh, want[c][0]))
+            if kv0 != pos[kh]:
+                out.append(("order", c, w, kv0, pos[kh]))
+            pos[kh] = kv1
+    for kh in range(H):
+        if pos[kh] != pbase[-1]:
+            out.append(("placed", kh, pos[kh], int(pbase[-1])))
+    return out
+
+
+@pytest.mark.parametrize("B,H,ql,kind", CASES)
+def test_plan_exact_capacities(B, H, ql, kind):
+    rng = np.random.default_rng(B * 7 + H * 3 + ql)
+    ctx = _ctxs(rng, B, kind)
+    for bins_per_head in (1, 2, 3, 7, 40, 96, 768):
+        for gran in (256, 16):
+            num_cu = H * bins_per_head
+            p = worklist.pa_metadata_v1(ctx, H, 4, ql, num_cu, gran)
+            assert capacity_violations(p, ctx, H, num_cu, gran) == [], (bins_per_head, gran)
+
+
+def _mutant(old, new):
+    """The restated planner with one planted mistake (test-only)."""
+    import inspect
+    import textwrap
+
+    src = textwrap.dedent(inspect.getsource(worklist.pa_metadata_v1))
+    assert src.count(old) == 1, old
+    ns = dict(vars(worklist))
+    exec(compile(src.replace(old, new), "<mutant>", "exec"), ns)
+    return ns["pa_metadata_v1"]
+
+
+@pytest.mark.parametrize("old,new", [
+    ("do_finish = remain >= remain_kv", "do_finish = remain > remain_kv"),            # finish test slip
+    ("return average + (1 if c % nspk < reminder else 0)",
+     "return average + (1 if c % nspk <= reminder else 0)"),                          # one extra +1 bin
+    ("return average + (1 if c % nspk < reminder else 0)",
+     "return average + (1 if c < reminder else 0)"),                                  # +1 bins of head 0 only
+    ("s_kv_end = min(kv_start + remain, kvend)", "s_kv_end = min(kv_start + remain + 1, kvend)"),
+])
+def test_capacity_invariants_catch_planted_mistakes(old, new):
+    """Each planted slip breaks the exact-capacity invariants on some batch
+    (the load-only bound and the tiling checks let the first three pass)."""
+    bad = _mutant(old, new)
+    rng = np.random.default_rng(5)
+    caught = False
+    for trial in range(40):
+        B = int(rng.integers(3, 40))
+        H = int(rng.choice([1, 2, 4, 8]))
+        ctx = _ctxs(rng, B, ["uniform", "ragged", "aligned"][trial % 3])
+        for bph in (3, 7, 40):
+            try:
+                p = bad(ctx, H, 4, 1, H * bph, 256)
+            except (IndexError, ValueError):
+                caught = True
+                break
+            if capacity_violations(p, ctx, H, H * bph, 256):
+                caught = True
+                break
+        if caught:
+            break
+    assert caught
