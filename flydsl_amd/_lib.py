@@ -32,6 +32,7 @@ ERRORS = {
     -6: "PA_ERR_SHAPE",
     -7: "PA_ERR_ALIGN",
     -8: "PA_ERR_ABI",
+    -9: "PA_ERR_SCRATCH",
 }
 
 EXPORTED_SYMBOLS = (
@@ -45,6 +46,8 @@ EXPORTED_SYMBOLS = (
     "pa_fp8_decode_worklist",
     "pa_fp8_decode_balanced",
     "pa_fp8_merge_balanced",
+    "pa_fp8_decode_balanced_static",
+    "pa_fp8_static_scratch_bytes",
     "pa_fp8_balanced_workspace_bytes",
     "pa_fp8_stream_workers",
     "pa_fp8_reduce_worklist",
@@ -377,6 +380,10 @@ def load(path: Optional[str] = None) -> ctypes.CDLL:
     lib.pa_fp8_decode_balanced.restype = ctypes.c_int
     lib.pa_fp8_merge_balanced.argtypes = [ctypes.POINTER(StreamArgs), _vp, _i64, _vp]
     lib.pa_fp8_merge_balanced.restype = ctypes.c_int
+    lib.pa_fp8_decode_balanced_static.argtypes = [ctypes.POINTER(StreamArgs), _vp]
+    lib.pa_fp8_decode_balanced_static.restype = ctypes.c_int
+    lib.pa_fp8_static_scratch_bytes.argtypes = []
+    lib.pa_fp8_static_scratch_bytes.restype = _i64
     lib.pa_fp8_balanced_workspace_bytes.argtypes = [ctypes.c_int] * 5
     lib.pa_fp8_balanced_workspace_bytes.restype = _i64
     lib.pa_fp8_stream_workers.argtypes = [ctypes.c_int] * 4

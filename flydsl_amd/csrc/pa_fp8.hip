@@ -33,6 +33,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "pa_fp8.h"
@@ -2502,6 +2504,40 @@ BalancedLayout balanced_layout(int B, int H, int eq, int nw) {
   return l;
 }
 
+// Device scratch of pa_fp8_decode_balanced_static: the balanced split's
+// workspace (pair descriptors, partial lse, partial rows) for callers that
+// cannot allocate.  Each device holds its own copy for the life of the
+// process; the kernels take its device address (kept per device below),
+// never this name, which in host code is only a stand-in.
+constexpr int64_t kStaticScratchBytes = (int64_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of the current device's scratch, looked up once per device
+// (with that device current) by its first call.
+int static_scratch(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return PA_ERR_SHAPE;
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return (int)e;
+      if (p == nullptr) return PA_ERR_NULL_ARG;
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return PA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -2663,6 +2699,24 @@ int pa_fp8_merge_balanced(const pa_fp8_stream_args* a, const void* workspace, in
   return err == hipSuccess ? PA_OK : (int)err;
 }
 
+int pa_fp8_decode_balanced_static(const pa_fp8_stream_args* a, void* stream) {
+  int rc = check_stream_args(a);
+  if (rc != PA_OK) return rc;
+  if (a->num_seqs > 1024) return PA_ERR_SHAPE;
+  const int eq = a->query_length * a->query_group_size;
+  const BalancedLayout l = balanced_layout(a->num_seqs, a->num_kv_heads, eq, a->num_workers);
+  if (l.total > kStaticScratchBytes) return PA_ERR_SCRATCH;
+  if (a->num_seqs == 0) return PA_OK;
+  void* ws = nullptr;
+  rc = static_scratch(&ws);
+  if (rc != PA_OK) return rc;
+  rc = pa_fp8_decode_balanced(a, ws, l.total, stream);
+  if (rc != PA_OK) return rc;
+  return pa_fp8_merge_balanced(a, ws, l.total, stream);
+}
+
+int64_t pa_fp8_static_scratch_bytes(void) { return kStaticScratchBytes; }
+
 int pa_fp8_decode_worklist(const pa_fp8_stream_args* a, void* stream) {
   int rc = check_stream_args(a);
   if (rc != PA_OK) return rc;
@@ -2750,6 +2804,7 @@ const char* pa_fp8_error_string(int code) {
     case PA_ERR_SHAPE: return "invalid dimension";
     case PA_ERR_ALIGN: return "pointer or stride not 16-byte aligned";
     case PA_ERR_ABI: return "abi_version mismatch";
+    case PA_ERR_SCRATCH: return "the call needs more workspace than the library's static scratch (64 MiB)";
     default: return hipGetErrorString((hipError_t)code);
   }
 }

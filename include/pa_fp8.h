@@ -5,8 +5,10 @@
  * split-context decode of the reference's `pa_decode_ps_launch` routes and a
  * few host-side planning helpers.  Every tensor is passed as a raw device
  * pointer plus element strides; the library never allocates device memory
- * and keeps no mutable global state, so calls are re-entrant and may be
- * captured into a HIP graph when the caller preallocates every buffer.
+ * and keeps no mutable global state (except the per-device address of the
+ * static scratch of pa_fp8_decode_balanced_static, looked up once), so calls
+ * are re-entrant and may be captured into a HIP graph when the caller
+ * preallocates every buffer.
  *
  * Return codes: 0 on success, a positive hipError_t value when the HIP
  * runtime rejects a launch, or one of the negative PA_ERR_* codes below for
@@ -52,6 +54,7 @@ enum pa_fp8_error {
   PA_ERR_SHAPE = -6,          /* non-positive dimension or partition count */
   PA_ERR_ALIGN = -7,          /* a pointer or stride breaks 16-byte alignment */
   PA_ERR_ABI = -8,            /* struct abi_version mismatch */
+  PA_ERR_SCRATCH = -9,        /* workspace beyond the static scratch of pa_fp8_decode_balanced_static */
 };
 
 /*
@@ -247,6 +250,24 @@ int pa_fp8_merge_balanced(const pa_fp8_stream_args* args, const void* workspace,
                           void* hip_stream);
 int64_t pa_fp8_balanced_workspace_bytes(int num_seqs, int num_kv_heads, int query_length, int query_group_size,
                                         int num_workers);
+/*
+ * pa_fp8_decode_balanced_static: pa_fp8_decode_balanced followed by
+ * pa_fp8_merge_balanced (same kernels, same results), with the workspace
+ * taken from a static device array of the library instead of an argument,
+ * so the call allocates nothing (no hipMalloc, no allocating library call).
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation).  The array holds pa_fp8_static_scratch_bytes() = 64 MiB per
+ * device, for the life of the process; a call whose workspace
+ * (pa_fp8_balanced_workspace_bytes) exceeds it returns PA_ERR_SCRATCH.
+ * Every call on a device shares that device's array: calls that overlap on
+ * one device (other streams, other host threads) race and must be
+ * serialised by the caller.  The workspace needs no initialisation, so
+ * nothing is cleared between calls.
+ */
+int pa_fp8_decode_balanced_static(const pa_fp8_stream_args* args, void* hip_stream);
+int64_t pa_fp8_static_scratch_bytes(void);
+
 /* Runs a streaming launch keeps resident on num_cu CUs: waves for up to 16
  * query columns (4 per workgroup; two workgroups per CU when their LDS
  * fits, else one), cooperative workgroups for 17..64 columns. */

@@ -132,3 +132,31 @@ def test_struct_layout_matches_header(tmp_path, struct, cname):
     vals = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
     assert vals[0] == ctypes.sizeof(struct)
     assert vals[1:] == [getattr(struct, f).offset for f in fields]
+
+
+def test_static_scratch_entry_checks_before_any_gpu_call():
+    """pa_fp8_decode_balanced_static validates like pa_fp8_decode_balanced
+    and refuses a workspace beyond its 64 MiB static scratch (PA_ERR_SCRATCH)
+    before touching the device."""
+    lib = _lib.load()
+    assert lib.pa_fp8_static_scratch_bytes() == 64 << 20
+    assert lib.pa_fp8_decode_balanced_static(None, None) == -1
+    sa = _lib.StreamArgs()
+    sa.abi_version = 99
+    assert lib.pa_fp8_decode_balanced_static(ctypes.byref(sa), None) == -8
+    sa.abi_version = _lib.ABI_VERSION
+    for f in ("output", "query", "key_cache", "value_cache", "block_tables", "context_lengths", "key_scale",
+              "value_scale"):
+        setattr(sa, f, 4096)  # aligned stand-ins; nothing is dereferenced on these paths
+    sa.head_size, sa.block_size, sa.num_blocks, sa.max_blocks_per_seq = 128, 16, 64, 4
+    sa.num_seqs, sa.num_kv_heads, sa.query_length, sa.query_group_size = 8, 4, 4, 16
+    sa.query_dtype = sa.output_dtype = _lib.DTYPE_BF16
+    sa.stride_q_tok, sa.stride_q_head, sa.stride_out_tok, sa.stride_out_head = 64 * 128, 128, 64 * 128, 128
+    sa.stride_k_block, sa.stride_k_head, sa.stride_v_block, sa.stride_v_head = 4 * 2048, 2048, 4 * 2048, 2048
+    sa.num_workers = 2048  # 64 columns x 2048 runs: 128 MiB of partial rows
+    need = _lib.balanced_workspace_bytes(8, 4, 4, 16, 2048)
+    assert need > 64 << 20
+    assert lib.pa_fp8_decode_balanced_static(ctypes.byref(sa), None) == -9
+    assert lib.pa_fp8_error_string(-9).startswith(b"the call needs more workspace")
+    sa.num_seqs = 1025  # the balanced split's batch limit
+    assert lib.pa_fp8_decode_balanced_static(ctypes.byref(sa), None) == -6
