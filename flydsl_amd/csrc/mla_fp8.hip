@@ -36,10 +36,16 @@
 //     value dims d0+c (low dword) and d0+16+c (high dword), i.e. the A
 //     operands of two 16-dim row tiles with the same token order as P^T.
 // The O^T accumulators are 32 heads x 512 dims per wave (256 registers).
-// Softmax is base 2 with a lazy rescale: the reference maximum of a head
-// moves only when a block's maximum exceeds it by more than 8, so p <= 256
-// stays inside e4m3fn and the 256-register rescale runs on the first block
-// of a work and rarely after.
+// Softmax is base 2 against a per-head reference exponent m0, set on a
+// work's first block to the head's maximum + 40; the accumulators and the
+// denominator stay in units of 2^m0.  Each half block's probabilities are
+// p = 2^(x - e) <= 1 with e = ceil(max of the lane pair) and enter the value
+// product with the e8m0 block scale 2^(e - m0), clamped to 2^-127 .. 2^127
+// (logits more than 127 below m0 count as 2^-127 of m0, i.e. nothing).  A
+// half block whose head maximum lies more than 64 above m0 (rare: it needs
+// logits that grow by over 44 nats inside one work) first moves m0 to its
+// maximum + 40 and multiplies the head's 128 accumulators and its sum by
+// 2^(old - new), so e - m0 never exceeds 65 and nothing overflows.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -72,6 +78,10 @@ constexpr int kDmaPerWave = kQkDim / 32;     // 18 instructions of 1 KiB
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.69314718055994531f;
 constexpr float kNegInf = -__builtin_inff();
+// A head's block maximum this far (base 2) above its reference exponent m0
+// moves m0 (the e8m0 block scales reach 2^127; accumulators and sums stay
+// far from float overflow).
+constexpr float kRescaleMargin = 64.f;
 
 static_assert(kGroupBytes * 4 == kStageBytes, "four 32-token groups per stage");
 static_assert(kQuadBytes * (kQkDim / 64) == kGroupBytes, "9 quads per group");
@@ -134,6 +144,23 @@ __device__ __forceinline__ f32x4 read_acc(const f32x4& acc) {
   return r;
 }
 __device__ __forceinline__ void agpr_settle() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
+
+// Rare path of the softmax: head tile ht's accumulators times f (a power of
+// two, exact).  The scaled tiles go back to AGPRs; the asm statements that
+// take them as in/out operands keep every write ahead of the next value
+// product, whose MFMAs wait their own two states.
+__device__ __forceinline__ void rescale_acc(f32x4 (&o)[16][2][2], int ht, float f) {
+  agpr_settle();
+#pragma unroll
+  for (int db = 0; db < 16; ++db)
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) o[db][rt][ht] = read_acc(o[db][rt][ht]) * f;
+#pragma unroll
+  for (int db = 0; db < 16; db += 4)
+    asm volatile("s_nop 1"
+                 : "+a"(o[db][0][ht]), "+a"(o[db][1][ht]), "+a"(o[db + 1][0][ht]), "+a"(o[db + 1][1][ht]),
+                   "+a"(o[db + 2][0][ht]), "+a"(o[db + 2][1][ht]), "+a"(o[db + 3][0][ht]), "+a"(o[db + 3][1][ht]));
+}
 
 __device__ __forceinline__ void lds_dma16(const void* gsrc, LDS_AS void* ldst) {
   __builtin_amdgcn_global_load_lds(gsrc, ldst, 16, 0, 2);
@@ -483,9 +510,18 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
         float x = kNegInf;
 #pragma unroll
         for (int t = 0; t < 4; ++t) x = fmaxf(x, fmaxf(fmaxf(s[t][ht][0], s[t][ht][1]), fmaxf(s[t][ht][2], s[t][ht][3])));
-        if (half == 0 && first) {
-          const float hm = max_over_groups(x);
-          m0[ht] = hm == kNegInf ? 0.f : __builtin_ceilf(hm) + 40.f;
+        const float hm = max_over_groups(x);  // the head's maximum over this half block
+        if (half == 0 && first) m0[ht] = hm == kNegInf ? 0.f : __builtin_ceilf(hm) + 40.f;
+        const bool up = hm > m0[ht] + kRescaleMargin;
+        if (__builtin_expect(__ballot(up) != 0, 0)) {
+          // move m0: the denominator, the first half's block exponents and
+          // (past the work's first block) the accumulators follow it
+          const float mn = up ? __builtin_ceilf(hm) + 40.f : m0[ht];
+          const float f = __builtin_amdgcn_exp2f(m0[ht] - mn);
+          lsum[ht] *= f;
+          if (half == 1) kexp[0][ht] = max(kexp[0][ht] + (int)(m0[ht] - mn), -127);
+          m0[ht] = mn;
+          if (!first) rescale_acc(o, ht, f);
         }
         const float xp = max_over_pair(x);
         // exponents beyond m0 +- 127 leave the e8m0 range
@@ -552,7 +588,10 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
         for (int db = 0; db < 16; ++db)
 #pragma unroll
           for (int rt = 0; rt < 2; ++rt) {
-            const f32x4 v = read_acc(o[db][rt][ht]) * inv;
+            f32x4 v = read_acc(o[db][rt][ht]) * inv;
+            // an empty range (l = 0) stores zeros whatever its page held
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = l > 0.f ? v[i] : 0.f;
             const int d = 32 * db + 16 * rt + 4 * g;
             if (direct) {
               const uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);

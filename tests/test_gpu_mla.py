@@ -43,23 +43,45 @@ DEV = "cuda:0"
 FP8 = torch.float8_e4m3fn
 
 
-def make_case(lens, seed, extra_pages=7):
+def make_case(lens, seed, extra_pages=7, wide=None, nan_page0=False):
+    """wide = (boost, fractions): rows at those fractions of each sequence get
+    keys aligned with the (head-shared) query direction, scaled so their
+    logits reach about `boost` nats.  nan_page0: no sequence uses page 0,
+    whose bytes are all 0x7f (e4m3fn NaN)."""
     g = torch.Generator().manual_seed(seed)
     B = len(lens)
     kv_indptr = torch.zeros(B + 1, dtype=torch.int32)
     kv_indptr[1:] = torch.cumsum(torch.tensor(lens, dtype=torch.int32), 0)
     total = int(kv_indptr[-1])
     num_pages = total + extra_pages
-    kv_indices = torch.randperm(num_pages, generator=g)[:total].to(torch.int32)
-    kv = torch.randn(num_pages, 1, 1, QK_HEAD_DIM, generator=g).to(torch.bfloat16).to(FP8)
-    q = torch.randn(B, 128, QK_HEAD_DIM, generator=g).to(torch.bfloat16).to(FP8)
+    first = 1 if nan_page0 else 0
+    kv_indices = (torch.randperm(num_pages - first, generator=g)[:total] + first).to(torch.int32)
+    kv = torch.randn(num_pages, 1, 1, QK_HEAD_DIM, generator=g)
+    q = torch.randn(B, 128, QK_HEAD_DIM, generator=g)
+    if wide is not None:
+        boost, fracs = wide
+        # one query direction for every head (plus a little noise), and keys
+        # along its sign pattern: logit ~ a * sum |q| / 24
+        base = torch.randn(QK_HEAD_DIM, generator=g)
+        q = base + 0.05 * torch.randn(B, 128, QK_HEAD_DIM, generator=g)
+        a = boost * 24.0 / float(base.abs().sum())
+        a = float(torch.tensor(a).to(torch.bfloat16).to(FP8).float())
+        for b in range(B):
+            n = lens[b]
+            for f0, f1 in fracs:
+                for t in range(int(f0 * n), max(int(f1 * n), int(f0 * n) + 1)):
+                    kv[int(kv_indices[int(kv_indptr[b]) + t]), 0, 0] = a * torch.sign(base)
+    kv = kv.to(torch.bfloat16).to(FP8)
+    q = q.to(torch.bfloat16).to(FP8)
+    if nan_page0:
+        kv.view(torch.uint8)[0].fill_(0x7F)
     qo_indptr = torch.arange(B + 1, dtype=torch.int32)
     last = torch.ones(B, dtype=torch.int32)
     return q, kv, qo_indptr, kv_indptr, kv_indices, last
 
 
-def run(lens, seed=0, num_cu=None, precise=False):
-    q, kv, qo_indptr, kv_indptr, kv_indices, last = make_case(lens, seed)
+def run(lens, seed=0, num_cu=None, precise=False, **case_kw):
+    q, kv, qo_indptr, kv_indptr, kv_indices, last = make_case(lens, seed, **case_kw)
     B = len(lens)
     sizes = get_mla_metadata_info_v1(B, 1, 128, FP8, FP8, num_cu=num_cu)
     bufs = [torch.empty(s, dtype=t, device=DEV) for s, t in sizes]
@@ -147,7 +169,9 @@ def test_many_small_pieces():
 
 
 def test_empty_sequence_writes_zeros():
-    r = run([0, 200, 0], seed=14, num_cu=2)
+    """Empty ranges write zeros even when the page their DMA touches (page 0)
+    holds NaN bytes."""
+    r = run([0, 200, 0], seed=14, num_cu=2, nan_page0=True)
     assert np.all(r["out"][0] == 0) and np.all(r["out"][2] == 0)
     want, _, wabs = om.mla_decode_ref(r["q"], r["kv"], r["qo"], r["kvp"], r["kvi"], r["sm"])
     assert np.all(np.abs(r["out"][1] - want[1]) <= tolerance(wabs[1], want[1], False))
@@ -157,3 +181,17 @@ def test_rerun_is_deterministic():
     a = run([3000, 900], seed=15, num_cu=16)
     b = run([3000, 900], seed=15, num_cu=16)
     assert np.array_equal(a["out"], b["out"])
+
+
+@pytest.mark.parametrize("precise", [False, True])
+def test_wide_logits_with_late_maxima(precise):
+    """Logits spanning ~150 nats whose maxima sit late in a work (the last
+    tenth of every sequence, and a run in the middle that ends pieces when
+    the rows are cut): the reference exponent set on a work's first block
+    has to move (the softmax's rare rescale), and nothing overflows."""
+    lens = [5000, 3000, 777, 9000]
+    r = run(lens, seed=21, num_cu=5, precise=precise, wide=(150.0, [(0.9, 1.0), (0.45, 0.5)]))
+    assert np.all(np.isfinite(r["out"]))
+    want, want_lse, _ = om.mla_decode_ref(r["q"], r["kv"], r["qo"], r["kvp"], r["kvi"], r["sm"])
+    assert float(np.min(want_lse)) > 120.0  # the boosted rows dominate every head
+    check(r, precise=precise)
