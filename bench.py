@@ -6,7 +6,8 @@ KV heads, head 128, 16-token pages, every context 4096, per-tensor fp8
 scales) unless ``--config`` names another.
 
 A step is one ``pa_decode_ps_launch`` call as the reference harness makes
-it (recommended split count; the window route with preallocated partials):
+it (recommended split count; the window route with preallocated partials;
+the persistent route with the work list planned once):
 one launch when workgroups own whole (sequence, kv head) pairs, else the
 partition pass plus the LSE reduce.  Inputs are resident in HBM; the timed steps
 rotate over several independent KV-cache copies whose total exceeds twice
@@ -43,6 +44,7 @@ if ROOT not in sys.path:
 
 PEAK_HBM_GBPS = 8000.0
 MALL_BYTES = 256 * 1024 * 1024
+WARMUP_SECONDS = 0.2  # minimum untimed warm-up before each timed loop
 
 
 def parse_args():
@@ -261,9 +263,15 @@ def run_config(name: str, args) -> dict:
                                    case["softmax_scale"], ks, vs, sliding_window=cfg.sliding_window,
                                    block_tables=bt_arg, max_context_partition_num=P, **sw_scratch)
 
-    route = None
-    for i in range(args.warmup):
-        route = step(i)
+    route, warm = None, 0
+    t_warm = time.perf_counter()
+    # W warm-up steps, and at least WARMUP_SECONDS of them: the GPU's clocks
+    # take a few milliseconds of load to settle, longer than W short steps.
+    while warm < args.warmup or time.perf_counter() - t_warm < WARMUP_SECONDS:
+        route = step(warm)
+        warm += 1
+        if warm % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -285,8 +293,13 @@ def run_config(name: str, args) -> dict:
                                        block_tables=bt_arg, max_context_partition_num=P, **sw_scratch))
     kernel_name, _ = calls[0].kernels()[0]
     decode = [c.kernels()[0][1] for c in calls]
-    for i in range(max(3, args.warmup)):
+    t_warm = time.perf_counter()
+    i = 0
+    while i < max(3, args.warmup) or time.perf_counter() - t_warm < WARMUP_SECONDS:
         calls[i % copies].launch()
+        i += 1
+        if i % 8 == 0:
+            torch.cuda.synchronize()
     k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     k0.record(stream)
@@ -307,7 +320,7 @@ def run_config(name: str, args) -> dict:
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": warm,
         "ms_per_step": round(ms, 5),
         "us_per_step": round(ms * 1e3, 2),
         "pct_of_peak": round(100.0 * value / PEAK_HBM_GBPS, 2),

@@ -299,7 +299,11 @@ __device__ __forceinline__ void prepare_query(QueryTile<NCG>& q, const i32x4 (&q
     amax = max_over_groups(amax);
     int sexp = 261 - (int)((__float_as_uint(amax) >> 23) & 0xffu);
     sexp = sexp < 1 ? 1 : (sexp > 254 ? 254 : sexp);
-    const float sq = amax > 0.0f ? __uint_as_float((uint32_t)sexp << 23) : 1.0f;
+    // The logit factor's sign (a launch constant: softmax scale times the
+    // per-tensor key scale) goes into the query, so the column factor is
+    // positive and the softmax takes its maxima on raw logits.
+    const float sq0 = amax > 0.0f ? __uint_as_float((uint32_t)sexp << 23) : 1.0f;
+    const float sq = logit_scale < 0.0f ? -sq0 : sq0;
 #pragma unroll
     for (int sI = 0; sI < 4; ++sI) {
       float xs[8];
@@ -312,7 +316,9 @@ __device__ __forceinline__ void prepare_query(QueryTile<NCG>& q, const i32x4 (&q
       q.lo[cg][2 * sI] = (int)(uint32_t)lo;
       q.lo[cg][2 * sI + 1] = (int)(uint32_t)((uint64_t)lo >> 32);
     }
-    q.fac[cg] = logit_scale / sq;
+    // > 0; a zero scale gives a tiny factor (all logits ~0, masked -inf
+    // stays -inf rather than 0 * -inf)
+    q.fac[cg] = fmaxf(logit_scale / sq, 1e-30f);
     int lo = 0, hi = 0;
     if (valid) pa_plan_visible(ctx, qi, ql, W, &lo, &hi);
     q.vis_lo[cg] = lo;
@@ -418,12 +424,10 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<NCG>& s, const QueryT
 #pragma unroll
   for (int cg = 0; cg < NCG; ++cg) {
     // Base-2 logits l = raw * fac (* per-token key scale).  The column
-    // factor is positive unless the softmax or key scale is not: then the
-    // maximum is taken on the products without it, which orders them the
-    // same way, and the factor goes into the exponent's FMA.
-    const float fac = q.fac[cg];
-    const bool prescale = __ballot(!(fac > 0.0f)) != 0;  // wave-uniform
-    const float post = prescale ? 1.0f : fac;
+    // factor is positive (prepare_query), so the maximum is taken on the
+    // raw products, which orders them the same way, and the factor goes
+    // into the exponent's FMA.
+    const float post = q.fac[cg];
     float lg[NCH][8];
     float cmax = kNegInf;
 #pragma unroll
@@ -438,10 +442,6 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<NCG>& s, const QueryT
         scales(ch, 0, ksc);
 #pragma unroll
         for (int j = 0; j < 8; ++j) lg[ch][j] *= ksc[j];
-      }
-      if (prescale) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) lg[ch][j] *= fac;
       }
       const bool interior = tb[ch] >= q.lo_max && tb[ch] + kChunk <= q.hi_min;
       if (__builtin_expect(!interior, 0)) {
@@ -500,6 +500,324 @@ __device__ __forceinline__ void chunk_softmax_pv(WaveState<NCG>& s, const QueryT
     }
     s.lsum[cg] = s.lsum[cg] * alpha + psum * vmul;
   }
+}
+
+// Softmax and value product of a unit of NCH = 4 (128 tokens) or 2 chunks
+// (raw logits la/lb, stages sk, per-token K scales at ssc and V scales 32
+// floats later, first tokens tb) of one 16-column block, as one
+// online-softmax step.
+//
+// The value product runs on v_mfma_f32_16x16x128_f8f6f4 with the unit's
+// tokens along K: for k-bytes 8 ch .. 8 ch + 7, lane (grp, c16) supplies
+// tokens 8 grp .. 8 grp + 7 of chunk ch -- the probabilities its QK results
+// hold (B operand, column c16) and the values of head dim 16 j + c16 of the
+// same tokens (A operand, one 8-byte LDS read per chunk); a 2-chunk unit
+// leaves k-bytes 16 .. 31 zero.  So one MFMA per 16 head dims and fp8 term
+// covers the unit: 16 per four chunks instead of 64 of the K = 32 form.
+//
+// The reference maximum moves lazily: only when the unit's column maximum
+// passes it by more than kLazyMax (base 2); the value-scale reference only
+// when the unit's largest value scale is more than twice it.  Probabilities
+// are 2^(kPBias + l - m) * (value scale / reference) <= 2^(4 + 3) * 2 = 256,
+// inside e4m3fn, and the accumulator rescale is skipped unless a reference
+// moved -- for smooth logits, after a piece's first unit almost never.
+constexpr float kPBias = 4.0f;
+constexpr float kLazyMax = 3.0f;
+
+template <bool PER_TOKEN, int NCH>
+__device__ __forceinline__ void unit_softmax_pv(WaveState<1>& s, const QueryTile<1>& q, const f32x4 (&la)[NCH][1],
+                                                const f32x4 (&lb)[NCH][1],
+                                                const LDS_AS unsigned char* const (&sk)[NCH],
+                                                const LDS_AS float* const (&ssc)[NCH], int grp, int c16,
+                                                const int (&tb)[NCH]) {
+  static_assert(NCH == 2 || NCH == 4, "units of two or four chunks");
+  bool edge[NCH];
+  int jlo[NCH], jhi[NCH];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    edge[ch] = tb[ch] < q.lo_all || tb[ch] + kChunk > q.hi_all;
+    const int tok0 = tb[ch] + 8 * grp;
+    jlo[ch] = pa_min(pa_max(q.lo_all - tok0, 0), 8);
+    jhi[ch] = pa_min(pa_max(q.hi_all - tok0, jlo[ch]), 8);
+  }
+  auto scales = [&](int ch, int off, float (&x)[8]) {
+    const LDS_AS float* ss = ssc[ch] + off + 8 * grp;
+    const f32x4 x0 = *(const LDS_AS f32x4*)ss;
+    const f32x4 x1 = *(const LDS_AS f32x4*)(ss + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x[j] = x0[j];
+      x[4 + j] = x1[j];
+    }
+  };
+
+  float vsc[NCH][8];
+  float vratio = 1.0f, vmul = 1.0f, vlog = 0.0f;
+  if (PER_TOKEN) {
+    float cmax = 0.0f;
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+      scales(ch, 32, vsc[ch]);
+      if (__builtin_expect(edge[ch], 0)) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) vsc[ch][j] = (j >= jlo[ch] && j < jhi[ch]) ? vsc[ch][j] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) cmax = fmaxf(cmax, vsc[ch][j]);
+    }
+    cmax = max_over_groups(cmax);
+    const float vnew = cmax > 2.0f * s.vsmax ? cmax : s.vsmax;
+    vratio = vnew > s.vsmax && s.vsmax > 0.0f ? s.vsmax * __builtin_amdgcn_rcpf(vnew) : 1.0f;
+    vmul = vnew > 0.0f ? vnew : 1.0f;
+    vlog = __builtin_amdgcn_logf(vmul);
+    s.vsmax = vnew;
+  }
+
+  const float post = q.fac[0];  // > 0 (prepare_query)
+  float lg[NCH][8];
+  float cmax = kNegInf;
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lg[ch][i] = la[ch][0][i];
+      lg[ch][4 + i] = lb[ch][0][i];
+    }
+    if (PER_TOKEN) {
+      float ksc[8];
+      scales(ch, 0, ksc);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) lg[ch][j] *= ksc[j];
+    }
+    const bool interior = tb[ch] >= q.lo_max && tb[ch] + kChunk <= q.hi_min;
+    if (__builtin_expect(!interior, 0)) {
+      const int tok0 = tb[ch] + 8 * grp;
+      const int jl = q.vis_lo[0] - tok0, jh = q.vis_hi[0] - tok0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) lg[ch][j] = (j >= jl && j < jh) ? lg[ch][j] : kNegInf;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) cmax = fmaxf(cmax, lg[ch][j]);
+  }
+  cmax = max_over_groups(cmax) * post;
+  const bool move = cmax > s.m2[0] + kLazyMax;  // also: the first visible key of the piece
+  const float mnew = move ? cmax : s.m2[0];
+  const float muse = mnew == kNegInf ? 0.0f : mnew;
+  const float alpha = move ? __builtin_amdgcn_exp2f(s.m2[0] - muse) : 1.0f;
+  s.m2[0] = mnew;
+  const float f = alpha * vratio;
+  if (__ballot(f != 1.0f)) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s.acc[0][j] *= f;
+  }
+  const float bias = kPBias - muse - vlog;
+  float psum = 0.0f;
+  i32x8 PH = {0, 0, 0, 0, 0, 0, 0, 0}, PL = PH;
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    float pr[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(lg[ch][j], post, bias));
+      psum += ev;
+      pr[j] = PER_TOKEN ? ev * vsc[ch][j] : ev;
+    }
+    long phi, plo;
+    split8_fp8(pr, phi, plo);
+    PH[2 * ch] = (int)(uint32_t)phi;
+    PH[2 * ch + 1] = (int)(uint32_t)((uint64_t)phi >> 32);
+    PL[2 * ch] = (int)(uint32_t)plo;
+    PL[2 * ch + 1] = (int)(uint32_t)((uint64_t)plo >> 32);
+  }
+  // value operands: head dim 16 j + c16, tokens 8 grp .. 8 grp + 7 of each
+  // chunk; a unit with an edge chunk zeroes the bytes of tokens no column
+  // sees (one wave-uniform test per unit, the masked loop a copy)
+  auto pv = [&](auto masked) {
+    uint64_t keep[NCH];
+    if (masked) {
+#pragma unroll
+      for (int ch = 0; ch < NCH; ++ch) {
+        const uint64_t below_hi = jhi[ch] >= 8 ? ~0ull : (1ull << (8 * jhi[ch])) - 1;
+        const uint64_t below_lo = jlo[ch] >= 8 ? ~0ull : (1ull << (8 * jlo[ch])) - 1;
+        keep[ch] = below_hi & ~below_lo;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      i32x8 V = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int ch = 0; ch < NCH; ++ch) {
+        const LDS_AS unsigned char* sv = sk[ch] + kKBytes;
+        uint64_t v = *(const LDS_AS uint64_t*)(sv + (grp >> 1) * 2048 + (16 * j + c16) * 16 + 8 * (grp & 1));
+        if (masked) v &= keep[ch];
+        V[2 * ch] = (int)(uint32_t)v;
+        V[2 * ch + 1] = (int)(uint32_t)(v >> 32);
+      }
+      s.acc[0][j] = mfma_fp8_k128(V, PH, s.acc[0][j]);
+      s.acc[0][j] = mfma_fp8_k128(V, PL, s.acc[0][j]);
+    }
+  };
+  bool any_edge = false;
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) any_edge |= edge[ch];
+  if (__builtin_expect(any_edge, 0))
+    pv(std::true_type{});
+  else
+    pv(std::false_type{});
+  s.lsum[0] = s.lsum[0] * alpha + psum * vmul;
+}
+
+// QK, softmax and value product of a 128-token unit of four chunks for one
+// 16-column block (the cooperative kernel's four-chunk units), as one
+// online-softmax step, with lane group g holding chunk g:
+//   * QK tile t (t = 0 .. 7) takes key rows 4 c + i = token 4 t + i of
+//     chunk c, so the result rows 4 g .. 4 g + 3 of lane group g are tokens
+//     4 t .. 4 t + 3 of chunk g: after the eight tiles a lane holds its
+//     column's logits for all 32 tokens of chunk g, in order;
+//   * the value product (v_mfma_f32_16x16x128_f8f6f4, tokens along K) then
+//     takes k-bytes 0 .. 31 of lane (g, c) = tokens 0 .. 31 of chunk g: the
+//     probabilities the lane holds (B operand) and, for head dim 16 j + c,
+//     the two 16-byte rows [half][dim][16 tokens] of the chunk's value image
+//     (A operand: two ds_read_b128 straight into the operand registers).
+// sk[c] is chunk c's slot (a missing chunk, c >= nch, points at chunk 0's
+// and is masked); tb0 the unit's first token.  References move lazily, as
+// unit_softmax_pv describes.
+template <bool PER_TOKEN>
+__device__ __forceinline__ void unit4_softmax_pv(WaveState<1>& s, const QueryTile<1>& q,
+                                                 const LDS_AS unsigned char* const (&sk)[4], int nch, int tb0,
+                                                 int grp, int c16) {
+  // per-lane bases: the key row's chunk (c16 / 4) and the lane's own chunk
+  // (grp)
+  const LDS_AS unsigned char* kb = sk[c16 >> 2] + (c16 & 3) * 16 + grp * 256;
+  const LDS_AS unsigned char* vb = sk[grp] + kKBytes + c16 * 16;
+  const LDS_AS float* sb = (const LDS_AS float*)(sk[grp] + kKBytes + kVBytes);
+  f32x4 lg4[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int off = (t >> 2) * kKHalf + (t & 3) * 64;
+    const i32x4 k0 = *(const LDS_AS i32x4*)(kb + off);
+    const i32x4 k1 = *(const LDS_AS i32x4*)(kb + off + 1024);
+    const i32x8 KA = {k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
+    const f32x4 zz = {0.f, 0.f, 0.f, 0.f};
+    lg4[t] = mfma_fp8_k128(KA, q.hi[0], zz);
+    lg4[t] = mfma_fp8_k128(KA, q.lo[0], lg4[t]);
+  }
+  float lg[32];
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lg[4 * t + i] = lg4[t][i];
+
+  // Tokens of the lane's chunk: tok0 + k.  full: every token of the unit
+  // is visible to every column (wave-uniform).
+  const int tok0 = tb0 + 32 * grp;
+  const bool full = nch == 4 && tb0 >= q.lo_max && tb0 + 128 <= q.hi_min;
+  // keys some column sees: [klo, khi) of the lane's 32 (empty for a missing
+  // chunk); stale page tails outside it must not reach the value product
+  int klo = 0, khi = 32;
+  if (!full) {
+    klo = pa_min(pa_max(q.lo_all - tok0, 0), 32);
+    khi = grp < nch ? pa_min(pa_max(q.hi_all - tok0, klo), 32) : klo;
+  }
+
+  float vsc[32];
+  float vratio = 1.0f, vmul = 1.0f, vlog = 0.0f;
+  if (PER_TOKEN) {
+#pragma unroll
+    for (int k = 0; k < 32; k += 4) {
+      const f32x4 ks = *(const LDS_AS f32x4*)(sb + k);
+      const f32x4 vs = *(const LDS_AS f32x4*)(sb + 32 + k);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        lg[k + i] *= ks[i];
+        vsc[k + i] = vs[i];
+      }
+    }
+    if (!full) {
+#pragma unroll
+      for (int k = 0; k < 32; ++k) vsc[k] = (k >= klo && k < khi) ? vsc[k] : 0.0f;
+    }
+    float cmax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) cmax = fmaxf(cmax, vsc[k]);
+    cmax = max_over_groups(cmax);
+    const float vnew = cmax > 2.0f * s.vsmax ? cmax : s.vsmax;
+    vratio = vnew > s.vsmax && s.vsmax > 0.0f ? s.vsmax * __builtin_amdgcn_rcpf(vnew) : 1.0f;
+    vmul = vnew > 0.0f ? vnew : 1.0f;
+    vlog = __builtin_amdgcn_logf(vmul);
+    s.vsmax = vnew;
+  }
+  if (!full) {
+    // the column's own visible keys
+    const int jl = q.vis_lo[0] - tok0;
+    const int jh = grp < nch ? q.vis_hi[0] - tok0 : jl;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) lg[k] = (k >= jl && k < jh) ? lg[k] : kNegInf;
+  }
+  const float post = q.fac[0];  // > 0 (prepare_query)
+  float cmax = kNegInf;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) cmax = fmaxf(cmax, lg[k]);
+  cmax = max_over_groups(cmax) * post;
+  const bool move = cmax > s.m2[0] + kLazyMax;
+  const float mnew = move ? cmax : s.m2[0];
+  const float muse = mnew == kNegInf ? 0.0f : mnew;
+  const float alpha = move ? __builtin_amdgcn_exp2f(s.m2[0] - muse) : 1.0f;
+  s.m2[0] = mnew;
+  const float f = alpha * vratio;
+  if (__ballot(f != 1.0f)) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s.acc[0][j] *= f;
+  }
+  const float bias = kPBias - muse - vlog;
+  float psum = 0.0f;
+  i32x8 PH, PL;
+#pragma unroll
+  for (int k8 = 0; k8 < 4; ++k8) {
+    float pr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(lg[8 * k8 + i], post, bias));
+      psum += ev;
+      pr[i] = PER_TOKEN ? ev * vsc[8 * k8 + i] : ev;
+    }
+    long phi, plo;
+    split8_fp8(pr, phi, plo);
+    PH[2 * k8] = (int)(uint32_t)phi;
+    PH[2 * k8 + 1] = (int)(uint32_t)((uint64_t)phi >> 32);
+    PL[2 * k8] = (int)(uint32_t)plo;
+    PL[2 * k8 + 1] = (int)(uint32_t)((uint64_t)plo >> 32);
+  }
+  // keep-masks of the lane's value bytes (k in [klo, khi)), per dword
+  uint32_t keep[8];
+  if (!full) {
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      const int lo = pa_min(pa_max(klo - 4 * w, 0), 4), hi = pa_min(pa_max(khi - 4 * w, lo), 4);
+      const uint32_t below_hi = hi >= 4 ? ~0u : (1u << (8 * hi)) - 1;
+      const uint32_t below_lo = lo >= 4 ? ~0u : (1u << (8 * lo)) - 1;
+      keep[w] = below_hi & ~below_lo;
+    }
+  }
+  auto pv = [&](auto masked) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const i32x4 v0 = *(const LDS_AS i32x4*)(vb + j * 256);
+      const i32x4 v1 = *(const LDS_AS i32x4*)(vb + j * 256 + 2048);
+      i32x8 V = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+      if (masked) {
+#pragma unroll
+        for (int w = 0; w < 8; ++w) V[w] &= (int)keep[w];
+      }
+      s.acc[0][j] = mfma_fp8_k128(V, PH, s.acc[0][j]);
+      s.acc[0][j] = mfma_fp8_k128(V, PL, s.acc[0][j]);
+    }
+  };
+  if (__builtin_expect(full, 1))
+    pv(std::false_type{});
+  else
+    pv(std::true_type{});
+  s.lsum[0] = s.lsum[0] * alpha + psum * vmul;
 }
 
 // One 32-token chunk of keys and values, staged in LDS at sk (keys: two
@@ -1195,13 +1513,13 @@ __device__ __forceinline__ void dma_chunk(const pa_fp8_stream_args& a, const flo
 // head dims 16 j + 4 grp .. + 3 in acc[j]): the output rows when the piece
 // is a whole (sequence, kv head), else a float32 partial row and its
 // natural-log lse (work list: rows target + qi; balanced split: partial id
-// target).  m is the column's base-2 maximum, L its sum of 256 * 2^(l - m),
+// target).  m is the column's base-2 maximum, L its sum of 2^(pbias + l - m),
 // and acc * vfin / L the normalised output.
 template <bool WORKLIST>
 __device__ __forceinline__ void store_piece(const pa_fp8_stream_args& a, void* __restrict__ output,
                                             float* __restrict__ part_out, float* __restrict__ part_lse,
                                             const Piece& p, const f32x4 (&acc)[8], float L, float m, float vfin,
-                                            int e, int grp) {
+                                            int e, int grp, float pbias = 8.0f) {
   const int gqa = a.query_group_size;
   const int eq = a.query_length * gqa;
   if (e >= eq) return;
@@ -1224,7 +1542,7 @@ __device__ __forceinline__ void store_piece(const pa_fp8_stream_args& a, void* _
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) *(f32x4*)(part_out + po + 16 * j + 4 * grp) = acc[j] * sc;
-    if (grp == 0) part_lse[pl] = L > 0.0f ? kLn2 * (m + __builtin_amdgcn_logf(L) - 8.0f) : kNegInf;
+    if (grp == 0) part_lse[pl] = L > 0.0f ? kLn2 * (m + __builtin_amdgcn_logf(L) - pbias) : kNegInf;
   }
 }
 
@@ -1786,23 +2104,32 @@ __global__ __launch_bounds__(64 * kBinWaves) void pa_fp8_bin_kernel(
 // Cooperative column-split decode for 17..64 query columns per kv head
 // (two to four 16-column blocks).  A workgroup has one wave per column
 // block; all of its waves read the same 32-token chunks from one shared
-// LDS ring of kCoopStages stages, each wave DMAing an equal share of every
-// chunk, with one barrier per chunk.  A wave therefore holds only its own
-// block's accumulators and query operands (no register spills, several
-// waves per SIMD), and the chunk is fetched from HBM once for all blocks.
-// Work comes from the same walks as pa_fp8_stream_kernel, at workgroup
-// granularity (one run or one bin per workgroup); every wave writes its own
-// columns of each piece (no merge inside the workgroup).  A piece's query
-// rows are loaded into registers during the previous piece's last chunk.
-// A cooperative workgroup moves through its chunks in units of two: one
-// ring stage, one wait and one barrier per unit, and one softmax step for
-// both chunks.  Three unit stages per workgroup (3 x 50 KiB of LDS per CU).
-constexpr int kCoopStages = 3;
-constexpr int kUnit = 2;  // chunks per unit
+// LDS ring of chunk slots, each wave DMAing an equal share of every chunk
+// (its last wave also the chunk's per-token scales).  A wave holds only its
+// own block's accumulators and query operands, and a chunk is fetched from
+// HBM once for all blocks.  Work comes from the same walks as
+// pa_fp8_stream_kernel, at workgroup granularity (a run of the balanced
+// split, or one bin of the work list); every wave writes its own columns of
+// each piece.  A piece's query rows are loaded into registers during the
+// previous piece's last unit.
+//
+// The workgroup computes its chunks in units: one wait, one barrier and
+// one online-softmax step per unit, and a value product on the K = 128 MFMA
+// (unit_softmax_pv).  The ring has S chunk slots; while a unit is computed
+// the next S - U chunks are in flight, and after its barrier the ring is
+// refilled up to S chunks past its start, which covers the next unit when
+// S >= 2 U: four waves of the balanced split run units of four chunks over
+// nine slots (77 KiB), two workgroups per CU; otherwise units of two over
+// six slots, three workgroups per CU (the work list then keeps the
+// reference's CU * 3 bins resident).
 constexpr int kFarToken = 1 << 30;  // first token of a unit's missing chunk
 
+constexpr int coop_slots(int nw, bool worklist) { return nw == 4 && !worklist ? 9 : 6; }
+constexpr int coop_unit(int nw, bool worklist) { return nw == 4 && !worklist ? 4 : 2; }
+constexpr int coop_wgs_per_cu(int nw, bool worklist) { return nw == 4 && !worklist ? 2 : 3; }
+
 template <int NW, bool PER_TOKEN, bool BS16, bool WORKLIST>
-__global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
+__global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8_coop_kernel(
     const pa_fp8_stream_args a, const int32_t* __restrict__ block_tables, const int32_t* __restrict__ kv_indptr,
     const int32_t* __restrict__ context_lengths, const float* __restrict__ key_scale,
     const float* __restrict__ value_scale, const int32_t* __restrict__ work_indptr,
@@ -1810,14 +2137,13 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
     int32_t* __restrict__ segdesc, float* __restrict__ part_out, float* __restrict__ part_lse,
     void* __restrict__ output) {
   static_assert(NW == 2 || NW == 4, "two or four waves share a chunk");
-  constexpr int S = kCoopStages;
-  // Unit stage: [chunk 0 keys, values][chunk 1 keys, values][per-token
-  // scales: chunk 0 K, V, chunk 1 K, V (128 B each)].
-  constexpr int kStageBytes = kKBytes + kVBytes;  // one chunk
-  constexpr int kUnitBytes = kUnit * kStageBytes + (PER_TOKEN ? kUnit * kScaleBytes : 0);
+  constexpr int S = coop_slots(NW, WORKLIST);
+  constexpr int U = coop_unit(NW, WORKLIST);  // chunks per unit
+  static_assert(S >= 2 * U, "the refill after a unit's barrier covers the next unit");
+  // Chunk slot: keys, values, per-token K then V scales.
+  constexpr int kSlotBytes = kKBytes + kVBytes + (PER_TOKEN ? kScaleBytes : 0);
   constexpr int kDmaPerWave = 8 / NW;  // of a chunk's 8 one-KiB key/value loads
-  constexpr int kLoads = kUnit * kDmaPerWave + (PER_TOKEN ? 1 : 0);  // per unit
-  __shared__ __attribute__((aligned(16))) unsigned char smem[S * kUnitBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char smem[S * kSlotBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1832,6 +2158,9 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
   const int bs_shift = BS16 ? 4 : __builtin_ctz((unsigned)bs);
   const int nblocks = a.num_blocks;
   const int e = wave * 16 + c16;  // this lane's query column
+  // The last wave also loads every chunk's per-token scales; loads per chunk:
+  const bool scale_wave = PER_TOKEN && wave == NW - 1;
+  const int lpc = kDmaPerWave + (scale_wave ? 1 : 0);
 
   using Walk = typename std::conditional<WORKLIST, WorklistWalk, BalancedWalk>::type;
   Walk walk;
@@ -1857,10 +2186,10 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
 
   // ---------------- piece window ----------------
   // The walk is seen through two pieces: `cur` is being computed, `nxt`
-  // follows.  The issue side runs up to S - 1 chunks ahead of the compute
-  // side but never past `nxt`: once it has issued all of `nxt` it pauses
-  // until the compute side moves on.  One walker serves both sides, which
-  // keeps the scalar state small enough to stay in SGPRs.
+  // follows.  The issue side runs ahead of the compute side but never past
+  // `nxt`: once it has issued all of `nxt` it pauses until the compute side
+  // moves on.  One walker serves both sides, which keeps the scalar state
+  // small enough to stay in SGPRs.
   Piece cur, nxt;
   bool has_cur = next_piece(cur);
   if (!has_cur) return;
@@ -1901,22 +2230,11 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
   }
   const uint8_t* ibase = rbase;  // rbase + ih * rstride_head
   bool iok = false;
-  // Page ids of the next unit (prefetched): its first chunk's (np0, and np1
-  // for the chunk's second 16-token page) and its second chunk's (np2, np3),
-  // which repeat the first's when the unit has one chunk.
-  int np0 = 0, np1 = 0, np2 = 0, np3 = 0;
+  int np0 = 0, np1 = 0;  // page ids of the next chunk (prefetched)
   auto fetch_pages = [&]() {
     const int lp0 = itb >> bs_shift;
     np0 = ld_uniform(block_tables, ibt + pa_min(lp0, ilast));
-    if (BS16) {
-      np1 = ld_uniform(block_tables, ibt + pa_min(lp0 + 1, ilast));
-      np2 = irem >= 2 ? ld_uniform(block_tables, ibt + pa_min(lp0 + 2, ilast)) : np0;
-      np3 = irem >= 2 ? ld_uniform(block_tables, ibt + pa_min(lp0 + 3, ilast)) : np1;
-    } else {
-      np1 = np0;
-      np2 = irem >= 2 ? ld_uniform(block_tables, ibt + pa_min((itb + kChunk) >> bs_shift, ilast)) : np0;
-      np3 = np2;
-    }
+    np1 = BS16 ? ld_uniform(block_tables, ibt + pa_min(lp0 + 1, ilast)) : np0;
   };
   auto issue_enter = [&](const Piece& p, int which) {
     itb = p.tb0;
@@ -1934,48 +2252,32 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
   else if (has_nxt && nxt.n > 0)
     issue_enter(nxt, 1);
 
-  // This wave's share of the chunk at token tb of kv head ih (pages q0, q1),
-  // into chunk slot sl of unit stage st.
-  auto issue_chunk = [&](int st, int sl, int tb, int q0, int q1) {
-    const int p0 = clamp_page(q0);
-    const int p1 = BS16 ? clamp_page(q1) : p0;
-    const int64_t inpage = BS16 ? 0 : (int64_t)(((tb & (bs - 1)) >> sh1) << sh2);
-    LDS_AS unsigned char* sk = (LDS_AS unsigned char*)smem + st * kUnitBytes + sl * kStageBytes;
+  // This wave's share of the next chunk (and, for the scale wave, the
+  // chunk's 32 K and 32 V scales: lane l < 16 carries 4 tokens' scales, keys
+  // or values by bit 3) into chunk slot `issued % S` (islot).
+  int issued = 0;    // chunks this workgroup has issued
+  int islot = 0;     // their next slot: issued % S
+  auto issue_next = [&]() {
+    const int p0 = clamp_page(np0);
+    const int p1 = BS16 ? clamp_page(np1) : p0;
+    const int64_t inpage = BS16 ? 0 : (int64_t)(((itb & (bs - 1)) >> sh1) << sh2);
+    LDS_AS unsigned char* sk = (LDS_AS unsigned char*)smem + islot * kSlotBytes;
+    islot = islot + 1 == S ? 0 : islot + 1;
 #pragma unroll
     for (int j = 0; j < kDmaPerWave; ++j) {
       const int pg = (BS16 && hsel[j]) ? p1 : p0;
       lds_dma16(ibase + (int64_t)pg * rstride_block + inpage + loff[j], sk + ldsoff[j]);
     }
-  };
-  // Per-token scales of a unit's two chunks (at tokens tb0, tb1; pages as
-  // issue_chunk) in one load of 32 lanes: lane l carries 4 tokens' scales,
-  // chunk l / 16, keys or values by bit 3.  Every wave loads them, so each
-  // wave's own wait covers them.
-  auto issue_scales = [&](int st, int tb0, int tb1) {
-    LDS_AS unsigned char* ss = (LDS_AS unsigned char*)smem + st * kUnitBytes + kUnit * kStageBytes;
-    if (lane < 32) {
-      const int c = lane >> 4;
+    if (scale_wave && lane < 16) {
       const int tt = (lane & 7) * 4;
-      const int tb = c ? tb1 : tb0;
-      const int q0 = c ? np2 : np0, q1 = c ? np3 : np1;
-      const int pg = clamp_page(BS16 ? (tt >= 16 ? q1 : q0) : q0);
-      const int sidx = BS16 ? (tt & 15) : (tb & (bs - 1)) + tt;
+      const int pg = BS16 ? (tt >= 16 ? p1 : p0) : p0;
+      const int sidx = BS16 ? (tt & 15) : (itb & (bs - 1)) + tt;
       const float* base = ((lane & 8) ? value_scale : key_scale) + (int64_t)ih * a.stride_ks_head;
-      lds_dma16(base + (int64_t)pg * a.stride_ks_block + sidx, ss);
+      lds_dma16(base + (int64_t)pg * a.stride_ks_block + sidx, sk + kKBytes + kVBytes);
     }
-  };
-  // The next unit: the next two chunks of the issue piece, or its last one
-  // loaded twice (the copy keeps the load count per unit fixed; the compute
-  // side masks it).
-  auto issue_unit = [&](int st) {
-    const bool two = irem >= 2;
-    const int tb1 = two ? itb + kChunk : itb;
-    issue_chunk(st, 0, itb, np0, np1);
-    issue_chunk(st, 1, tb1, np2, np3);
-    if (PER_TOKEN) issue_scales(st, itb, tb1);
-    itb += two ? 2 * kChunk : kChunk;
-    irem -= two ? 2 : 1;
-    if (irem > 0)
+    ++issued;
+    itb += kChunk;
+    if (--irem > 0)
       fetch_pages();
     else if (iw == 0 && has_nxt && nxt.n > 0)
       issue_enter(nxt, 1);
@@ -2012,36 +2314,43 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
   // Query rows are loaded during the previous piece's last unit when the
   // next piece is known by then (qready), else at the piece's first unit.
   bool qready = false;
-  int issued = 0;  // units this workgroup has issued
-  int gu = 0;      // units computed
-#pragma unroll
-  for (int k = 0; k < S - 1; ++k)
-    if (iok) {
-      issue_unit(issued % S);
-      ++issued;
-    }
+  int gc = 0;     // chunks computed
+  int cslot = 0;  // gc % S
+  while (iok && issued < S) issue_next();
 
   while (has_cur) {
-    const int units = (cur.n + kUnit - 1) / kUnit;
+    const int units = (cur.n + U - 1) / U;
     for (int u = 0; u < units; ++u) {
-      if (issued == gu) {
-        // The issue side paused past an empty piece: unit gu goes now (its
-        // stage last held unit gu - S, which every wave has left).
-        issue_unit(gu % S);
-        ++issued;
+      const int nch = pa_min(U, cur.n - U * u);
+      if (issued < gc + nch) {
+        // The issue side paused past an empty piece: this unit's chunks go
+        // now, once every wave is done with the previous unit (their slots
+        // held chunks S back).  Workgroup-uniform: every wave walks the same
+        // pieces.
+        asm volatile("s_barrier" ::: "memory");
+        while (issued < gc + nch) issue_next();
       }
-      // Wait for this wave's loads of unit gu: newer units (up to S - 2)
-      // may stay in flight.  Loads retire in order; query rows issued in
-      // between are only waited for early.
-      const int newer = issued - gu - 1;
-      if (newer >= 1)
-        __builtin_amdgcn_s_waitcnt(vmcnt_only(kLoads));
-      else
+      // This wave's loads of the unit: up to two newer chunks may stay in
+      // flight (loads retire in order; more newer chunks, or query rows
+      // issued in between, are only waited for early).
+      const int newer = issued - gc - nch;
+      if (newer >= 2) {
+        if (scale_wave)
+          __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * (kDmaPerWave + 1)));
+        else
+          __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * kDmaPerWave));
+      } else if (newer == 1) {
+        if (scale_wave)
+          __builtin_amdgcn_s_waitcnt(vmcnt_only(kDmaPerWave + 1));
+        else
+          __builtin_amdgcn_s_waitcnt(vmcnt_only(kDmaPerWave));
+      } else {
         __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-      // Every wave's share of unit gu is now in LDS and every wave is done
-      // with unit gu - 1.  A bare s_barrier: the DMA completion was awaited
-      // explicitly above (a fenced barrier would also wait for the units
-      // still in flight).
+      }
+      // Every wave's share of the unit is in LDS and every wave is done
+      // with the previous unit.  A bare s_barrier: the DMA completion was
+      // awaited explicitly above (a fenced barrier would also wait for the
+      // chunks still in flight).
       asm volatile("s_barrier" ::: "memory");
       if (u == 0) {
         if (!qready) load_query(cur);
@@ -2051,28 +2360,38 @@ __global__ __launch_bounds__(64 * NW, 3) void pa_fp8_coop_kernel(
         qready = has_nxt && nxt.n > 0;
         if (qready) load_query(nxt);
       }
-      // Stages of units up to gu + S - 1 are free (their previous units are
-      // at most gu - 1).
-      while (iok && issued < gu + S) {
-        issue_unit(issued % S);
-        ++issued;
-      }
-      const LDS_AS unsigned char* sb = (const LDS_AS unsigned char*)smem + (gu % S) * kUnitBytes;
-      const LDS_AS unsigned char* const sks[kUnit] = {sb, sb + kStageBytes};
-      const LDS_AS float* const sss[kUnit] = {(const LDS_AS float*)(sb + kUnit * kStageBytes),
-                                              (const LDS_AS float*)(sb + kUnit * kStageBytes + kScaleBytes)};
-      const int tb0 = cur.tb0 + u * (kUnit * kChunk);
-      const int tbs[kUnit] = {tb0, kUnit * u + 1 < cur.n ? tb0 + kChunk : kFarToken};
-      f32x4 la[kUnit][1], lb[kUnit][1];
+      // Slots of chunks before gc are free: every wave has passed this
+      // unit's barrier, so it is done with them.
+      while (iok && issued < gc + S) issue_next();
+      const LDS_AS unsigned char* sks[U];
+      const LDS_AS float* sss[U];
+      int tbs[U];
+      const int tb0 = cur.tb0 + u * (U * kChunk);
 #pragma unroll
-      for (int ch = 0; ch < kUnit; ++ch) chunk_logits<1>(qt, sks[ch], krow, grp, la[ch], lb[ch]);
-      chunk_softmax_pv<1, PER_TOKEN, kUnit>(st, qt, la, lb, sks, sss, grp, c16, tbs);
-      ++gu;
+      for (int ch = 0; ch < U; ++ch) {
+        // a missing chunk reads the unit's first slot and is masked
+        int sl = cslot + (ch < nch ? ch : 0);
+        sl = sl >= S ? sl - S : sl;
+        sks[ch] = (const LDS_AS unsigned char*)smem + sl * kSlotBytes;
+        sss[ch] = (const LDS_AS float*)(sks[ch] + kKBytes + kVBytes);
+        tbs[ch] = ch < nch ? tb0 + ch * kChunk : kFarToken;
+      }
+      if constexpr (U == 4) {
+        unit4_softmax_pv<PER_TOKEN>(st, qt, sks, nch, tb0, grp, c16);
+      } else {
+        f32x4 la[U][1], lb[U][1];
+#pragma unroll
+        for (int ch = 0; ch < U; ++ch) chunk_logits<1>(qt, sks[ch], krow, grp, la[ch], lb[ch]);
+        unit_softmax_pv<PER_TOKEN, U>(st, qt, la, lb, sks, sss, grp, c16, tbs);
+      }
+      gc += nch;
+      cslot += nch;
+      cslot = cslot >= S ? cslot - S : cslot;
     }
     // ---- the piece is complete: this wave's columns ----
     const float vfin = PER_TOKEN ? st.vsmax : v_tensor_scale;
     store_piece<WORKLIST>(a, output, part_out, part_lse, cur, st.acc[0], sum_over_groups(st.lsum[0]), st.m2[0],
-                          vfin, e, grp);
+                          vfin, e, grp, kPBias);
     if (!WORKLIST && cur.desc_cnt > 0 && wave == 0 && lane == 0)
       *(i32x2*)(segdesc + 2 * ((int64_t)cur.b * a.num_kv_heads + cur.h)) = i32x2{cur.target, cur.desc_cnt};
     st.reset();
@@ -2418,9 +2737,9 @@ hipError_t dispatch_coop_nw(const pa_fp8_stream_args& a, unsigned grid, hipStrea
 // blocks run on four waves, the fourth computing only masked columns).
 int coop_waves(int eq) { return eq <= 32 ? 2 : 4; }
 
-// Resident cooperative workgroups per CU (LDS: kCoopStages unit stages of
-// up to 17 KiB per workgroup; registers: three waves per SIMD).
-int coop_per_cu(int) { return 3; }
+// Resident cooperative workgroups per CU of a balanced launch (LDS: nine
+// chunk slots of up to 8.4 KiB for four waves, six for two).
+int coop_per_cu(int nw) { return coop_wgs_per_cu(nw, false); }
 
 // Workgroups of a work-list launch: as many as fit on the GPU at once (one
 // per CU for eight waves, three for three), at most one per bin.

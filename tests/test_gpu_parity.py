@@ -504,3 +504,24 @@ def test_graph_capture_every_schedule(sched):
                 call()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"eager after replay {i}"
+
+
+@pytest.mark.parametrize("softmax_scale,neg_key_scale", [(-0.09, False), (0.0, False), (0.09, True), (-0.05, True)])
+@pytest.mark.parametrize("shape", ["gqa4", "mtp_gqa16_pt"])
+def test_negative_and_zero_logit_scales(softmax_scale, neg_key_scale, shape):
+    """The logit factor (softmax scale x per-tensor key scale) may be negative
+    or zero: the kernels fold its sign into the queries (and a zero factor
+    gives uniform attention over the visible keys).  Every schedule, the
+    balanced split and, for 64 columns, the cooperative kernel."""
+    spec = dict(gqa4=dict(batch=5, ctx=[1, 40, 300, 2100, 5000]),
+                mtp_gqa16_pt=dict(batch=4, query_length=4, num_query_heads=64, num_kv_heads=4, block_size=64,
+                                  per_token=True, ctx=[4, 100, 1500, 4100]))[shape]
+    case = make_case(seed=301, **spec)
+    case["softmax_scale"] = softmax_scale
+    if neg_key_scale and case["key_scale"].dim() == 1:
+        case["key_scale"] = -case["key_scale"]
+    ref = torch_oracle(case, float_out=False)
+    d = to_dev(case)
+    for sched in ("auto", "slot", "owner"):
+        out, route, _ = launch(d, sched=sched)
+        assert_parity(out, ref, f"scale={softmax_scale} negk={neg_key_scale} {shape} {sched} {route}")
