@@ -102,9 +102,10 @@ def test_stream_worker_counts():
     assert _lib.stream_workers(256, 1, 4, True) == 2048
     assert _lib.stream_workers(256, 1, 8, False) == 1024
     assert _lib.stream_workers(256, 4, 4, True) == 1024
-    # 17..64 columns: cooperative workgroups (3 per CU, by the LDS of their ring)
+    # 17..64 columns: cooperative workgroups, by the LDS of their ring: two
+    # waves (17..32 columns) 3 per CU, four waves (nine chunk slots) 2 per CU
     assert _lib.stream_workers(256, 4, 8, True) == 768
-    assert _lib.stream_workers(256, 4, 16, True) == 768
+    assert _lib.stream_workers(256, 4, 16, True) == 512
     with pytest.raises(RuntimeError):
         _lib.stream_workers(256, 4, 32, True)  # 128 columns: not supported
     ws = _lib.balanced_workspace_bytes(128, 8, 1, 4, 2048)
