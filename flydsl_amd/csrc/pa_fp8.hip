@@ -106,18 +106,55 @@ __device__ __forceinline__ uint32_t pack4_fp8(float a, float b, float c, float d
   return (uint32_t)r;
 }
 
+// pack4_fp8 without the zeroing move: the first conversion writes the low
+// half of a fresh register whose old high half the second one overwrites.
+// The statement is outside the compiler's hazard tracking, so a and b must
+// not come straight from a transcendental instruction (which needs a wait
+// state before another VALU reads its result).
+__device__ __forceinline__ uint32_t pack4_fp8_fresh(float a, float b, float c, float d) {
+  int r;
+  asm("v_cvt_pk_fp8_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  r = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, r, true);
+  return (uint32_t)r;
+}
+
 // x[0..7] -> (hi, lo) with x ~= hi + lo, both packed e4m3fn, byte i = x[i].
+// kFresh: x was not written by a transcendental instruction directly (the
+// residuals never are), so the high part packs without zeroing moves too.
+template <bool kFresh = false>
 __device__ __forceinline__ void split8_fp8(const float* x, long& hi, long& lo) {
-  uint32_t h0 = pack4_fp8(x[0], x[1], x[2], x[3]);
-  uint32_t h1 = pack4_fp8(x[4], x[5], x[6], x[7]);
+  uint32_t h0, h1;
+  if constexpr (kFresh) {
+    h0 = pack4_fp8_fresh(x[0], x[1], x[2], x[3]);
+    h1 = pack4_fp8_fresh(x[4], x[5], x[6], x[7]);
+  } else {
+    h0 = pack4_fp8(x[0], x[1], x[2], x[3]);
+    h1 = pack4_fp8(x[4], x[5], x[6], x[7]);
+  }
   f32x2 b0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h0, false);
   f32x2 b1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h0, true);
   f32x2 b2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h1, false);
   f32x2 b3 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h1, true);
-  uint32_t l0 = pack4_fp8(x[0] - b0[0], x[1] - b0[1], x[2] - b1[0], x[3] - b1[1]);
-  uint32_t l1 = pack4_fp8(x[4] - b2[0], x[5] - b2[1], x[6] - b3[0], x[7] - b3[1]);
+  uint32_t l0 = pack4_fp8_fresh(x[0] - b0[0], x[1] - b0[1], x[2] - b1[0], x[3] - b1[1]);
+  uint32_t l1 = pack4_fp8_fresh(x[4] - b2[0], x[5] - b2[1], x[6] - b3[0], x[7] - b3[1]);
   hi = (long)((uint64_t)h0 | ((uint64_t)h1 << 32));
   lo = (long)((uint64_t)l0 | ((uint64_t)l1 << 32));
+}
+
+// Wait states between an MFMA that an inline statement issued (the
+// compiler's hazard tracking does not see it) and the next VALU access of
+// its result: 20, more than the longest MFMA used here needs.
+#define PA_MFMA_DRAIN "s_nop 7\n\ts_nop 7\n\ts_nop 3\n\t"
+
+// acc *= f in place (tied operands): a conditional rescale then keeps the
+// accumulators in their registers on both paths (no copies on the path
+// that skips it).  Its input may come from mfma_k128_pair.
+__device__ __forceinline__ void scale_inplace(f32x4 (&acc)[8], float f) {
+  asm volatile(PA_MFMA_DRAIN ::: "memory");
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) asm volatile("v_mul_f32 %0, %0, %1" : "+v"(acc[j][i]) : "v"(f));
 }
 
 __device__ __forceinline__ f32x4 mfma_fp8(long a, long b, f32x4 c) {
@@ -125,6 +162,31 @@ __device__ __forceinline__ f32x4 mfma_fp8(long a, long b, f32x4 c) {
 }
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+// acc += A B0, then acc += A B1 (v_mfma_f32_16x16x128_f8f6f4, fp8 e4m3fn
+// operands), the accumulator tied in place (the accumulate chain needs no
+// moves).  The compiler does not see inside the statement, so the hazards
+// it would cover are covered here: s_nop 1 gives the two wait states a
+// VALU write of an operand needs before an MFMA reads it; the second
+// product reads the first's result as srcC with the same registers and
+// opcode (no wait).  Any other access of acc first waits out the MFMA
+// (mfma_drain, scale_inplace).
+__device__ __forceinline__ void mfma_k128_pair(f32x4& acc, const i32x8& a, const i32x8& b0, const i32x8& b1) {
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0\n\t"
+      "v_mfma_f32_16x16x128_f8f6f4 %0, %1, %3, %0"
+      : "+v"(acc)
+      : "v"(a), "v"(b0), "v"(b1));
+}
+
+// Waits out mfma_k128_pair before acc is read or written by anything else;
+// the tied operands keep every later access of acc after it.
+__device__ __forceinline__ void mfma_drain(f32x4 (&acc)[8]) {
+  asm volatile(PA_MFMA_DRAIN
+               : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(acc[4]), "+v"(acc[5]), "+v"(acc[6]),
+                 "+v"(acc[7]));
+}
 
 // v_mfma_f32_16x16x128_f8f6f4 with both operands e4m3fn and unit scales:
 // lane l holds 32 k-values of row (A) / column (B) l % 16.
@@ -606,10 +668,7 @@ __device__ __forceinline__ void unit_softmax_pv(WaveState<1>& s, const QueryTile
   const float alpha = move ? __builtin_amdgcn_exp2f(s.m2[0] - muse) : 1.0f;
   s.m2[0] = mnew;
   const float f = alpha * vratio;
-  if (__ballot(f != 1.0f)) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) s.acc[0][j] *= f;
-  }
+  if (__ballot(f != 1.0f)) scale_inplace(s.acc[0], f);
   const float bias = kPBias - muse - vlog;
   float psum = 0.0f;
   i32x8 PH = {0, 0, 0, 0, 0, 0, 0, 0}, PL = PH;
@@ -630,40 +689,19 @@ __device__ __forceinline__ void unit_softmax_pv(WaveState<1>& s, const QueryTile
     PL[2 * ch + 1] = (int)(uint32_t)((uint64_t)plo >> 32);
   }
   // value operands: head dim 16 j + c16, tokens 8 grp .. 8 grp + 7 of each
-  // chunk; a unit with an edge chunk zeroes the bytes of tokens no column
-  // sees (one wave-uniform test per unit, the masked loop a copy)
-  auto pv = [&](auto masked) {
-    uint64_t keep[NCH];
-    if (masked) {
+  // chunk (stale bytes of edge chunks were zeroed in LDS)
 #pragma unroll
-      for (int ch = 0; ch < NCH; ++ch) {
-        const uint64_t below_hi = jhi[ch] >= 8 ? ~0ull : (1ull << (8 * jhi[ch])) - 1;
-        const uint64_t below_lo = jlo[ch] >= 8 ? ~0ull : (1ull << (8 * jlo[ch])) - 1;
-        keep[ch] = below_hi & ~below_lo;
-      }
+  for (int j = 0; j < 8; ++j) {
+    i32x8 V = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+      const LDS_AS unsigned char* sv = sk[ch] + kKBytes;
+      const uint64_t v = *(const LDS_AS uint64_t*)(sv + (grp >> 1) * 2048 + (16 * j + c16) * 16 + 8 * (grp & 1));
+      V[2 * ch] = (int)(uint32_t)v;
+      V[2 * ch + 1] = (int)(uint32_t)(v >> 32);
     }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      i32x8 V = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-      for (int ch = 0; ch < NCH; ++ch) {
-        const LDS_AS unsigned char* sv = sk[ch] + kKBytes;
-        uint64_t v = *(const LDS_AS uint64_t*)(sv + (grp >> 1) * 2048 + (16 * j + c16) * 16 + 8 * (grp & 1));
-        if (masked) v &= keep[ch];
-        V[2 * ch] = (int)(uint32_t)v;
-        V[2 * ch + 1] = (int)(uint32_t)(v >> 32);
-      }
-      s.acc[0][j] = mfma_fp8_k128(V, PH, s.acc[0][j]);
-      s.acc[0][j] = mfma_fp8_k128(V, PL, s.acc[0][j]);
-    }
-  };
-  bool any_edge = false;
-#pragma unroll
-  for (int ch = 0; ch < NCH; ++ch) any_edge |= edge[ch];
-  if (__builtin_expect(any_edge, 0))
-    pv(std::true_type{});
-  else
-    pv(std::false_type{});
+    mfma_k128_pair(s.acc[0][j], V, PH, PL);
+  }
   s.lsum[0] = s.lsum[0] * alpha + psum * vmul;
 }
 
@@ -682,25 +720,38 @@ __device__ __forceinline__ void unit_softmax_pv(WaveState<1>& s, const QueryTile
 // sk[c] is chunk c's slot (a missing chunk, c >= nch, points at chunk 0's
 // and is masked); tb0 the unit's first token.  References move lazily, as
 // unit_softmax_pv describes.
-template <bool PER_TOKEN>
+template <bool PER_TOKEN, int S, int kSlotBytes>
 __device__ __forceinline__ void unit4_softmax_pv(WaveState<1>& s, const QueryTile<1>& q,
-                                                 const LDS_AS unsigned char* const (&sk)[4], int nch, int tb0,
+                                                 const LDS_AS unsigned char* ring, int cslot, int nch, int tb0,
                                                  int grp, int c16) {
-  // per-lane bases: the key row's chunk (c16 / 4) and the lane's own chunk
-  // (grp)
-  const LDS_AS unsigned char* kb = sk[c16 >> 2] + (c16 & 3) * 16 + grp * 256;
-  const LDS_AS unsigned char* vb = sk[grp] + kKBytes + c16 * 16;
-  const LDS_AS float* sb = (const LDS_AS float*)(sk[grp] + kKBytes + kVBytes);
-  f32x4 lg4[8];
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
+  // Per-lane bases: the key row's chunk (c16 / 4) and the lane's own chunk
+  // (grp), chunk c sitting in ring slot (cslot + c) mod S (a missing chunk
+  // reads chunk 0's slot).
+  auto slot_of = [&](int c) {
+    int sl = cslot + (c < nch ? c : 0);
+    sl = sl >= S ? sl - S : sl;
+    return ring + sl * kSlotBytes;
+  };
+  const LDS_AS unsigned char* kb = slot_of(c16 >> 2) + (c16 & 3) * 16 + grp * 256;
+  const LDS_AS unsigned char* own = slot_of(grp);
+  const LDS_AS unsigned char* vb = own + kKBytes + c16 * 16;
+  const LDS_AS float* sb = (const LDS_AS float*)(own + kKBytes + kVBytes);
+  // key products, the next tile's operand read ahead of this tile's MFMAs
+  auto key_tile = [&](int t) {
     const int off = (t >> 2) * kKHalf + (t & 3) * 64;
     const i32x4 k0 = *(const LDS_AS i32x4*)(kb + off);
     const i32x4 k1 = *(const LDS_AS i32x4*)(kb + off + 1024);
-    const i32x8 KA = {k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
+    return i32x8{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
+  };
+  f32x4 lg4[8];
+  i32x8 KA[2];
+  KA[0] = key_tile(0);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    if (t + 1 < 8) KA[(t + 1) & 1] = key_tile(t + 1);
     const f32x4 zz = {0.f, 0.f, 0.f, 0.f};
-    lg4[t] = mfma_fp8_k128(KA, q.hi[0], zz);
-    lg4[t] = mfma_fp8_k128(KA, q.lo[0], lg4[t]);
+    lg4[t] = mfma_fp8_k128(KA[t & 1], q.hi[0], zz);
+    lg4[t] = mfma_fp8_k128(KA[t & 1], q.lo[0], lg4[t]);
   }
   float lg[32];
 #pragma unroll
@@ -713,7 +764,7 @@ __device__ __forceinline__ void unit4_softmax_pv(WaveState<1>& s, const QueryTil
   const int tok0 = tb0 + 32 * grp;
   const bool full = nch == 4 && tb0 >= q.lo_max && tb0 + 128 <= q.hi_min;
   // keys some column sees: [klo, khi) of the lane's 32 (empty for a missing
-  // chunk); stale page tails outside it must not reach the value product
+  // chunk); the value scales of the others, possibly stale, are zeroed
   int klo = 0, khi = 32;
   if (!full) {
     klo = pa_min(pa_max(q.lo_all - tok0, 0), 32);
@@ -765,10 +816,7 @@ __device__ __forceinline__ void unit4_softmax_pv(WaveState<1>& s, const QueryTil
   const float alpha = move ? __builtin_amdgcn_exp2f(s.m2[0] - muse) : 1.0f;
   s.m2[0] = mnew;
   const float f = alpha * vratio;
-  if (__ballot(f != 1.0f)) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) s.acc[0][j] *= f;
-  }
+  if (__ballot(f != 1.0f)) scale_inplace(s.acc[0], f);
   const float bias = kPBias - muse - vlog;
   float psum = 0.0f;
   i32x8 PH, PL;
@@ -782,41 +830,20 @@ __device__ __forceinline__ void unit4_softmax_pv(WaveState<1>& s, const QueryTil
       pr[i] = PER_TOKEN ? ev * vsc[8 * k8 + i] : ev;
     }
     long phi, plo;
-    split8_fp8(pr, phi, plo);
+    split8_fp8<PER_TOKEN>(pr, phi, plo);  // per-token: pr = ev * scale
     PH[2 * k8] = (int)(uint32_t)phi;
     PH[2 * k8 + 1] = (int)(uint32_t)((uint64_t)phi >> 32);
     PL[2 * k8] = (int)(uint32_t)plo;
     PL[2 * k8 + 1] = (int)(uint32_t)((uint64_t)plo >> 32);
   }
-  // keep-masks of the lane's value bytes (k in [klo, khi)), per dword
-  uint32_t keep[8];
-  if (!full) {
+  // value operands (stale bytes of edge chunks were zeroed in LDS)
 #pragma unroll
-    for (int w = 0; w < 8; ++w) {
-      const int lo = pa_min(pa_max(klo - 4 * w, 0), 4), hi = pa_min(pa_max(khi - 4 * w, lo), 4);
-      const uint32_t below_hi = hi >= 4 ? ~0u : (1u << (8 * hi)) - 1;
-      const uint32_t below_lo = lo >= 4 ? ~0u : (1u << (8 * lo)) - 1;
-      keep[w] = below_hi & ~below_lo;
-    }
+  for (int j = 0; j < 8; ++j) {
+    const i32x4 v0 = *(const LDS_AS i32x4*)(vb + j * 256);
+    const i32x4 v1 = *(const LDS_AS i32x4*)(vb + j * 256 + 2048);
+    const i32x8 V = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+    mfma_k128_pair(s.acc[0][j], V, PH, PL);
   }
-  auto pv = [&](auto masked) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const i32x4 v0 = *(const LDS_AS i32x4*)(vb + j * 256);
-      const i32x4 v1 = *(const LDS_AS i32x4*)(vb + j * 256 + 2048);
-      i32x8 V = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-      if (masked) {
-#pragma unroll
-        for (int w = 0; w < 8; ++w) V[w] &= (int)keep[w];
-      }
-      s.acc[0][j] = mfma_fp8_k128(V, PH, s.acc[0][j]);
-      s.acc[0][j] = mfma_fp8_k128(V, PL, s.acc[0][j]);
-    }
-  };
-  if (__builtin_expect(full, 1))
-    pv(std::false_type{});
-  else
-    pv(std::true_type{});
   s.lsum[0] = s.lsum[0] * alpha + psum * vmul;
 }
 
@@ -1506,6 +1533,28 @@ __device__ __forceinline__ void dma_chunk(const pa_fp8_stream_args& a, const flo
       const float* base = (lane < 8 ? key_scale : value_scale) + (int64_t)ih * a.stride_ks_head;
       lds_dma16(base + (int64_t)pg2 * a.stride_ks_block + sidx, ss);
     }
+  }
+}
+
+// Zeroes the value bytes of tokens outside [lo, hi) in one 16-token half
+// of a chunk's value image in LDS ([head dim][16 tokens], 128 rows of 16
+// bytes starting at token th): lane l rewrites rows l and l + 64.
+__device__ __forceinline__ void zero_stale_values(LDS_AS unsigned char* v, int th, int lo, int hi, int lane) {
+  const int klo = pa_min(pa_max(lo - th, 0), 16);
+  const int khi = pa_min(pa_max(hi - th, klo), 16);
+  if (klo == 0 && khi == 16) return;
+  i32x4 keep;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int l4 = pa_min(pa_max(klo - 4 * w, 0), 4), h4 = pa_min(pa_max(khi - 4 * w, l4), 4);
+    const uint32_t below_hi = h4 >= 4 ? ~0u : (1u << (8 * h4)) - 1;
+    const uint32_t below_lo = l4 >= 4 ? ~0u : (1u << (8 * l4)) - 1;
+    keep[w] = (int)(below_hi & ~below_lo);
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    LDS_AS i32x4* row = (LDS_AS i32x4*)(v + (r * 64 + lane) * 16);
+    *row = *row & keep;
   }
 }
 
@@ -2229,12 +2278,27 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
     ldsoff[j] = (wk ? hh * kKHalf : kKBytes + hh * 2048) + q2 * 1024;
   }
   const uint8_t* ibase = rbase;  // rbase + ih * rstride_head
+  // Page strides fit 31 bits (checked on the host), so a page's offset is
+  // one unsigned 32 x 32 -> 64-bit product.
+  const uint32_t rsb = (uint32_t)rstride_block;
+  const uint32_t ssb = (uint32_t)a.stride_ks_block;
+  // the scale wave's lane: its scale row base for the piece's kv head
+  const int tt = (lane & 7) * 4;
+  const float* const sbase0 = ((lane & 8) ? value_scale : key_scale) + (BS16 ? (tt & 15) : tt);
+  const float* sbase = sbase0;
   bool iok = false;
   int np0 = 0, np1 = 0;  // page ids of the next chunk (prefetched)
+  int nlp = -1;          // logical page of np0 (pages of 64 tokens and more hold several chunks)
   auto fetch_pages = [&]() {
-    const int lp0 = itb >> bs_shift;
-    np0 = ld_uniform(block_tables, ibt + pa_min(lp0, ilast));
-    np1 = BS16 ? ld_uniform(block_tables, ibt + pa_min(lp0 + 1, ilast)) : np0;
+    const int lp0 = pa_min(itb >> bs_shift, ilast);
+    if (BS16) {
+      np0 = ld_uniform(block_tables, ibt + lp0);
+      np1 = ld_uniform(block_tables, ibt + pa_min(lp0 + 1, ilast));
+    } else if (lp0 != nlp) {
+      np0 = ld_uniform(block_tables, ibt + lp0);
+      np1 = np0;
+      nlp = lp0;
+    }
   };
   auto issue_enter = [&](const Piece& p, int which) {
     itb = p.tb0;
@@ -2245,6 +2309,8 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
     iw = which;
     iok = true;
     ibase = rbase + (int64_t)ih * rstride_head;
+    if (PER_TOKEN) sbase = sbase0 + (int64_t)ih * a.stride_ks_head;
+    nlp = -1;
     fetch_pages();
   };
   if (cur.n > 0)
@@ -2263,17 +2329,14 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
     const int64_t inpage = BS16 ? 0 : (int64_t)(((itb & (bs - 1)) >> sh1) << sh2);
     LDS_AS unsigned char* sk = (LDS_AS unsigned char*)smem + islot * kSlotBytes;
     islot = islot + 1 == S ? 0 : islot + 1;
+    const uint8_t* pb0 = ibase + (uint64_t)(uint32_t)p0 * rsb + inpage;
+    const uint8_t* pb1 = BS16 ? ibase + (uint64_t)(uint32_t)p1 * rsb : pb0;
 #pragma unroll
-    for (int j = 0; j < kDmaPerWave; ++j) {
-      const int pg = (BS16 && hsel[j]) ? p1 : p0;
-      lds_dma16(ibase + (int64_t)pg * rstride_block + inpage + loff[j], sk + ldsoff[j]);
-    }
+    for (int j = 0; j < kDmaPerWave; ++j) lds_dma16(((BS16 && hsel[j]) ? pb1 : pb0) + loff[j], sk + ldsoff[j]);
     if (scale_wave && lane < 16) {
-      const int tt = (lane & 7) * 4;
       const int pg = BS16 ? (tt >= 16 ? p1 : p0) : p0;
-      const int sidx = BS16 ? (tt & 15) : (itb & (bs - 1)) + tt;
-      const float* base = ((lane & 8) ? value_scale : key_scale) + (int64_t)ih * a.stride_ks_head;
-      lds_dma16(base + (int64_t)pg * a.stride_ks_block + sidx, sk + kKBytes + kVBytes);
+      const int sidx = BS16 ? 0 : (itb & (bs - 1));
+      lds_dma16(sbase + (uint64_t)(uint32_t)pg * ssb + sidx, sk + kKBytes + kVBytes);
     }
     ++issued;
     itb += kChunk;
@@ -2347,6 +2410,28 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
       } else {
         __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
       }
+      // Value bytes of page slots outside the sequence's visible keys
+      // [lo_all, hi_all) -- a page's tail past the context, slots before a
+      // window -- may hold any byte, e4m3fn NaN included, which a zero
+      // probability does not cancel.  The wave that loaded a 16-token value
+      // half zeroes them (edge units only; workgroup-uniform test), so the
+      // value products need no masks.
+      if (!wk) {
+        const int ub = cur.tb0 + u * (U * kChunk);
+        if (ub < cur.lo_all || ub + nch * kChunk > cur.hi_all) {
+          for (int ch = 0; ch < nch; ++ch) {
+            int sl = cslot + ch;
+            sl = sl >= S ? sl - S : sl;
+#pragma unroll
+            for (int j = 0; j < kDmaPerWave; j += 2) {
+              const int hh = ((wave * kDmaPerWave + j) >> 1) & 1;  // this wave's loads j, j + 1
+              zero_stale_values((LDS_AS unsigned char*)smem + sl * kSlotBytes + kKBytes + hh * 2048,
+                                ub + ch * kChunk + 16 * hh, cur.lo_all, cur.hi_all, lane);
+            }
+          }
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+      }
       // Every wave's share of the unit is in LDS and every wave is done
       // with the previous unit.  A bare s_barrier: the DMA completion was
       // awaited explicitly above (a fenced barrier would also wait for the
@@ -2377,7 +2462,8 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
         tbs[ch] = ch < nch ? tb0 + ch * kChunk : kFarToken;
       }
       if constexpr (U == 4) {
-        unit4_softmax_pv<PER_TOKEN>(st, qt, sks, nch, tb0, grp, c16);
+        unit4_softmax_pv<PER_TOKEN, S, kSlotBytes>(st, qt, (const LDS_AS unsigned char*)smem, cslot, nch, tb0, grp,
+                                                   c16);
       } else {
         f32x4 la[U][1], lb[U][1];
 #pragma unroll
@@ -2388,6 +2474,7 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
       cslot += nch;
       cslot = cslot >= S ? cslot - S : cslot;
     }
+    mfma_drain(st.acc[0]);
     // ---- the piece is complete: this wave's columns ----
     const float vfin = PER_TOKEN ? st.vsmax : v_tensor_scale;
     store_piece<WORKLIST>(a, output, part_out, part_lse, cur, st.acc[0], sum_over_groups(st.lsum[0]), st.m2[0],
@@ -2806,6 +2893,11 @@ int check_stream_args(const pa_fp8_stream_args* a) {
       (!aligned16(a->key_scale) || !aligned16(a->value_scale) || (a->stride_ks_block % 4) || (a->stride_ks_head % 4)))
     return PA_ERR_ALIGN;
   if (!aligned16(a->output) || (a->stride_out_tok % 4) || (a->stride_out_head % 4)) return PA_ERR_ALIGN;
+  // a page's offset is computed as a 32 x 32-bit product
+  const int64_t smax = 0x7fffffffLL;
+  if (a->stride_k_block < 0 || a->stride_k_block > smax || a->stride_v_block < 0 || a->stride_v_block > smax ||
+      (a->per_token_kv && (a->stride_ks_block < 0 || a->stride_ks_block > smax)))
+    return PA_ERR_SHAPE;
   return PA_OK;
 }
 
