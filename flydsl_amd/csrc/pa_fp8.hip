@@ -148,9 +148,11 @@ __device__ __forceinline__ void split8_fp8(const float* x, long& hi, long& lo) {
 
 // acc *= f in place (tied operands): a conditional rescale then keeps the
 // accumulators in their registers on both paths (no copies on the path
-// that skips it).  Its input may come from mfma_k128_pair.
+// that skips it).  Its input may come from mfma_k128_pair, whose MFMAs it
+// waits out first (mfma_drain).
+__device__ __forceinline__ void mfma_drain(f32x4 (&acc)[8]);
 __device__ __forceinline__ void scale_inplace(f32x4 (&acc)[8], float f) {
-  asm volatile(PA_MFMA_DRAIN ::: "memory");
+  mfma_drain(acc);
 #pragma unroll
   for (int j = 0; j < 8; ++j)
 #pragma unroll
@@ -170,9 +172,10 @@ typedef int i32x8 __attribute__((ext_vector_type(8)));
 // VALU write of an operand needs before an MFMA reads it; the second
 // product reads the first's result as srcC with the same registers and
 // opcode (no wait).  Any other access of acc first waits out the MFMA
-// (mfma_drain, scale_inplace).
+// (mfma_drain, scale_inplace).  Not volatile: the operands order it, and
+// the next tile's LDS reads may then be scheduled ahead of it.
 __device__ __forceinline__ void mfma_k128_pair(f32x4& acc, const i32x8& a, const i32x8& b0, const i32x8& b1) {
-  asm volatile(
+  asm(
       "s_nop 1\n\t"
       "v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0\n\t"
       "v_mfma_f32_16x16x128_f8f6f4 %0, %1, %3, %0"
@@ -689,9 +692,9 @@ __device__ __forceinline__ void unit_softmax_pv(WaveState<1>& s, const QueryTile
     PL[2 * ch + 1] = (int)(uint32_t)((uint64_t)plo >> 32);
   }
   // value operands: head dim 16 j + c16, tokens 8 grp .. 8 grp + 7 of each
-  // chunk (stale bytes of edge chunks were zeroed in LDS)
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  // chunk (stale bytes of edge chunks were zeroed in LDS), the next tile's
+  // read ahead of this tile's products
+  auto value_tile = [&](int j) {
     i32x8 V = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int ch = 0; ch < NCH; ++ch) {
@@ -700,7 +703,14 @@ __device__ __forceinline__ void unit_softmax_pv(WaveState<1>& s, const QueryTile
       V[2 * ch] = (int)(uint32_t)v;
       V[2 * ch + 1] = (int)(uint32_t)(v >> 32);
     }
-    mfma_k128_pair(s.acc[0][j], V, PH, PL);
+    return V;
+  };
+  i32x8 VA[2];
+  VA[0] = value_tile(0);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (j + 1 < 8) VA[(j + 1) & 1] = value_tile(j + 1);
+    mfma_k128_pair(s.acc[0][j], VA[j & 1], PH, PL);
   }
   s.lsum[0] = s.lsum[0] * alpha + psum * vmul;
 }
@@ -732,13 +742,16 @@ __device__ __forceinline__ void unit4_softmax_pv(WaveState<1>& s, const QueryTil
     sl = sl >= S ? sl - S : sl;
     return ring + sl * kSlotBytes;
   };
-  const LDS_AS unsigned char* kb = slot_of(c16 >> 2) + (c16 & 3) * 16 + grp * 256;
+  const int kc = c16 >> 2;  // the chunk whose key rows this lane supplies
+  const LDS_AS unsigned char* kb = slot_of(kc) + (c16 & 3) * 16 + grp * 256;
   const LDS_AS unsigned char* own = slot_of(grp);
   const LDS_AS unsigned char* vb = own + kKBytes + c16 * 16;
   const LDS_AS float* sb = (const LDS_AS float*)(own + kKBytes + kVBytes);
-  // key products, the next tile's operand read ahead of this tile's MFMAs
+  // key products, the next tile's operand read ahead of this tile's MFMAs;
+  // token 4 t + i of chunk kc sits in row (4 t + i) ^ 4 kc of its half (the
+  // loads' swizzle)
   auto key_tile = [&](int t) {
-    const int off = (t >> 2) * kKHalf + (t & 3) * 64;
+    const int off = (t >> 2) * kKHalf + (((t & 3) ^ kc) << 6);
     const i32x4 k0 = *(const LDS_AS i32x4*)(kb + off);
     const i32x4 k1 = *(const LDS_AS i32x4*)(kb + off + 1024);
     return i32x8{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
@@ -836,13 +849,19 @@ __device__ __forceinline__ void unit4_softmax_pv(WaveState<1>& s, const QueryTil
     PL[2 * k8] = (int)(uint32_t)plo;
     PL[2 * k8 + 1] = (int)(uint32_t)((uint64_t)plo >> 32);
   }
-  // value operands (stale bytes of edge chunks were zeroed in LDS)
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  // value operands (stale bytes of edge chunks were zeroed in LDS), the
+  // next tile's read ahead of this tile's products
+  auto value_tile = [&](int j) {
     const i32x4 v0 = *(const LDS_AS i32x4*)(vb + j * 256);
     const i32x4 v1 = *(const LDS_AS i32x4*)(vb + j * 256 + 2048);
-    const i32x8 V = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-    mfma_k128_pair(s.acc[0][j], V, PH, PL);
+    return i32x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+  };
+  i32x8 VA[2];
+  VA[0] = value_tile(0);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (j + 1 < 8) VA[(j + 1) & 1] = value_tile(j + 1);
+    mfma_k128_pair(s.acc[0][j], VA[j & 1], PH, PL);
   }
   s.lsum[0] = s.lsum[0] * alpha + psum * vmul;
 }
@@ -2247,6 +2266,7 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
   // Issue cursor: next chunk at token itb of kv head ih, irem chunks left
   // in its piece, which is nxt when iw (else cur).
   int itb = 0, ih = 0, ilast = 0, irem = 0, iw = 0;
+  int ipos = 0;  // position of the next chunk in its piece
   int64_t ibt = 0;
   // This wave's share of every chunk, fixed for the launch: load i = wave *
   // kDmaPerWave + j of a chunk's eight 1 KiB loads is keys for i < 4 (else
@@ -2306,6 +2326,7 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
     ibt = p.bt_off;
     ilast = p.last_page;
     irem = p.n;
+    ipos = 0;
     iw = which;
     iok = true;
     ibase = rbase + (int64_t)ih * rstride_head;
@@ -2331,14 +2352,22 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
     islot = islot + 1 == S ? 0 : islot + 1;
     const uint8_t* pb0 = ibase + (uint64_t)(uint32_t)p0 * rsb + inpage;
     const uint8_t* pb1 = BS16 ? ibase + (uint64_t)(uint32_t)p1 * rsb : pb0;
+    // Four-chunk units: key token r of the chunk at unit position c goes to
+    // row r ^ 4c of its 16-token half (lane l of a key load fetches token
+    // (l & 15) ^ 4c), so the QK reads -- four tokens of each of the unit's
+    // four chunks per 16 lanes -- hit 16 different rows instead of the same
+    // banks of four slots.
+    const int kswz = (U == 4 && wk) ? (ipos & 3) << 6 : 0;
 #pragma unroll
-    for (int j = 0; j < kDmaPerWave; ++j) lds_dma16(((BS16 && hsel[j]) ? pb1 : pb0) + loff[j], sk + ldsoff[j]);
+    for (int j = 0; j < kDmaPerWave; ++j)
+      lds_dma16(((BS16 && hsel[j]) ? pb1 : pb0) + (loff[j] ^ kswz), sk + ldsoff[j]);
     if (scale_wave && lane < 16) {
       const int pg = BS16 ? (tt >= 16 ? p1 : p0) : p0;
       const int sidx = BS16 ? 0 : (itb & (bs - 1));
       lds_dma16(sbase + (uint64_t)(uint32_t)pg * ssb + sidx, sk + kKBytes + kVBytes);
     }
     ++issued;
+    ++ipos;
     itb += kChunk;
     if (--irem > 0)
       fetch_pages();
@@ -2728,6 +2757,687 @@ __global__ __launch_bounds__(256) void pa_fp8_lse_reduce_kernel(const pa_fp8_red
   }
 }
 
+// ===========================================================================
+// Generic decode: head size D = 64, 128, 192 or 256, any number of query
+// columns per kv head
+// ===========================================================================
+// The reference's small-block, window and persistent routes take any head
+// size that is a multiple of 64 and tile any query_length * gqa into
+// 16-column MFMA groups (kernels/pa_decode_fp8.py:2084-2085, 2101, 3058).
+// The tuned kernels above are built for D = 128 and up to 64 columns; every
+// other shape runs here, behind the same entry points and with the same
+// outputs.  A wave owns one 16-column block of one (sequence, kv head) and
+// streams a token range with K and V read straight from HBM into MFMA
+// operand registers (no LDS, no barriers: the waves of a workgroup are
+// independent, one per column block, and the grid's second dimension tiles
+// the blocks):
+//   * QK on v_mfma_f32_16x16x32_fp8_fp8, head dims along K: per 16-token
+//     tile, D / 32 MFMAs for each of the query's fp8 hi and lo terms; lane
+//     (grp, c16) supplies key row c16 (a token) and dims 8 grp .. 8 grp + 7
+//     of every 32-dim block, and gets the logits of tokens 4 grp .. 4 grp + 3
+//     of the tile for column c16;
+//   * PV on the same instruction with the chunk's 32 tokens along K: k-byte
+//     8 grp + i is token 4 grp + i (i < 4) or 16 + 4 grp + i - 4 of the
+//     chunk -- exactly the tokens whose logits the lane holds -- so the
+//     probabilities need no exchange; D / 16 output tiles, hi and lo
+//     probability terms.
+// The softmax is the online one of the tuned kernels (base-2 logits, a
+// power-of-two query scale, probabilities 2^(8 + l - m) <= 256 split into
+// two fp8 terms, per-token value scales folded into the probabilities
+// against a running reference).  Value bytes of tokens outside the
+// sequence's visible keys (stale page tails, slots before a window) are
+// zeroed before the value product, and their scales are zero.
+
+constexpr float kGenPBias = 8.0f;
+constexpr float kGenPUnscale = 1.0f / 256.0f;  // 2^-kGenPBias
+
+template <int D>
+struct GenState {
+  f32x4 acc[D / 16];
+  float m2;     // base-2 running maximum of the column's scaled logits
+  float lsum;   // this lane's share of sum 2^(pbias + l - m2)
+  float vsref;  // value-scale reference (1 for per-tensor scales)
+  __device__ __forceinline__ void reset(bool per_token) {
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m2 = kNegInf;
+    lsum = 0.0f;
+    vsref = per_token ? 0.0f : 1.0f;
+  }
+};
+
+// One (sequence, kv head) as a wave sees it: page list, bases and the
+// column block's query.
+template <int D>
+struct GenCtx {
+  const uint8_t* kbase;  // key_cache + h * stride_k_head
+  const uint8_t* vbase;
+  const float* ksbase;   // per-token scales + h * stride_ks_head
+  const float* vsbase;
+  const int32_t* pages;  // the sequence's page list
+  int ctx, last_page;
+  int lo_all, hi_all, lo_max, hi_min;  // union / intersection of the columns' keys
+  long qhi[D / 32], qlo[D / 32];
+  float fac;             // base-2 logit factor of the lane's column (> 0)
+  int vis_lo, vis_hi;    // keys the lane's column sees
+};
+
+struct GenArgs {
+  const void* query;
+  const uint8_t* key_cache;
+  const uint8_t* value_cache;
+  const int32_t* block_tables;
+  const int32_t* kv_indptr;
+  const int32_t* context_lengths;
+  const float* key_scale;
+  const float* value_scale;
+  int64_t stride_q_tok, stride_q_head;
+  int64_t stride_k_block, stride_k_head;
+  int64_t stride_v_block, stride_v_head;
+  int64_t stride_bt_seq;
+  int64_t stride_ks_block, stride_ks_head;
+  int num_seqs, num_kv_heads, query_length, query_group_size;
+  int block_size, num_blocks, max_blocks_per_seq, sliding_window, trans_v, query_dtype;
+  float softmax_scale;
+  // final output
+  void* output;
+  int output_dtype;
+  int64_t stride_out_tok, stride_out_head;
+  // slot partials (partition launches)
+  float* exp_sums;
+  float* max_logits;
+  void* tmp_out;
+  int tmp_dtype;
+  int64_t stride_es_seq, stride_es_head, stride_es_part;
+  int64_t stride_to_seq, stride_to_head, stride_to_part, stride_to_group;
+  int num_partitions;
+  int owner;  // one workgroup walks every slot and writes `output`
+  // work list
+  const int32_t* work_indptr;
+  const int32_t* work_info;
+  const int32_t* partition_indptr;
+  float* partial_output;
+  float* partial_lse;
+  int64_t stride_po_row, stride_pl_row;
+};
+
+// Sequence b, kv head h, the wave's column block (first column e0): page
+// list, bounds, and the query columns as fp8 hi + lo B operands scaled by a
+// power of two (prepare_query's scheme, for D dims).  Query row of column e:
+// orow + e / gqa.
+template <int D, bool PER_TOKEN>
+__device__ __forceinline__ bool gen_setup(GenCtx<D>& c, const GenArgs& a, int b, int h, int orow, int e0,
+                                          int grp, int c16) {
+  const int ql = a.query_length, gqa = a.query_group_size, eq = ql * gqa;
+  c.ctx = ld_uniform(a.context_lengths, b);
+  int row_len;
+  if (a.kv_indptr) {
+    const int p0 = ld_uniform(a.kv_indptr, b);
+    c.pages = a.block_tables + p0;
+    row_len = ld_uniform(a.kv_indptr, b + 1) - p0;
+  } else {
+    c.pages = a.block_tables + (int64_t)b * a.stride_bt_seq;
+    row_len = a.max_blocks_per_seq;
+  }
+  c.last_page = pa_min(pa_cdiv(c.ctx, a.block_size) - 1, row_len - 1);
+  pa_plan_visible(c.ctx, 0, ql, a.sliding_window, &c.lo_all, &c.hi_min);
+  pa_plan_visible(c.ctx, ql - 1, ql, a.sliding_window, &c.lo_max, &c.hi_all);
+  if (c.last_page < 0) c.hi_all = c.lo_all;
+  c.kbase = a.key_cache + (int64_t)h * a.stride_k_head;
+  c.vbase = a.value_cache + (int64_t)h * a.stride_v_head;
+  c.ksbase = PER_TOKEN ? a.key_scale + (int64_t)h * a.stride_ks_head : a.key_scale;
+  c.vsbase = PER_TOKEN ? a.value_scale + (int64_t)h * a.stride_ks_head : a.value_scale;
+
+  const int e = e0 + c16;
+  const bool valid = e < eq;
+  const int qi = valid ? e / gqa : 0;
+  const int g = valid ? e - qi * gqa : 0;
+  float v[D / 32][8];
+#pragma unroll
+  for (int blk = 0; blk < D / 32; ++blk) {
+    i32x4 w = i32x4{0, 0, 0, 0};
+    if (valid)
+      w = *(const i32x4*)((const uint16_t*)a.query + (int64_t)(orow + qi) * a.stride_q_tok +
+                          (int64_t)(h * gqa + g) * a.stride_q_head + 32 * blk + 8 * grp);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t u = (uint32_t)w[i];
+      v[blk][2 * i] = a.query_dtype == PA_DTYPE_F16 ? f16_bits_to_f32(u & 0xffffu) : bf16_bits_to_f32(u & 0xffffu);
+      v[blk][2 * i + 1] = a.query_dtype == PA_DTYPE_F16 ? f16_bits_to_f32(u >> 16) : bf16_bits_to_f32(u >> 16);
+    }
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int blk = 0; blk < D / 32; ++blk)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[blk][i]));
+  amax = max_over_groups(amax);
+  int sexp = 261 - (int)((__float_as_uint(amax) >> 23) & 0xffu);
+  sexp = sexp < 1 ? 1 : (sexp > 254 ? 254 : sexp);
+  const float logit_scale = a.softmax_scale * kLog2e * (PER_TOKEN ? 1.0f : a.key_scale[0]);
+  const float sq0 = amax > 0.0f ? __uint_as_float((uint32_t)sexp << 23) : 1.0f;
+  const float sq = logit_scale < 0.0f ? -sq0 : sq0;
+#pragma unroll
+  for (int blk = 0; blk < D / 32; ++blk) {
+    float xs[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xs[i] = v[blk][i] * sq;
+    split8_fp8(xs, c.qhi[blk], c.qlo[blk]);
+  }
+  c.fac = fmaxf(logit_scale / sq, 1e-30f);
+  int lo = 0, hi = 0;
+  if (valid) pa_plan_visible(c.ctx, qi, ql, a.sliding_window, &lo, &hi);
+  c.vis_lo = lo;
+  c.vis_hi = hi;
+  c.lo_all = __builtin_amdgcn_readfirstlane(c.lo_all);
+  c.hi_all = __builtin_amdgcn_readfirstlane(c.hi_all);
+  c.lo_max = __builtin_amdgcn_readfirstlane(c.lo_max);
+  c.hi_min = __builtin_amdgcn_readfirstlane(c.hi_min);
+  return true;
+}
+
+__device__ __forceinline__ int gen_page(const GenArgs& a, const int32_t* pages, int last_page, int tok) {
+  int lp = pa_min(tok / a.block_size, last_page);
+  int p = ld_uniform(pages, lp);
+  p = p < 0 ? 0 : p;
+  return p < a.num_blocks ? p : a.num_blocks - 1;
+}
+
+// Byte mask keeping the bytes of tokens [lo, hi) among the 4 tokens t .. t + 3.
+__device__ __forceinline__ uint32_t gen_keep4(int t, int lo, int hi) {
+  const int l = pa_min(pa_max(lo - t, 0), 4), u = pa_min(pa_max(hi - t, l), 4);
+  const uint32_t below_u = u >= 4 ? ~0u : (1u << (8 * u)) - 1;
+  const uint32_t below_l = l >= 4 ? ~0u : (1u << (8 * l)) - 1;
+  return below_u & ~below_l;
+}
+
+// Online softmax of the lane's column over keys [t0, t1) into st.
+template <int D, bool PER_TOKEN>
+__device__ void gen_range(GenState<D>& st, const GenCtx<D>& c, const GenArgs& a, int t0, int t1, int grp,
+                          int c16) {
+  // keys any column may use, and the stale-byte bound
+  const int A = pa_max(t0, c.lo_all), B = pa_min(t1, c.hi_all);
+  if (B <= A) return;
+  const int bs = a.block_size;
+  const int vis_lo = pa_max(c.vis_lo, t0), vis_hi = pa_min(c.vis_hi, t1);
+  for (int tc = A & ~31; tc < B; tc += 32) {
+    int pg[2], sb[2];
+#pragma unroll
+    for (int tau = 0; tau < 2; ++tau) {
+      pg[tau] = gen_page(a, c.pages, c.last_page, tc + 16 * tau);
+      sb[tau] = (tc + 16 * tau) % bs;
+    }
+    // ---- logits of tokens tc + 16 tau + 4 grp + i ----
+    f32x4 lt[2];
+#pragma unroll
+    for (int tau = 0; tau < 2; ++tau) {
+      const uint8_t* kp = c.kbase + (int64_t)pg[tau] * a.stride_k_block + (sb[tau] + c16) * 16 + 8 * (grp & 1);
+      long kr[D / 32];
+#pragma unroll
+      for (int blk = 0; blk < D / 32; ++blk) kr[blk] = *(const long*)(kp + (int64_t)(2 * blk + (grp >> 1)) * bs * 16);
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int blk = 0; blk < D / 32; ++blk) {
+        acc = mfma_fp8(kr[blk], c.qhi[blk], acc);
+        acc = mfma_fp8(kr[blk], c.qlo[blk], acc);
+      }
+      lt[tau] = acc;
+    }
+    float x[8], vs[8];
+#pragma unroll
+    for (int tau = 0; tau < 2; ++tau)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[4 * tau + i] = lt[tau][i];
+        vs[4 * tau + i] = 1.0f;
+      }
+    if (PER_TOKEN) {
+#pragma unroll
+      for (int tau = 0; tau < 2; ++tau) {
+        const int64_t so = (int64_t)pg[tau] * a.stride_ks_block + sb[tau] + 4 * grp;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x[4 * tau + i] *= c.ksbase[so + i];
+          vs[4 * tau + i] = c.vsbase[so + i];
+        }
+      }
+    }
+    // ---- masks (edge chunks only) ----
+    const bool all_vis = tc >= pa_max(t0, c.lo_max) && tc + 32 <= pa_min(t1, c.hi_min);
+    if (!all_vis) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int t = tc + 16 * (k >> 2) + 4 * grp + (k & 3);
+        x[k] = (t >= vis_lo && t < vis_hi) ? x[k] : kNegInf;
+        if (PER_TOKEN) vs[k] = (t >= A && t < B) ? vs[k] : 0.0f;
+      }
+    }
+    // ---- online softmax ----
+    float cmax = kNegInf;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) cmax = fmaxf(cmax, x[k]);
+    cmax = max_over_groups(cmax) * c.fac;
+    const float mnew = fmaxf(st.m2, cmax);
+    const float muse = mnew == kNegInf ? 0.0f : mnew;
+    const float alpha = __builtin_amdgcn_exp2f(st.m2 - muse);
+    float vratio = 1.0f, vinv = 1.0f;
+    if (PER_TOKEN) {
+      float vmax = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) vmax = fmaxf(vmax, vs[k]);
+      vmax = max_over_groups(vmax);
+      const float vnew = fmaxf(st.vsref, vmax);
+      vratio = st.vsref > 0.0f ? st.vsref / vnew : 1.0f;
+      vinv = vnew > 0.0f ? 1.0f / vnew : 0.0f;
+      st.vsref = vnew;
+    }
+    st.m2 = mnew;
+    const float f = alpha * vratio;
+    if (__ballot(f != 1.0f)) {
+#pragma unroll
+      for (int j = 0; j < D / 16; ++j) st.acc[j] *= f;
+    }
+    const float bias = kGenPBias - muse;
+    float psum = 0.0f, pr[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(x[k], c.fac, bias));
+      psum += p;
+      pr[k] = PER_TOKEN ? p * (vs[k] * vinv) : p;
+    }
+    st.lsum = st.lsum * alpha + psum;
+    long phi, plo;
+    split8_fp8(pr, phi, plo);
+    // ---- value product: tokens 4 grp .. +3 and 16 + 4 grp .. +3 ----
+    uint32_t keep[2] = {~0u, ~0u};
+    const bool stale = tc < A || tc + 32 > B;
+    if (stale) {
+#pragma unroll
+      for (int tau = 0; tau < 2; ++tau) keep[tau] = gen_keep4(tc + 16 * tau + 4 * grp, A, B);
+    }
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) {
+      const int d = 16 * j + c16;
+      uint32_t w[2];
+#pragma unroll
+      for (int tau = 0; tau < 2; ++tau) {
+        const int s = sb[tau] + 4 * grp;
+        const int64_t off = a.trans_v ? ((int64_t)(s >> 4) * D + d) * 16 + (s & 15) : (int64_t)d * bs + s;
+        w[tau] = *(const uint32_t*)(c.vbase + (int64_t)pg[tau] * a.stride_v_block + off) & keep[tau];
+      }
+      const long vv = (long)((uint64_t)w[0] | ((uint64_t)w[1] << 32));
+      st.acc[j] = mfma_fp8(vv, phi, st.acc[j]);
+      st.acc[j] = mfma_fp8(vv, plo, st.acc[j]);
+    }
+  }
+}
+
+// s := s merged with t (two disjoint key ranges of one column).
+template <int D, bool PER_TOKEN>
+__device__ __forceinline__ void gen_merge(GenState<D>& s, const GenState<D>& t) {
+  const float m = fmaxf(s.m2, t.m2);
+  if (__ballot(m != kNegInf) == 0) return;
+  const float mu = m == kNegInf ? 0.0f : m;
+  const float as = __builtin_amdgcn_exp2f(s.m2 - mu), at = __builtin_amdgcn_exp2f(t.m2 - mu);
+  float fs = as, ft = at, vref = 1.0f;
+  if (PER_TOKEN) {
+    vref = fmaxf(s.vsref, t.vsref);
+    fs *= vref > 0.0f ? s.vsref / vref : 0.0f;
+    ft *= vref > 0.0f ? t.vsref / vref : 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < D / 16; ++j) s.acc[j] = s.acc[j] * fs + t.acc[j] * ft;
+  s.lsum = s.lsum * as + t.lsum * at;
+  s.m2 = m;
+  s.vsref = vref;
+}
+
+// Normalised result of the lane's column: out = acc * scale; returns the
+// column's natural-log log-sum-exp (-inf when it saw no key) and, in *es /
+// *ml, the exp-sum and maximum of the slot-partial convention.
+template <int D, bool PER_TOKEN>
+__device__ __forceinline__ float gen_finish(const GenState<D>& st, const GenArgs& a, float& scale, float& es,
+                                            float& ml) {
+  const float L = sum_over_groups(st.lsum);
+  const float vfin = PER_TOKEN ? st.vsref : a.value_scale[0];
+  scale = L > 0.0f ? vfin / L : 0.0f;
+  es = L > 0.0f ? L * kGenPUnscale : 0.0f;  // sum 2^(l - m) = L / 2^pbias
+  ml = L > 0.0f ? kLn2 * st.m2 : kNegInf;
+  return L > 0.0f ? kLn2 * (st.m2 + __builtin_amdgcn_logf(L) - kGenPBias) : kNegInf;
+}
+
+__device__ __forceinline__ void gen_store4(void* base, int dtype, int64_t off, f32x4 v) {
+  if (dtype == PA_DTYPE_F32) {
+    *(f32x4*)((float*)base + off) = v;
+  } else if (dtype == PA_DTYPE_F16) {
+    *(uint2*)((uint16_t*)base + off) = uint2{f32_to_f16_bits(v[0]) | (f32_to_f16_bits(v[1]) << 16),
+                                             f32_to_f16_bits(v[2]) | (f32_to_f16_bits(v[3]) << 16)};
+  } else {
+    *(uint2*)((uint16_t*)base + off) = uint2{f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16),
+                                             f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16)};
+  }
+}
+
+// Partition launches: workgroup (b, h, slot) -- or (b, h) when `owner` --
+// and column block 4 * blockIdx.y + wave.  A slot stores exp_sums /
+// max_logits / tmp_out for its columns; an owner walks every slot (storing
+// its partials when the buffers are given), folds them and writes `output`.
+template <int D, bool PER_TOKEN>
+__global__ __launch_bounds__(256) void pa_fp8_generic_partition_kernel(const GenArgs a) {
+  const int lane = threadIdx.x & 63, grp = lane >> 4, c16 = lane & 15;
+  const int wave = threadIdx.x >> 6;
+  const int eq = a.query_length * a.query_group_size;
+  const int e0 = (4 * (int)blockIdx.y + wave) * 16;
+  if (e0 >= eq) return;
+  const int P = a.num_partitions;
+  const int per = a.owner ? 1 : P;
+  const int z0 = a.owner ? 0 : (int)(blockIdx.x % per);
+  const int bh = (int)(blockIdx.x / per);
+  const int h = bh % a.num_kv_heads, b = bh / a.num_kv_heads;
+  GenCtx<D> c;
+  gen_setup<D, PER_TOKEN>(c, a, b, h, b * a.query_length, e0, grp, c16);
+  const int e = e0 + c16;
+  const bool valid = e < eq;
+  GenState<D> fin;
+  fin.reset(PER_TOKEN);
+  const int z1 = a.owner ? P : z0 + 1;
+  for (int z = z0; z < z1; ++z) {
+    int t0, t1;
+    pa_plan_slot_tokens(c.ctx, P, z, a.sliding_window, a.query_length, &t0, &t1);
+    GenState<D> st;
+    st.reset(PER_TOKEN);
+    gen_range<D, PER_TOKEN>(st, c, a, t0, t1, grp, c16);
+    if (a.exp_sums) {
+      float sc, es, ml;
+      gen_finish<D, PER_TOKEN>(st, a, sc, es, ml);
+      if (valid) {
+        const int64_t so = (int64_t)b * a.stride_es_seq + (int64_t)h * a.stride_es_head + (int64_t)z * a.stride_es_part + e;
+        if (grp == 0) {
+          a.exp_sums[so] = es;
+          a.max_logits[so] = ml;
+        }
+        const int64_t to = (int64_t)b * a.stride_to_seq + (int64_t)h * a.stride_to_head + (int64_t)z * a.stride_to_part +
+                           (int64_t)e * a.stride_to_group + 4 * grp;
+#pragma unroll
+        for (int j = 0; j < D / 16; ++j) gen_store4(a.tmp_out, a.tmp_dtype, to + 16 * j, st.acc[j] * sc);
+      }
+    }
+    if (a.owner) gen_merge<D, PER_TOKEN>(fin, st);
+  }
+  if (a.owner && valid) {
+    float sc, es, ml;
+    gen_finish<D, PER_TOKEN>(fin, a, sc, es, ml);
+    const int qi = e / a.query_group_size, g = e - qi * a.query_group_size;
+    const int64_t off = (int64_t)(b * a.query_length + qi) * a.stride_out_tok +
+                        (int64_t)(h * a.query_group_size + g) * a.stride_out_head + 4 * grp;
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) gen_store4(a.output, a.output_dtype, off + 16 * j, fin.acc[j] * sc);
+  }
+}
+
+// Work-list launches: workgroup = bin blockIdx.x (its works in order), column
+// block 4 * blockIdx.y + wave.  A work writes output rows qo_start + qi
+// (partial row < 0) or float32 partial rows ploc + query_length + qi and
+// their log-sum-exp.
+template <int D, bool PER_TOKEN>
+__global__ __launch_bounds__(256) void pa_fp8_generic_worklist_kernel(const GenArgs a) {
+  const int lane = threadIdx.x & 63, grp = lane >> 4, c16 = lane & 15;
+  const int wave = threadIdx.x >> 6;
+  const int gqa = a.query_group_size, eq = a.query_length * gqa;
+  const int e0 = (4 * (int)blockIdx.y + wave) * 16;
+  if (e0 >= eq) return;
+  const int e = e0 + c16;
+  const bool valid = e < eq;
+  const int qi = valid ? e / gqa : 0, g = valid ? e - qi * gqa : 0;
+  const int w0 = ld_uniform(a.work_indptr, blockIdx.x), w1 = ld_uniform(a.work_indptr, blockIdx.x + 1);
+  for (int w = w0; w < w1; ++w) {
+    const int64_t wi = 8 * (int64_t)w;
+    const int b = ld_uniform(a.work_info, wi), ploc = ld_uniform(a.work_info, wi + 1);
+    const int qo0 = ld_uniform(a.work_info, wi + 2);
+    const int kv0 = ld_uniform(a.work_info, wi + 4), kv1 = ld_uniform(a.work_info, wi + 5);
+    const int h = (ld_uniform(a.work_info, wi + 7) & 0xffff) / gqa;
+    GenCtx<D> c;
+    gen_setup<D, PER_TOKEN>(c, a, b, h, qo0, e0, grp, c16);
+    const int pb = ld_uniform(a.partition_indptr, b);
+    const int t0 = (kv0 - pb) * PA_PARTITION_TOKENS, t1 = pa_min((kv1 - pb) * PA_PARTITION_TOKENS, c.ctx);
+    GenState<D> st;
+    st.reset(PER_TOKEN);
+    gen_range<D, PER_TOKEN>(st, c, a, t0, t1, grp, c16);
+    float sc, es, ml;
+    const float lse = gen_finish<D, PER_TOKEN>(st, a, sc, es, ml);
+    if (!valid) continue;
+    const int qh = h * gqa + g;
+    if (ploc < 0) {
+      const int64_t off = (int64_t)(qo0 + qi) * a.stride_out_tok + (int64_t)qh * a.stride_out_head + 4 * grp;
+#pragma unroll
+      for (int j = 0; j < D / 16; ++j) gen_store4(a.output, a.output_dtype, off + 16 * j, st.acc[j] * sc);
+    } else {
+      const int64_t row = ploc + a.query_length + qi;
+#pragma unroll
+      for (int j = 0; j < D / 16; ++j)
+        *(f32x4*)(a.partial_output + row * a.stride_po_row + (int64_t)qh * D + 16 * j + 4 * grp) = st.acc[j] * sc;
+      if (grp == 0) a.partial_lse[row * a.stride_pl_row + qh] = lse;
+    }
+  }
+}
+
+// Log-sum-exp merges for any head size: lane l of a wave takes head dims
+// l + 64 k, k < NK = D / 64 (the 128-dim kernels above keep their
+// two-adjacent-dims layout).
+template <int NK>
+__global__ __launch_bounds__(256) void pa_fp8_generic_lse_reduce_kernel(const pa_fp8_reduce_args a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int eq = a.query_length * a.query_group_size;
+  const int64_t rows = (int64_t)a.num_seqs * a.num_kv_heads * eq;
+  if (row >= rows) return;
+  const int e = (int)(row % eq);
+  const int h = (int)((row / eq) % a.num_kv_heads);
+  const int b = (int)(row / ((int64_t)eq * a.num_kv_heads));
+  const int64_t sbase = (int64_t)b * a.stride_es_seq + (int64_t)h * a.stride_es_head + e;
+  const int64_t tbase = (int64_t)b * a.stride_to_seq + (int64_t)h * a.stride_to_head + (int64_t)e * a.stride_to_group + lane;
+  float M = kNegInf;
+  for (int p = 0; p < a.num_partitions; ++p) M = fmaxf(M, a.max_logits[sbase + p * a.stride_es_part]);
+  float tot = 0.0f, o[NK];
+#pragma unroll
+  for (int k = 0; k < NK; ++k) o[k] = 0.0f;
+  if (M != kNegInf) {
+    for (int p = 0; p < a.num_partitions; ++p) {
+      const float m = a.max_logits[sbase + p * a.stride_es_part];
+      if (m == kNegInf) continue;
+      const float w = a.exp_sums[sbase + p * a.stride_es_part] * __expf(m - M);
+      tot += w;
+      const int64_t off = tbase + (int64_t)p * a.stride_to_part;
+#pragma unroll
+      for (int k = 0; k < NK; ++k) {
+        const float x = a.tmp_dtype == PA_DTYPE_F32 ? ((const float*)a.tmp_out)[off + 64 * k]
+                                                    : bf16_bits_to_f32(((const uint16_t*)a.tmp_out)[off + 64 * k]);
+        o[k] += w * x;
+      }
+    }
+  }
+  const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
+  const int gqa = a.query_group_size;
+  const int qi = e / gqa, g = e - qi * gqa;
+  const int64_t off = (int64_t)b * a.stride_out_seq + (int64_t)qi * a.stride_out_ql + (int64_t)h * a.stride_out_kv_head +
+                      (int64_t)g * a.stride_out_group + lane;
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    const float v = o[k] * inv;
+    if (a.output_dtype == PA_DTYPE_F32)
+      ((float*)a.output)[off + 64 * k] = v;
+    else if (a.output_dtype == PA_DTYPE_F16)
+      ((uint16_t*)a.output)[off + 64 * k] = (uint16_t)f32_to_f16_bits(v);
+    else
+      ((uint16_t*)a.output)[off + 64 * k] = (uint16_t)f32_to_bf16_bits(v);
+  }
+}
+
+template <int NK>
+__global__ __launch_bounds__(256) void pa_fp8_generic_worklist_reduce_kernel(const pa_fp8_worklist_reduce_args a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int Hq = a.num_query_heads, mq = a.max_query_length;
+  if (row >= (int64_t)a.num_groups * mq * Hq) return;
+  const int qh = (int)(row % Hq);
+  const int qi = (int)((row / Hq) % mq);
+  const int g = (int)(row / ((int64_t)Hq * mq));
+  const int p0 = a.reduce_indptr[g], p1 = a.reduce_indptr[g + 1];
+  if (p1 <= p0) return;
+  const int qo0 = a.reduce_final_map[2 * g], qo1 = a.reduce_final_map[2 * g + 1];
+  if (qi >= qo1 - qo0) return;
+  const int32_t* pmap = a.reduce_partial_map + p0;
+  const int D = 64 * NK;
+  float M = kNegInf;
+  for (int i = 0; i < p1 - p0; ++i) M = fmaxf(M, a.partial_lse[(int64_t)(pmap[i] + qi) * a.stride_pl_row + qh]);
+  float tot = 0.0f, o[NK];
+#pragma unroll
+  for (int k = 0; k < NK; ++k) o[k] = 0.0f;
+  if (M != kNegInf) {
+    for (int i = 0; i < p1 - p0; ++i) {
+      const float l = a.partial_lse[(int64_t)(pmap[i] + qi) * a.stride_pl_row + qh];
+      if (l == kNegInf) continue;
+      const float w = __expf(l - M);
+      tot += w;
+      const float* r = a.partial_output + (int64_t)(pmap[i] + qi) * a.stride_po_row + (int64_t)qh * D + lane;
+#pragma unroll
+      for (int k = 0; k < NK; ++k) o[k] += w * r[64 * k];
+    }
+  }
+  const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
+  const int64_t off = (int64_t)(qo0 + qi) * a.stride_out_tok + (int64_t)qh * a.stride_out_head + lane;
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    const float v = o[k] * inv;
+    if (a.output_dtype == PA_DTYPE_F32)
+      ((float*)a.output)[off + 64 * k] = v;
+    else if (a.output_dtype == PA_DTYPE_F16)
+      ((uint16_t*)a.output)[off + 64 * k] = (uint16_t)f32_to_f16_bits(v);
+    else
+      ((uint16_t*)a.output)[off + 64 * k] = (uint16_t)f32_to_bf16_bits(v);
+  }
+}
+
+// Host side: the generic path takes D = 64 .. 256 and any column count.
+static bool generic_head_ok(int d) { return d == 64 || d == 128 || d == 192 || d == 256; }
+
+template <int D, bool PT>
+static hipError_t launch_generic_partition(const GenArgs& g, dim3 grid, dim3 block, hipStream_t s) {
+  hipLaunchKernelGGL((pa_fp8_generic_partition_kernel<D, PT>), grid, block, 0, s, g);
+  return hipGetLastError();
+}
+template <int D, bool PT>
+static hipError_t launch_generic_worklist(const GenArgs& g, dim3 grid, dim3 block, hipStream_t s) {
+  hipLaunchKernelGGL((pa_fp8_generic_worklist_kernel<D, PT>), grid, block, 0, s, g);
+  return hipGetLastError();
+}
+
+template <typename F>
+static hipError_t generic_dispatch(int d, bool pt, F&& f) {
+  switch (d) {
+    case 64: return pt ? f(std::integral_constant<int, 64>{}, std::true_type{}) : f(std::integral_constant<int, 64>{}, std::false_type{});
+    case 128: return pt ? f(std::integral_constant<int, 128>{}, std::true_type{}) : f(std::integral_constant<int, 128>{}, std::false_type{});
+    case 192: return pt ? f(std::integral_constant<int, 192>{}, std::true_type{}) : f(std::integral_constant<int, 192>{}, std::false_type{});
+    default: return pt ? f(std::integral_constant<int, 256>{}, std::true_type{}) : f(std::integral_constant<int, 256>{}, std::false_type{});
+  }
+}
+
+GenArgs gen_common(const void* query, const void* key_cache, const void* value_cache, const int32_t* block_tables,
+                   const int32_t* kv_indptr, const int32_t* context_lengths, const float* key_scale,
+                   const float* value_scale) {
+  GenArgs g = {};
+  g.query = query;
+  g.key_cache = (const uint8_t*)key_cache;
+  g.value_cache = (const uint8_t*)value_cache;
+  g.block_tables = block_tables;
+  g.kv_indptr = kv_indptr;
+  g.context_lengths = context_lengths;
+  g.key_scale = key_scale;
+  g.value_scale = value_scale;
+  return g;
+}
+
+template <typename Args>
+void gen_shape(GenArgs& g, const Args& a) {
+  g.stride_q_tok = a.stride_q_tok;
+  g.stride_q_head = a.stride_q_head;
+  g.stride_k_block = a.stride_k_block;
+  g.stride_k_head = a.stride_k_head;
+  g.stride_v_block = a.stride_v_block;
+  g.stride_v_head = a.stride_v_head;
+  g.stride_bt_seq = a.stride_bt_seq;
+  g.stride_ks_block = a.stride_ks_block;
+  g.stride_ks_head = a.stride_ks_head;
+  g.num_seqs = a.num_seqs;
+  g.num_kv_heads = a.num_kv_heads;
+  g.query_length = a.query_length;
+  g.query_group_size = a.query_group_size;
+  g.block_size = a.block_size;
+  g.num_blocks = a.num_blocks;
+  g.max_blocks_per_seq = a.max_blocks_per_seq;
+  g.sliding_window = a.sliding_window;
+  g.trans_v = a.trans_v;
+  g.query_dtype = a.query_dtype;
+  g.softmax_scale = a.softmax_scale;
+  g.output = a.output;
+  g.output_dtype = a.output_dtype;
+  g.stride_out_tok = a.stride_out_tok;
+  g.stride_out_head = a.stride_out_head;
+}
+
+// Columns per kv head beyond the tuned kernels' 64, or a head size other
+// than 128: the generic kernels (workgroup of one wave per 16-column block,
+// up to four; the grid's second dimension tiles the blocks).
+int generic_partition(const pa_fp8_partition_args& a, bool owner, hipStream_t s) {
+  GenArgs g = gen_common(a.query, a.key_cache, a.value_cache, a.block_tables, a.kv_indptr, a.context_lengths,
+                         a.key_scale, a.value_scale);
+  gen_shape(g, a);
+  g.exp_sums = a.exp_sums;
+  g.max_logits = a.max_logits;
+  g.tmp_out = a.tmp_out;
+  g.tmp_dtype = a.tmp_dtype;
+  g.stride_es_seq = a.stride_es_seq;
+  g.stride_es_head = a.stride_es_head;
+  g.stride_es_part = a.stride_es_part;
+  g.stride_to_seq = a.stride_to_seq;
+  g.stride_to_head = a.stride_to_head;
+  g.stride_to_part = a.stride_to_part;
+  g.stride_to_group = a.stride_to_group;
+  g.num_partitions = a.num_partitions;
+  g.owner = owner ? 1 : 0;
+  const int ncg = pa_cdiv(a.query_length * a.query_group_size, 16);
+  const int64_t gx = (int64_t)a.num_seqs * a.num_kv_heads * (owner ? 1 : a.num_partitions);
+  const int gy = pa_cdiv(ncg, 4);
+  if (gx == 0) return PA_OK;
+  if (gx > 0x7fffffffLL || gy > 65535) return PA_ERR_SHAPE;
+  const dim3 grid((unsigned)gx, (unsigned)gy), block(64 * pa_min(ncg, 4));
+  hipError_t err = generic_dispatch(a.head_size, a.per_token_kv != 0, [&](auto d, auto pt) {
+    return launch_generic_partition<decltype(d)::value, decltype(pt)::value>(g, grid, block, s);
+  });
+  return err == hipSuccess ? PA_OK : (int)err;
+}
+
+int generic_worklist(const pa_fp8_stream_args& a, hipStream_t s) {
+  GenArgs g = gen_common(a.query, a.key_cache, a.value_cache, a.block_tables, a.kv_indptr, a.context_lengths,
+                         a.key_scale, a.value_scale);
+  gen_shape(g, a);
+  g.work_indptr = a.work_indptr;
+  g.work_info = a.work_info;
+  g.partition_indptr = a.partition_indptr;
+  g.partial_output = a.partial_output;
+  g.partial_lse = a.partial_lse;
+  g.stride_po_row = a.stride_po_row;
+  g.stride_pl_row = a.stride_pl_row;
+  const int ncg = pa_cdiv(a.query_length * a.query_group_size, 16);
+  const int gy = pa_cdiv(ncg, 4);
+  if (gy > 65535) return PA_ERR_SHAPE;
+  const dim3 grid((unsigned)a.num_workers, (unsigned)gy), block(64 * pa_min(ncg, 4));
+  hipError_t err = generic_dispatch(a.head_size, a.per_token_kv != 0, [&](auto d, auto pt) {
+    return launch_generic_worklist<decltype(d)::value, decltype(pt)::value>(g, grid, block, s);
+  });
+  return err == hipSuccess ? PA_OK : (int)err;
+}
+
 template <int NCG, bool PT, bool BS16, bool MULTI, int WAVES>
 hipError_t launch_partition(const pa_fp8_partition_args& a, unsigned grid, hipStream_t s) {
   hipLaunchKernelGGL((pa_fp8_partition_kernel<NCG, PT, BS16, kStages, MULTI, WAVES>), dim3(grid), dim3(64 * WAVES), 0,
@@ -2869,19 +3579,21 @@ hipError_t dispatch_worklist(const pa_fp8_stream_args& a, hipStream_t s) {
 }
 
 // Checks shared by both streaming entry points.
-int check_stream_args(const pa_fp8_stream_args* a) {
+// generic_ok: the launch may run on the generic kernels (head sizes 64 ..
+// 256, any column count); the balanced decode may not.
+int check_stream_args(const pa_fp8_stream_args* a, bool generic_ok = false) {
   if (!a) return PA_ERR_NULL_ARG;
   if (a->abi_version != PA_FP8_ABI_VERSION) return PA_ERR_ABI;
   if (!a->output || !a->query || !a->key_cache || !a->value_cache || !a->block_tables || !a->context_lengths ||
       !a->key_scale || !a->value_scale)
     return PA_ERR_NULL_ARG;
-  if (a->head_size != kHead) return PA_ERR_HEAD_SIZE;
+  if (!(generic_ok ? generic_head_ok(a->head_size) : a->head_size == kHead)) return PA_ERR_HEAD_SIZE;
   const int bs = a->block_size;
   if (!(bs == 16 || (bs >= 32 && bs <= 1024 && (bs & (bs - 1)) == 0))) return PA_ERR_BLOCK_SIZE;
   if (a->num_seqs < 0 || a->num_kv_heads <= 0 || a->query_length <= 0 || a->query_group_size <= 0 ||
       a->num_blocks <= 0 || a->max_blocks_per_seq <= 0 || a->sliding_window < 0 || a->num_workers <= 0)
     return PA_ERR_SHAPE;
-  if (a->query_length * a->query_group_size > 64) return PA_ERR_GROUP;
+  if (!generic_ok && a->query_length * a->query_group_size > 64) return PA_ERR_GROUP;
   if (a->query_dtype != PA_DTYPE_BF16 && a->query_dtype != PA_DTYPE_F16) return PA_ERR_DTYPE;
   if (a->output_dtype != PA_DTYPE_BF16 && a->output_dtype != PA_DTYPE_F16 && a->output_dtype != PA_DTYPE_F32)
     return PA_ERR_DTYPE;
@@ -2968,14 +3680,14 @@ int pa_fp8_decode_partition(const pa_fp8_partition_args* a, void* stream) {
   if (a->output != nullptr && !owner) return PA_ERR_SHAPE;  // output needs every slot
   if (!partials && a->output == nullptr) return PA_ERR_NULL_ARG;
   const bool fused = !partials;
-  if (a->head_size != kHead) return PA_ERR_HEAD_SIZE;
+  if (!generic_head_ok(a->head_size)) return PA_ERR_HEAD_SIZE;
   const int bs = a->block_size;
   if (!(bs == 16 || (bs >= 32 && bs <= 1024 && (bs & (bs - 1)) == 0))) return PA_ERR_BLOCK_SIZE;
   if (a->num_seqs < 0 || a->num_kv_heads <= 0 || a->num_partitions <= 0 || a->query_length <= 0 ||
       a->query_group_size <= 0 || a->num_blocks <= 0 || a->max_blocks_per_seq <= 0 || a->sliding_window < 0)
     return PA_ERR_SHAPE;
   const int eq = a->query_length * a->query_group_size;
-  if (eq > 64) return PA_ERR_GROUP;
+  const bool generic = a->head_size != kHead || eq > 64;
   if (a->query_dtype != PA_DTYPE_BF16 && a->query_dtype != PA_DTYPE_F16) return PA_ERR_DTYPE;
   if (!fused && a->tmp_dtype != PA_DTYPE_BF16 && a->tmp_dtype != PA_DTYPE_F32) return PA_ERR_DTYPE;
   if (a->output && a->output_dtype != PA_DTYPE_BF16 && a->output_dtype != PA_DTYPE_F16 && a->output_dtype != PA_DTYPE_F32)
@@ -2996,6 +3708,7 @@ int pa_fp8_decode_partition(const pa_fp8_partition_args* a, void* stream) {
         (a->stride_to_seq % 8))
       return PA_ERR_ALIGN;
   }
+  if (generic) return generic_partition(*a, owner, (hipStream_t)stream);
   const int64_t grid = (int64_t)a->num_seqs * a->num_kv_heads * pa_cdiv(a->num_partitions, spw);
   if (grid == 0) return PA_OK;
   if (grid > 0x7fffffffLL) return PA_ERR_SHAPE;
@@ -3032,7 +3745,7 @@ int pa_fp8_decode_reduce(const pa_fp8_reduce_args* a, void* stream) {
   if (!a) return PA_ERR_NULL_ARG;
   if (a->abi_version != PA_FP8_ABI_VERSION) return PA_ERR_ABI;
   if (!a->output || !a->exp_sums || !a->max_logits || !a->tmp_out) return PA_ERR_NULL_ARG;
-  if (a->head_size != kHead) return PA_ERR_HEAD_SIZE;
+  if (!generic_head_ok(a->head_size)) return PA_ERR_HEAD_SIZE;
   if (a->num_seqs < 0 || a->num_kv_heads <= 0 || a->num_partitions <= 0 || a->query_length <= 0 ||
       a->query_group_size <= 0)
     return PA_ERR_SHAPE;
@@ -3043,7 +3756,13 @@ int pa_fp8_decode_reduce(const pa_fp8_reduce_args* a, void* stream) {
   if (rows == 0) return PA_OK;
   const int64_t grid = (rows + 3) / 4;
   if (grid > 0x7fffffffLL) return PA_ERR_SHAPE;
-  hipLaunchKernelGGL(pa_fp8_lse_reduce_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, *a);
+  hipStream_t s = (hipStream_t)stream;
+  switch (a->head_size) {
+    case 64: hipLaunchKernelGGL(pa_fp8_generic_lse_reduce_kernel<1>, dim3((unsigned)grid), dim3(256), 0, s, *a); break;
+    case 192: hipLaunchKernelGGL(pa_fp8_generic_lse_reduce_kernel<3>, dim3((unsigned)grid), dim3(256), 0, s, *a); break;
+    case 256: hipLaunchKernelGGL(pa_fp8_generic_lse_reduce_kernel<4>, dim3((unsigned)grid), dim3(256), 0, s, *a); break;
+    default: hipLaunchKernelGGL(pa_fp8_lse_reduce_kernel, dim3((unsigned)grid), dim3(256), 0, s, *a); break;
+  }
   hipError_t err = hipGetLastError();
   return err == hipSuccess ? PA_OK : (int)err;
 }
@@ -3129,12 +3848,14 @@ int pa_fp8_decode_balanced_static(const pa_fp8_stream_args* a, void* stream) {
 int64_t pa_fp8_static_scratch_bytes(void) { return kStaticScratchBytes; }
 
 int pa_fp8_decode_worklist(const pa_fp8_stream_args* a, void* stream) {
-  int rc = check_stream_args(a);
+  int rc = check_stream_args(a, true);
   if (rc != PA_OK) return rc;
   if (!a->work_indptr || !a->work_info || !a->partition_indptr || !a->partial_output || !a->partial_lse)
     return PA_ERR_NULL_ARG;
   if (!aligned16(a->partial_output) || (a->stride_po_row % 4)) return PA_ERR_ALIGN;
   if (a->num_seqs == 0) return PA_OK;
+  if (a->head_size != kHead || a->query_length * a->query_group_size > 64)
+    return generic_worklist(*a, (hipStream_t)stream);
   hipError_t err = dispatch_worklist(*a, (hipStream_t)stream);
   return err == hipSuccess ? PA_OK : (int)err;
 }
@@ -3145,7 +3866,7 @@ int pa_fp8_reduce_worklist(const pa_fp8_worklist_reduce_args* a, void* stream) {
   if (!a->output || !a->partial_output || !a->partial_lse || !a->reduce_indptr || !a->reduce_final_map ||
       !a->reduce_partial_map)
     return PA_ERR_NULL_ARG;
-  if (a->head_size != kHead) return PA_ERR_HEAD_SIZE;
+  if (!generic_head_ok(a->head_size)) return PA_ERR_HEAD_SIZE;
   if (a->num_groups < 0 || a->num_query_heads <= 0 || a->max_query_length <= 0) return PA_ERR_SHAPE;
   if (a->output_dtype != PA_DTYPE_BF16 && a->output_dtype != PA_DTYPE_F16 && a->output_dtype != PA_DTYPE_F32)
     return PA_ERR_DTYPE;
@@ -3155,8 +3876,14 @@ int pa_fp8_reduce_worklist(const pa_fp8_worklist_reduce_args* a, void* stream) {
   const int64_t rows = (int64_t)a->num_groups * a->max_query_length * a->num_query_heads;
   if (rows == 0) return PA_OK;
   if ((rows + 3) / 4 > 0x7fffffffLL) return PA_ERR_SHAPE;
-  hipLaunchKernelGGL(pa_fp8_worklist_reduce_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
-                     (hipStream_t)stream, *a);
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  hipStream_t s = (hipStream_t)stream;
+  switch (a->head_size) {
+    case 64: hipLaunchKernelGGL(pa_fp8_generic_worklist_reduce_kernel<1>, grid, dim3(256), 0, s, *a); break;
+    case 192: hipLaunchKernelGGL(pa_fp8_generic_worklist_reduce_kernel<3>, grid, dim3(256), 0, s, *a); break;
+    case 256: hipLaunchKernelGGL(pa_fp8_generic_worklist_reduce_kernel<4>, grid, dim3(256), 0, s, *a); break;
+    default: hipLaunchKernelGGL(pa_fp8_worklist_reduce_kernel, grid, dim3(256), 0, s, *a); break;
+  }
   hipError_t err = hipGetLastError();
   return err == hipSuccess ? PA_OK : (int)err;
 }

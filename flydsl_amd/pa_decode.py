@@ -233,6 +233,9 @@ def _schedule(route: str, batch: int, kv_heads: int, P: int, eqgs: int, capacity
 # (one wave per 16-column block), up to this many sequences (the in-kernel
 # split scans them in one pass).
 BALANCED_MAX_COLUMNS = 4
+# Head sizes the library decodes (128 on the tuned kernels, the others and
+# more than COOP_MAX_COLUMNS columns per kv head on the generic ones).
+GENERIC_HEAD_SIZES = (64, 128, 192, 256)
 BALANCED_MAX_SEQS = 1024
 # Per-wave streaming decode: one 16-column query block; cooperative beyond.
 STREAM_MAX_COLUMNS = 16
@@ -390,11 +393,13 @@ def prepare_pa_decode(
     head_size = int(query.shape[-1])
     if head_size % 64 != 0:
         raise ValueError(f"Unsupported head_dim={head_size}; must be a multiple of 64.")
-    if head_size != 128:
-        raise NotImplementedError(f"head_dim={head_size} is not built; this library supports head_dim=128.")
+    if head_size not in GENERIC_HEAD_SIZES:
+        raise NotImplementedError(
+            f"head_dim={head_size} is not built; this library supports head_dim in {GENERIC_HEAD_SIZES}.")
     eqgs = query_length * query_group_size
-    if eqgs > 64:
-        raise NotImplementedError(f"query_length * query_group_size = {eqgs} > 64 is not supported.")
+    # head sizes other than 128 and more than 64 query columns per kv head
+    # run on the library's generic kernels: no balanced split for them
+    generic = head_size != 128 or eqgs > COOP_MAX_COLUMNS
     block_size = int(key_cache.shape[-2])
     if tuple(key_cache.shape[2:]) != (head_size // 16, block_size, 16):
         raise ValueError(f"key_cache must be [NB, Hkv, {head_size // 16}, bs, 16], got {tuple(key_cache.shape)}")
@@ -464,7 +469,7 @@ def prepare_pa_decode(
         if max_context_partition_num == 0:
             max_context_partition_num = get_recommended_splits(batch_size, num_kv_heads, split_kv_blocks=1)
         kv_ind = kv_indptr
-        if metadata is not None and eqgs <= COOP_MAX_COLUMNS:
+        if metadata is not None:
             return _prepare_worklist(
                 metadata, output, query, key_cache, value_cache, context_lengths, kv_page_indices, kv_indptr,
                 softmax_scale, key_scale, value_scale, per_token_kv, trans_v, query_input_dtype, output_dtype, s)
@@ -478,7 +483,7 @@ def prepare_pa_decode(
     spw = _schedule(route, batch_size, num_kv_heads, P, eqgs, capacity, _cu_count(dev) if P > 1 else 1)
     owner = spw >= P
     user_partials = exp_sums is not None or max_logits is not None or temporary_output is not None
-    if _balanced_ok(route, batch_size, eqgs, user_partials, owner):
+    if not generic and _balanced_ok(route, batch_size, eqgs, user_partials, owner):
         route_name = "ps_small_block" if route == "small" else "ps_split_reduce"
         sa = _stream_args(output, query, key_cache, value_cache, context_lengths,
                           kv_page_indices if route == "flat" else block_tables, kv_ind, softmax_scale, key_scale,

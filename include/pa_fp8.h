@@ -26,6 +26,13 @@
  *   tmp_out      [B, Hkv, P, ql * gqa, D]   bf16 or float32
  *   output       [B * ql, Hq, D]            bf16, f16 or float32
  * where gqa = Hq / Hkv and P is the number of context slots.
+ *
+ * Head sizes D = 64, 128, 192 and 256 and any ql * gqa are decoded by the
+ * partition, reduce and work-list entry points; D = 128 with up to 64
+ * query columns per kv head runs on the tuned kernels, every other shape on
+ * generic ones (one wave per 16-column block, K and V read straight into
+ * MFMA operands) with the same outputs.  The balanced decode takes D = 128
+ * and up to 64 columns only.
  */
 #ifndef PA_FP8_H
 #define PA_FP8_H
@@ -47,9 +54,9 @@ enum pa_fp8_dtype {
 enum pa_fp8_error {
   PA_OK = 0,
   PA_ERR_NULL_ARG = -1,       /* a required pointer is NULL */
-  PA_ERR_HEAD_SIZE = -2,      /* head_size other than 128 */
+  PA_ERR_HEAD_SIZE = -2,      /* head_size not 64, 128, 192 or 256 (balanced decode: not 128) */
   PA_ERR_BLOCK_SIZE = -3,     /* page size not 16 or a multiple of 32 up to 1024 */
-  PA_ERR_GROUP = -4,          /* ql * gqa outside [1, 64] */
+  PA_ERR_GROUP = -4,          /* balanced decode: ql * gqa above 64 */
   PA_ERR_DTYPE = -5,          /* unsupported query / output / partial dtype */
   PA_ERR_SHAPE = -6,          /* non-positive dimension or partition count */
   PA_ERR_ALIGN = -7,          /* a pointer or stride breaks 16-byte alignment */

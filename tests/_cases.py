@@ -27,6 +27,7 @@ def make_case(
     seed: int = 0,
     extra_pages: int = 4,
     dist: str = "normal",
+    head_size: int = 128,
     device="cpu",
 ) -> dict:
     rng = np.random.default_rng(seed + 17)
@@ -44,6 +45,7 @@ def make_case(
         per_token,
         sliding_window,
         num_blocks=need + extra_pages,
+        head_size=head_size,
     )
     return workloads.build_inputs(cfg, device=device, seed=seed, context_lengths=ctx, dist=dist)
 

@@ -90,7 +90,7 @@ def _launch(case, *, P, out_dtype, tmp_dtype, flat, partials):
         eq = case["query_length"] * (q.shape[1] // hkv)
         es = torch.full((b, hkv, P, eq), 7.0, device=q.device)
         ml = torch.full((b, hkv, P, eq), 7.0, device=q.device)
-        to = torch.full((b, hkv, P, eq, 128), 7.0, device=q.device, dtype=tmp_dtype)
+        to = torch.full((b, hkv, P, eq, q.shape[-1]), 7.0, device=q.device, dtype=tmp_dtype)
         kw.update(exp_sums=es, max_logits=ml, temporary_output=to)
     route = pa_decode_ps_launch(
         out, q, case["key_cache"], case["value_cache"], case["context_lengths"], page_idx, indptr,
@@ -113,7 +113,7 @@ def launch_owner_with_partials(case, P, tmp_dtype=torch.float32):
     out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
     es = torch.full((b, hkv, P, eq), 7.0, device=q.device)
     ml = torch.full((b, hkv, P, eq), 7.0, device=q.device)
-    to = torch.full((b, hkv, P, eq, 128), 7.0, device=q.device, dtype=tmp_dtype)
+    to = torch.full((b, hkv, P, eq, q.shape[-1]), 7.0, device=q.device, dtype=tmp_dtype)
     with schedule("owner"):
         call = prepare_pa_decode(out, q, case["key_cache"], case["value_cache"], case["context_lengths"], None, None,
                                  case["softmax_scale"], case["key_scale"], case["value_scale"],
