@@ -161,3 +161,73 @@ def test_static_scratch_entry_checks_before_any_gpu_call():
     assert lib.pa_fp8_error_string(-9).startswith(b"the call needs more workspace")
     sa.num_seqs = 1025  # the balanced split's batch limit
     assert lib.pa_fp8_decode_balanced_static(ctypes.byref(sa), None) == -6
+
+
+def _stream_stub(head_size, ql, gqa):
+    sa = _lib.StreamArgs()
+    sa.abi_version = _lib.ABI_VERSION
+    for f in ("output", "query", "key_cache", "value_cache", "block_tables", "context_lengths", "key_scale",
+              "value_scale"):
+        setattr(sa, f, 4096)  # aligned stand-ins; nothing is dereferenced on these paths
+    sa.head_size, sa.block_size, sa.num_blocks, sa.max_blocks_per_seq = head_size, 16, 64, 4
+    sa.num_seqs, sa.num_kv_heads, sa.query_length, sa.query_group_size = 2, 2, ql, gqa
+    sa.query_dtype = sa.output_dtype = _lib.DTYPE_BF16
+    sa.stride_q_tok, sa.stride_q_head = 2 * gqa * head_size, head_size
+    sa.stride_out_tok, sa.stride_out_head = sa.stride_q_tok, sa.stride_q_head
+    sa.stride_k_block, sa.stride_k_head = 2 * 16 * head_size, 16 * head_size
+    sa.stride_v_block, sa.stride_v_head = sa.stride_k_block, sa.stride_k_head
+    sa.num_workers = 8
+    return sa
+
+
+def test_head_sizes_and_column_counts_without_gpu():
+    """Head sizes 64 / 128 / 192 / 256 and any ql * gqa pass the partition,
+    reduce and work-list checks (the generic kernels take them); other head
+    sizes are PA_ERR_HEAD_SIZE; the balanced decode keeps D = 128 and <= 64
+    columns.  Every call here stops before a launch."""
+    lib = _lib.load()
+    # balanced: D = 128 and at most 64 columns only
+    assert lib.pa_fp8_decode_balanced(ctypes.byref(_stream_stub(256, 1, 4)), None, 0, None) == -2
+    assert lib.pa_fp8_decode_balanced(ctypes.byref(_stream_stub(128, 8, 16)), None, 0, None) == -4
+    # work list: any of the four head sizes and any column count reach the
+    # work-list pointer check (NULL here)
+    for d, ql, gqa in ((64, 1, 4), (192, 2, 8), (256, 1, 16), (128, 8, 16), (256, 4, 32)):
+        assert lib.pa_fp8_decode_worklist(ctypes.byref(_stream_stub(d, ql, gqa)), None) == -1, (d, ql, gqa)
+    for d in (96, 320, 512):
+        assert lib.pa_fp8_decode_worklist(ctypes.byref(_stream_stub(d, 1, 4)), None) == -2, d
+    # partition: nothing to do for an empty batch once the shape is accepted
+    pa = _lib.PartitionArgs()
+    pa.abi_version = _lib.ABI_VERSION
+    for f in ("query", "key_cache", "value_cache", "block_tables", "context_lengths", "key_scale", "value_scale",
+              "exp_sums", "max_logits", "tmp_out"):
+        setattr(pa, f, 4096)
+    pa.slots_per_workgroup, pa.num_partitions = 1, 3
+    pa.block_size, pa.num_blocks, pa.max_blocks_per_seq = 16, 64, 4
+    pa.num_seqs, pa.num_kv_heads, pa.query_length, pa.query_group_size = 0, 2, 8, 16
+    pa.query_dtype = pa.tmp_dtype = _lib.DTYPE_BF16
+    for d in (64, 128, 192, 256):
+        pa.head_size = d
+        pa.stride_q_tok, pa.stride_q_head = 32 * d, d
+        pa.stride_to_group, pa.stride_to_part = d, 128 * d
+        pa.stride_to_head, pa.stride_to_seq = 3 * 128 * d, 2 * 3 * 128 * d
+        assert lib.pa_fp8_decode_partition(ctypes.byref(pa), None) == 0, d
+    pa.head_size = 96
+    assert lib.pa_fp8_decode_partition(ctypes.byref(pa), None) == -2
+    ra = _lib.ReduceArgs()
+    ra.abi_version = _lib.ABI_VERSION
+    for f in ("output", "exp_sums", "max_logits", "tmp_out"):
+        setattr(ra, f, 4096)
+    ra.num_seqs, ra.num_kv_heads, ra.num_partitions, ra.query_length, ra.query_group_size = 0, 2, 3, 8, 16
+    ra.output_dtype = ra.tmp_dtype = _lib.DTYPE_BF16
+    for d, rc in ((64, 0), (192, 0), (256, 0), (96, -2)):
+        ra.head_size = d
+        assert lib.pa_fp8_decode_reduce(ctypes.byref(ra), None) == rc, d
+    wr = _lib.WorklistReduceArgs()
+    wr.abi_version = _lib.ABI_VERSION
+    for f in ("output", "partial_output", "partial_lse", "reduce_indptr", "reduce_final_map", "reduce_partial_map"):
+        setattr(wr, f, 4096)
+    wr.num_groups, wr.num_query_heads, wr.max_query_length = 0, 32, 8
+    wr.output_dtype = _lib.DTYPE_BF16
+    for d, rc in ((64, 0), (256, 0), (320, -2)):
+        wr.head_size = d
+        assert lib.pa_fp8_reduce_worklist(ctypes.byref(wr), None) == rc, d

@@ -207,3 +207,28 @@ def test_prepared_call_is_freed_without_the_cycle_collector():
         assert ref() is None
     finally:
         gc.enable()
+
+
+@pytest.mark.parametrize("d,ql,hq,hkv", [(64, 1, 8, 2), (256, 2, 16, 4), (128, 8, 32, 2), (192, 1, 64, 1)])
+def test_generic_shapes_take_the_partition_routes(d, ql, hq, hkv):
+    """Head sizes other than 128 and more than 64 columns per kv head are
+    accepted (the library's generic kernels take them) and never use the
+    balanced split, which is built for D = 128 and up to 64 columns."""
+    case = make_case(batch=3, ctx=[ql, 300, 1000], query_length=ql, num_query_heads=hq, num_kv_heads=hkv,
+                     head_size=d, seed=2)
+    call = prep(case)
+    assert call.route == "ps_small_block"
+    assert call._pa is not None and call._pa.head_size == d
+    assert getattr(call, "_sa", None) is None
+    if call._ra is not None:
+        assert call._ra.head_size == d
+    call = prep(case, sliding_window=100)
+    assert call.route in ("ps_sw_partitioned", "ps_sw_fused_partitioned") and call._pa.head_size == d
+
+
+def test_unbuilt_head_size_is_not_implemented():
+    case = make_case(batch=1, ctx=[10], seed=5, head_size=64)
+    c = dict(case)
+    c["query"] = torch.zeros(1, 8, 320, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError, match="head_dim=320"):
+        prep(c, output=torch.empty(1, 8, 320, dtype=torch.bfloat16))

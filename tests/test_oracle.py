@@ -103,6 +103,11 @@ VARIANTS = {
     "page64": dict(block_size=64, ctx_range=(1, 300)),
     "gqa16_ql2": dict(query_length=2, num_query_heads=32, num_kv_heads=2, per_token=True),
     "uniform_dist": dict(dist="uniform"),
+    # the generic kernels' shapes: head sizes other than 128, > 64 columns
+    "d64": dict(head_size=64),
+    "d192_mtp": dict(head_size=192, query_length=2, num_query_heads=8, num_kv_heads=2, per_token=True),
+    "d256_pt": dict(head_size=256, per_token=True),
+    "eq128": dict(query_length=8, num_query_heads=32, num_kv_heads=2, ctx_range=(8, 120)),
 }
 
 
@@ -146,11 +151,11 @@ def test_equal_keys_give_mean_of_values():
         torch.testing.assert_close(out[b], exp, atol=1e-5, rtol=1e-5)
 
 
-@pytest.mark.parametrize("ql,window", [(1, 0), (3, 0), (2, 17)])
-def test_sdpa_library_routine(ql, window):
+@pytest.mark.parametrize("ql,window,d", [(1, 0, 128), (3, 0, 128), (2, 17, 128), (1, 0, 64), (2, 9, 256)])
+def test_sdpa_library_routine(ql, window, d):
     """Each sequence reduces to torch's scaled_dot_product_attention."""
     case = make_case(query_length=ql, num_query_heads=8, num_kv_heads=2, ctx=[ql + 5, 90, 161], seed=5,
-                     sliding_window=window)
+                     sliding_window=window, head_size=d)
     out = torch_oracle(case)
     ks, vs = flat_scales(case)
     for b, ctx in enumerate(case["context_lengths"].tolist()):
@@ -205,11 +210,12 @@ def test_gqa_heads_only_see_their_kv_head():
     assert not torch.equal(out[:, 4:], base[:, 4:])
 
 
-@pytest.mark.parametrize("P,window,ql", [(1, 0, 1), (3, 0, 1), (8, 0, 2), (6, 300, 1), (4, 77, 3)])
-def test_slot_partials_merge_to_full_attention(P, window, ql):
+@pytest.mark.parametrize("P,window,ql,d", [(1, 0, 1, 128), (3, 0, 1, 128), (8, 0, 2, 128), (6, 300, 1, 128),
+                                           (4, 77, 3, 128), (5, 0, 2, 256), (6, 120, 1, 64)])
+def test_slot_partials_merge_to_full_attention(P, window, ql, d):
     """Any slot split, merged by LSE, reproduces the unsplit attention."""
     case = make_case(ctx=[ql, 255, 256, 257, 700, 1100][: 6], query_length=ql, seed=9, sliding_window=window,
-                     per_token=True)
+                     per_token=True, head_size=d)
     if window:
         P = max(P, plan.sw_partition_count(window, query_length=ql))
     es, ml, to = slot_partials(case, P)
