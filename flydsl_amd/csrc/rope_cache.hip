@@ -6,7 +6,9 @@
 //
 // Work decomposition.  A head row (one token, one Q or K head, head_dim D
 // values) is held by D/8 lanes, 8 consecutive values (16 bytes) each, so a
-// wave holds 64/(D/8) rows at a time: rows of Q heads of one token, or one
+// wave holds floor(64/(D/8)) rows at a time (lanes past the last whole row,
+// when D/8 does not divide 64 -- D = 96: 5 rows of 12 lanes -- take no
+// part): rows of Q heads of one token, or one
 // K head's rows of consecutive tokens (which also carry the V rows and the
 // cache writes; see the kernel).  The NeoX partner of value d (d +- D/2)
 // sits in the lane D/16 further along the row and comes over with a lane
@@ -148,6 +150,7 @@ __global__ __launch_bounds__(kRcThreads) void pa_rope_cache_kernel(const pa_fp8_
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rw = lane / lpr;              // row within the wave
+  const bool dead = rw >= rpw;            // past the wave's last whole row
   const int l = lane - rw * lpr;          // lane within the row
   const bool first = l < half;
   const int partner = rw * lpr + (first ? l + half : l - half);
@@ -175,7 +178,7 @@ __global__ __launch_bounds__(kRcThreads) void pa_rope_cache_kernel(const pa_fp8_
       const int row = (int)(u - t * qwpt) * rpw + rw;
       tq[j] = t;
       rq[j] = row;
-      lq[j] = u < qunits && row < QH;
+      lq[j] = u < qunits && row < QH && !dead;
       const uint32_t tc = __builtin_amdgcn_readfirstlane(u < qunits ? t : (uint32_t)T - 1);
       const int rc = row < QH ? row : QH - 1;
       int p = load_index(a.positions, tc, i64);
@@ -206,7 +209,7 @@ __global__ __launch_bounds__(kRcThreads) void pa_rope_cache_kernel(const pa_fp8_
   const int kh = (int)(b - g * KH);
   const int gi = wave * rpw + rw;         // token within the group
   const int tok = (int)g * G + gi;        // this row's token
-  const bool live = tok < T;
+  const bool live = tok < T && !dead;  // a dead lane's gi aliases the next row
   const int d0 = 8 * l;
 
   float krcp = 1.0f, vrcp = 1.0f;
@@ -274,11 +277,13 @@ __global__ __launch_bounds__(kRcThreads) void pa_rope_cache_kernel(const pa_fp8_
   if (LAYOUT == PA_CACHE_FLASH) return;
 
   // value rows -> LDS [token in group][D] (element = 1 or 2 bytes), slots
-  if (SCALE)
-    *(LDS_AS i32x2*)(lds_v + gi * D + d0) = i32x2{(int)v8[0], (int)v8[1]};
-  else
-    *(LDS_AS i32x4*)(lds_v + (gi * D + d0) * 2) = vv;
-  if (l == 0) lds_slot[gi] = cached ? slot : -1;
+  if (!dead) {
+    if (SCALE)
+      *(LDS_AS i32x2*)(lds_v + gi * D + d0) = i32x2{(int)v8[0], (int)v8[1]};
+    else
+      *(LDS_AS i32x4*)(lds_v + (gi * D + d0) * 2) = vv;
+    if (l == 0) lds_slot[gi] = cached ? slot : -1;
+  }
   __syncthreads();
 
   // a 16-token sub-block is written whole when its slots are one page's
@@ -374,8 +379,8 @@ extern "C" int pa_fp8_rope_cache(const pa_fp8_rope_cache_args* a, void* stream) 
       a->max_pos <= 0)
     return PA_ERR_SHAPE;
   const int D = a->head_dim;
-  if (D < 16 || D > 256 || (D & 15)) return PA_ERR_HEAD_SIZE;
-  if (64 % (D >> 3) != 0) return PA_ERR_HEAD_SIZE;  // whole head rows per wave
+  // 8 values per lane, a half row a whole number of lanes, a row in a wave
+  if (D < 16 || D > 512 || (D & 15)) return PA_ERR_HEAD_SIZE;
   if (a->dtype != PA_DTYPE_BF16 && a->dtype != PA_DTYPE_F16) return PA_ERR_DTYPE;
   if (a->cache_layout != PA_CACHE_FLASH && a->cache_layout != PA_CACHE_ATOM && a->cache_layout != PA_CACHE_ATOM_TRANS_V)
     return PA_ERR_SHAPE;

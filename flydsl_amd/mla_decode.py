@@ -33,8 +33,12 @@ V_HEAD_DIM = KV_LORA_RANK  # 512
 BLOCK_TOKENS = 128  # tokens per work-list block (one LDS stage of the kernel)
 
 
+_FNUZ = torch.float8_e4m3fnuz
+
+
 def _is_fp8(dtype: torch.dtype) -> bool:
-    return dtype in (torch.float8_e4m3fn, torch.float8_e4m3fnuz)
+    """The fp8 dtypes the reference's launcher accepts (kernels/mla_fwd_decode.py:52-53)."""
+    return dtype in (torch.float8_e4m3fn, _FNUZ)
 
 
 def _stream_handle(device: torch.device):
@@ -71,7 +75,7 @@ def flydsl_mla_fwd_decode(
     num_heads = query.size(1)
     q_dtype = query.dtype
     kv_dtype = kv_buffer.dtype
-    if not (num_heads == NUM_QO_HEADS and q_dtype == torch.float8_e4m3fn and kv_dtype == torch.float8_e4m3fn):
+    if not (num_heads == NUM_QO_HEADS and _is_fp8(q_dtype) and _is_fp8(kv_dtype)):
         raise NotImplementedError(
             f"flydsl_mla_fwd_decode: unsupported num_heads={num_heads}, q_dtype={q_dtype}, kv_dtype={kv_dtype}"
         )
@@ -119,6 +123,15 @@ def flydsl_mla_fwd_decode(
     assert query.is_contiguous() and kv_buffer.is_contiguous(), "query and kv_buffer must be contiguous"
     if dev.type != "cuda":
         raise RuntimeError("flydsl_mla_fwd_decode: tensors must be on a GPU (the decode runs only in libpa_fp8.so)")
+    # gfx950's matrix cores read OCP e4m3fn only.  float8_e4m3fnuz inputs
+    # (gfx942's format, which the reference's launcher also accepts) are
+    # converted by value: exact for |x| >= 2^-6, smaller magnitudes rounded
+    # to a multiple of 2^-9 (e4m3fn's subnormal step; e4m3fnuz goes to
+    # 2^-10).  A compatibility path: the copy costs a pass over the tensor.
+    if query.dtype == _FNUZ:
+        query = query.to(torch.float32).to(torch.float8_e4m3fn)
+    if kv_buffer.dtype == _FNUZ:
+        kv_buffer = kv_buffer.to(torch.float32).to(torch.float8_e4m3fn)
 
     kv_idx = kv_page_indices.contiguous()
     wi = work_info_set.contiguous().view(-1)

@@ -17,8 +17,9 @@ Layouts (``flash_layout``):
 With ``apply_scale`` the caches are fp8 e4m3fn (torch.float8_e4m3fn or
 uint8) holding value / scale, saturated at +-448.
 
-Differences from the reference, by design: head_dim must be a power of two
-in [16, 256] (the reference also takes 96); positions outside the cos/sin
+Differences from the reference, by design: head_dim must be a multiple of
+16 in [16, 512] (the reference's flash layout also takes other even sizes,
+such as 72, that its atom layouts reject); positions outside the cos/sin
 tables are clamped into them and slots past the cache are skipped instead of
 reading or writing out of bounds; the fp8 path saturates instead of writing
 NaN for values beyond the fp8 range.
@@ -59,8 +60,8 @@ def build_fused_rope_cache_module(
         raise ValueError(f"dtype_str must be 'bf16' or 'f16', got {dtype_str!r}")
     if rotary_dim % 2 != 0:
         raise ValueError(f"rotary_dim must be even, got {rotary_dim}")
-    if head_dim not in (16, 32, 64, 128, 256):
-        raise ValueError(f"head_dim must be a power of two in [16, 256], got {head_dim}")
+    if head_dim % 16 != 0 or not 16 <= head_dim <= 512:
+        raise ValueError(f"head_dim must be a multiple of 16 in [16, 512], got {head_dim}")
     if pos_dtype not in ("i32", "i64"):
         raise ValueError(f"pos_dtype must be 'i32' or 'i64', got {pos_dtype!r}")
     if block_size <= 0:

@@ -360,7 +360,8 @@ int pa_fp8_plan_worklist(const int32_t* context_lengths, int num_seqs, int num_k
  *                            counterpart in the reference writer)
  *     element: the input dtype, or fp8 e4m3fn when apply_scale = 1 (value *
  *     1 / k_scale[0] or 1 / v_scale[0], saturated at +-448)
- * D in {16, 32, 64, 128, 256}.
+ * D a multiple of 16 from 16 to 512 (D = 96, for one, runs 5 rows of 12
+ * lanes per wave).
  */
 enum pa_fp8_cache_layout {
   PA_CACHE_FLASH = 0,

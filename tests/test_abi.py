@@ -58,8 +58,12 @@ def test_null_args_rejected_without_gpu():
     ra.abi_version = 99
     assert lib.pa_fp8_rope_cache(ctypes.byref(ra), None) == -8
     ra.abi_version = _lib.ABI_VERSION
-    ra.head_dim, ra.block_size, ra.max_pos, ra.num_tokens, ra.num_q_heads = 96, 16, 8, 1, 1
-    assert lib.pa_fp8_rope_cache(ctypes.byref(ra), None) == -2  # 12 lanes per row do not tile a wave
+    ra.head_dim, ra.block_size, ra.max_pos, ra.num_tokens, ra.num_q_heads = 72, 16, 8, 1, 1
+    assert lib.pa_fp8_rope_cache(ctypes.byref(ra), None) == -2  # half a row is not a whole number of lanes
+    ra.head_dim = 1024
+    assert lib.pa_fp8_rope_cache(ctypes.byref(ra), None) == -2  # a row beyond one wave
+    ra.head_dim = 96
+    assert lib.pa_fp8_rope_cache(ctypes.byref(ra), None) == -1  # 5 rows of 12 lanes per wave: accepted; no tensors
     ra.head_dim = 128
     assert lib.pa_fp8_rope_cache(ctypes.byref(ra), None) == -1  # no tensors
     ra.num_tokens = 0

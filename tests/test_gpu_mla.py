@@ -80,8 +80,13 @@ def make_case(lens, seed, extra_pages=7, wide=None, nan_page0=False):
     return q, kv, qo_indptr, kv_indptr, kv_indices, last
 
 
-def run(lens, seed=0, num_cu=None, precise=False, **case_kw):
+def run(lens, seed=0, num_cu=None, precise=False, fnuz=False, **case_kw):
     q, kv, qo_indptr, kv_indptr, kv_indices, last = make_case(lens, seed, **case_kw)
+    q_val, kv_val = om.fp8_to_f64(q), om.fp8_to_f64(kv.view(-1, QK_HEAD_DIM))
+    if fnuz:  # the same values as float8_e4m3fnuz tensors (every e4m3fn value below 240 is one)
+        q = q.float().to(torch.float8_e4m3fnuz)
+        kv = kv.float().to(torch.float8_e4m3fnuz)
+        assert np.array_equal(q.to(torch.float64).numpy(), q_val)
     B = len(lens)
     sizes = get_mla_metadata_info_v1(B, 1, 128, FP8, FP8, num_cu=num_cu)
     bufs = [torch.empty(s, dtype=t, device=DEV) for s, t in sizes]
@@ -104,7 +109,7 @@ def run(lens, seed=0, num_cu=None, precise=False, **case_kw):
     mla_reduce_v1(split_o, split_l, reduce_indptr, reduce_final_map, reduce_partial_map, 1, out, final_lse)
     torch.cuda.synchronize()
     meta_h = meta.cpu().numpy()
-    return dict(q=om.fp8_to_f64(q), kv=om.fp8_to_f64(kv.view(-1, QK_HEAD_DIM)), qo=qo_indptr.numpy(),
+    return dict(q=q_val, kv=kv_val, qo=qo_indptr.numpy(),
                 kvp=kv_indptr.numpy(), kvi=kv_indices.numpy(), sm=sm, out=out.float().cpu().numpy(),
                 lse=final_lse.cpu().numpy(), split=[t.cpu() for t in split_snapshot],
                 work_info=work_info.cpu().numpy(), n=int(meta_h[0]), ng=int(meta_h[1]), npart=int(meta_h[2]))
@@ -166,6 +171,12 @@ def test_one_worker_no_splits():
 def test_many_small_pieces():
     # more workers than blocks: every block its own piece, long merges
     check(run([1100, 40], seed=13, num_cu=64))
+
+
+def test_fnuz_inputs():
+    """float8_e4m3fnuz query and kv tensors (accepted, as the reference's
+    launcher accepts them) decode to the oracle's result on their values."""
+    check(run([700, 33, 2000], seed=17, fnuz=True))
 
 
 def test_empty_sequence_writes_zeros():

@@ -144,6 +144,17 @@ def test_fp8_cache(D, T, flash):
     run(T, 8, 1, D, flash=flash, apply_scale=True)
 
 
+@pytest.mark.parametrize("flash", [True, False])
+@pytest.mark.parametrize("apply_scale", [False, True])
+@pytest.mark.parametrize("D", [48, 96, 192, 512])
+def test_head_sizes_whose_rows_do_not_tile_a_wave(D, apply_scale, flash):
+    """D / 8 lanes per row not dividing 64 (48: 6 lanes, 96: 12, 192: 24)
+    leaves lanes past the last whole row idle; 512 is one row per wave.
+    Decode, prefill and scattered slots, with a ragged tail."""
+    for T in (1, 37, 16 * 5 + 3):
+        run(T, 12, 3, D, flash=flash, apply_scale=apply_scale, scattered=T == 37, block_size=16 if flash else 32)
+
+
 @pytest.mark.parametrize("apply_scale", [False, True])
 @pytest.mark.parametrize("block_size", [16, 64])
 def test_scattered_slots_and_decode_value_layout(block_size, apply_scale):

@@ -69,7 +69,7 @@ def _inputs(T, H, D, dtype, reuse, seed=0, max_pos=64):
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 @pytest.mark.parametrize("reuse", [True, False])
-@pytest.mark.parametrize("D", [16, 64, 128])
+@pytest.mark.parametrize("D", [16, 64, 96, 128, 192])
 def test_rotation_matches_bitwise_restatement(dtype, reuse, D):
     x, cos, sin, pos = _inputs(5, 3, D, dtype, reuse, seed=D + reuse)
     got = rc.rope_neox(x, cos[pos.long()], sin[pos.long()], reuse).float().numpy()
