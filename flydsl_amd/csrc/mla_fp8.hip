@@ -10,24 +10,26 @@
 // (5.0 PFLOP/s / 8 TB/s = 625 FLOP/B), so both the matrix cores and HBM
 // must run near their peaks.
 //
-// Work decomposition.  One 256-thread workgroup per worker (grid = number
-// of workers, one per CU); it walks its works (work_indptr / work_info) and
-// each work's kv range in 128-token blocks.  The four waves split the heads
-// (wave w: heads 32w .. 32w+31) and share each block through LDS: wave w
-// DMAs tokens 32w .. 32w+31 of the block (gfx950 global_load_lds, 16 B per
-// lane) into one of two 72 KiB stages while the block before is computed.
+// Work decomposition.  One workgroup per worker (grid = number of workers,
+// one per CU); it walks its works (work_indptr / work_info) and each work's
+// kv range in 128-token blocks.  Eight waves (two per SIMD, so one wave's
+// softmax runs beside the other's matrix products) split the heads (wave w:
+// heads 16w .. 16w+15) and share each block through LDS: wave w DMAs tokens
+// 16w .. 16w+15 of the block (gfx950 global_load_lds, 16 B per lane) into
+// one of two 72 KiB stages while the block before is computed.
 //
-// LDS image of a stage: [4 token groups of 32][36 column units of 16 B]
-// [32 tokens][16 B].  Each DMA instruction of a wave fills two column units
-// of its 32 tokens, so every lane keeps one token (one page index) for the
-// whole block, and both the key reads (16 consecutive tokens of one unit)
-// and the transposed value reads cover whole 256-byte runs.
+// LDS image of a stage: [4 token groups of 32][9 quads of 4 column units]
+// [32 tokens][4 slots of 16 B], the slots XOR-swizzled by token.  Each DMA
+// instruction fills one quad of 16 tokens, so every lane keeps one token
+// (one page index) for the whole block, and both the key reads (16
+// consecutive tokens of one unit) and the transposed value reads cover
+// whole 256-byte runs.
 //
 // Arithmetic, all on v_mfma_scale_f32_16x16x128_f8f6f4 (e4m3fn operands,
 // unit scales):
 //   * S^T = K Q^T per 16-token tile: A = 16 key rows x 128 dims (two 16-byte
-//     LDS reads), B = Q^T of 16 heads, held in registers for the work; 4
-//     latent blocks + 1 rope block (its upper 64 k-slots zero);
+//     LDS reads), B = Q^T of 16 heads, in registers; 4 latent blocks + 1
+//     rope block (the key operand's upper 64 k-slots zero);
 //   * the result lane (c, g) = (l % 16, l / 16) holds tokens 4g .. 4g+3 of
 //     the tile for head c, which is exactly the B-operand slot order the
 //     value product needs: dword T of P^T = the four probabilities of tile T;
@@ -35,7 +37,8 @@
 //     transpose read) gives lane (c, g) four tokens 16T+4g .. 16T+4g+3 of
 //     value dims d0+c (low dword) and d0+16+c (high dword), i.e. the A
 //     operands of two 16-dim row tiles with the same token order as P^T.
-// The O^T accumulators are 32 heads x 512 dims per wave (256 registers).
+// The O^T accumulators are 16 heads x 512 dims per wave (128 AGPRs, the
+// AGPR half of a wave's 256 registers at two waves per SIMD).
 // Softmax is base 2 against a per-head reference exponent m0, set on a
 // work's first block to the head's maximum + 40; the accumulators and the
 // denominator stay in units of 2^m0.  Each half block's probabilities are
@@ -68,13 +71,20 @@ typedef int i32x8 __attribute__((ext_vector_type(8)));
 constexpr int kHeads = 128;
 constexpr int kQkDim = 576;
 constexpr int kVDim = 512;
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
 constexpr int kBlock = MLA_PLAN_BLOCK;       // tokens per LDS stage
 constexpr int kQuadBytes = 32 * 64;         // four column units of a 32-token group
 constexpr int kGroupBytes = 32 * kQkDim;     // one wave's 32 tokens
 constexpr int kStageBytes = kBlock * kQkDim; // 73728
-constexpr int kDmaPerWave = kQkDim / 32;     // 18 instructions of 1 KiB
+// Waves of a workgroup with NHT 16-head tiles per wave: 4 waves of 32 heads
+// (one wave per SIMD, 256 accumulator registers each) or 8 waves of 16 heads
+// (two waves per SIMD, 128 accumulator registers each).
+template <int NHT>
+struct Shape {
+  static_assert(NHT == 1 || NHT == 2, "one or two head tiles per wave");
+  static constexpr int waves = 8 / NHT;
+  static constexpr int threads = 64 * waves;
+  static constexpr int dma = kQkDim / 32 * NHT / 2;  // 1 KiB DMA instructions per wave and block
+};
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.69314718055994531f;
 constexpr float kNegInf = -__builtin_inff();
@@ -82,6 +92,9 @@ constexpr float kNegInf = -__builtin_inff();
 // moves m0 (the e8m0 block scales reach 2^127; accumulators and sums stay
 // far from float overflow).
 constexpr float kRescaleMargin = 64.f;
+#ifndef MLA_HEAD_TILES
+#define MLA_HEAD_TILES 1
+#endif
 
 static_assert(kGroupBytes * 4 == kStageBytes, "four 32-token groups per stage");
 static_assert(kQuadBytes * (kQkDim / 64) == kGroupBytes, "9 quads per group");
@@ -101,31 +114,22 @@ __device__ __forceinline__ void pv_mfma(f32x4& acc, const i32x8& a, const i32x8&
   else
     asm volatile("s_nop 1\n\tv_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4" : "+a"(acc) : "v"(a), "v"(b), "v"(sa), "v"(sb));
 }
-// Key product into logits pinned to VGPRs (first: srcC = 0).  The logits
-// are read by VALU only after logits_settle().
+// Key product into logits in VGPRs (first: srcC = 0).  Compiler builtins,
+// so the scheduler knows the MFMA latency and reads the next key operands
+// from LDS while the products run, and the hazard recognizer covers the
+// operand and result hazards.
 template <bool FIRST>
 __device__ __forceinline__ void qk_mfma(f32x4& acc, const i32x8& a, const i32x8& b) {
-  if (FIRST)
-    asm volatile("s_nop 1\n\tv_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "v"(b));
-  else
-    asm volatile("s_nop 1\n\tv_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+  acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, FIRST ? f32x4{0.f, 0.f, 0.f, 0.f} : acc, 0, 0, 0, 0,
+                                                         0, 0);
 }
-template <bool DUMMY = false>
-__device__ __forceinline__ void qk_rope_mfma(f32x4& acc, const i32x8& a, const i32x8& b, int sa, int sb) {
-  asm volatile("s_nop 1\n\tv_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4" : "+v"(acc) : "v"(a), "v"(b), "v"(sa), "v"(sb));
-}
-// The compiler does not know that the inline-asm MFMAs are MFMAs, so the
-// hazards it would cover are covered here (s_nop n waits n + 1 states):
+// The compiler does not know that the inline-asm MFMAs of the value product
+// are MFMAs, so the hazards it would cover are covered here (s_nop n waits
+// n + 1 states):
 //   * VALU write of an operand -> MFMA read: 2 wait states, the s_nop 1 in
-//     front of every MFMA above;
-//   * MFMA result -> first VALU read: logits_settle() ties the logits to a
-//     24-state wait (as in/out operands, so no read can be scheduled ahead
-//     of it), agpr_settle() does the same before the accumulator reads.
-__device__ __forceinline__ void logits_settle(f32x4 (&s)[4][2]) {
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
-               : "+v"(s[0][0]), "+v"(s[0][1]), "+v"(s[1][0]), "+v"(s[1][1]), "+v"(s[2][0]), "+v"(s[2][1]),
-                 "+v"(s[3][0]), "+v"(s[3][1]));
-}
+//     front of every value-product MFMA;
+//   * MFMA result -> first VALU read: agpr_settle() waits 24 states before
+//     the accumulator reads.
 // Orders the probability packing before the value product.
 template <bool PRECISE>
 __device__ __forceinline__ void probs_ready(i32x8 (&phi)[2], i32x8 (&plo)[2]) {
@@ -133,6 +137,13 @@ __device__ __forceinline__ void probs_ready(i32x8 (&phi)[2], i32x8 (&plo)[2]) {
     asm volatile("" : "+v"(phi[0]), "+v"(phi[1]), "+v"(plo[0]), "+v"(plo[1]));
   else
     asm volatile("" : "+v"(phi[0]), "+v"(phi[1]));
+}
+template <bool PRECISE>
+__device__ __forceinline__ void probs_ready(i32x8 (&phi)[1], i32x8 (&plo)[1]) {
+  if (PRECISE)
+    asm volatile("" : "+v"(phi[0]), "+v"(plo[0]));
+  else
+    asm volatile("" : "+v"(phi[0]));
 }
 // Accumulator tile -> VGPRs through explicit v_accvgpr_read (opaque to the
 // compiler, so the epilogue's scaling cannot be hoisted ahead of its
@@ -149,7 +160,8 @@ __device__ __forceinline__ void agpr_settle() { asm volatile("s_nop 7\n\ts_nop 7
 // two, exact).  The scaled tiles go back to AGPRs; the asm statements that
 // take them as in/out operands keep every write ahead of the next value
 // product, whose MFMAs wait their own two states.
-__device__ __forceinline__ void rescale_acc(f32x4 (&o)[16][2][2], int ht, float f) {
+template <int NHT>
+__device__ __forceinline__ void rescale_acc(f32x4 (&o)[16][2][NHT], int ht, float f) {
   agpr_settle();
 #pragma unroll
   for (int db = 0; db < 16; ++db)
@@ -162,8 +174,18 @@ __device__ __forceinline__ void rescale_acc(f32x4 (&o)[16][2][2], int ht, float 
                    "+a"(o[db + 2][0][ht]), "+a"(o[db + 2][1][ht]), "+a"(o[db + 3][0][ht]), "+a"(o[db + 3][1][ht]));
 }
 
+// 16 bytes per lane from global memory straight into LDS (M0 = the wave's
+// LDS destination, lane l writing 16 l bytes past it), non-temporal.
+// Inline assembly rather than __builtin_amdgcn_global_load_lds: while the
+// builtin's DMA is in flight, the compiler's wait insertion takes every LDS
+// read to be unordered behind it and waits for each with lgkmcnt(0), which
+// serialises the pipelined key reads.  The DMA is awaited explicitly
+// (vmcnt(0) and a barrier before its stage is read).
 __device__ __forceinline__ void lds_dma16(const void* gsrc, LDS_AS void* ldst) {
-  __builtin_amdgcn_global_load_lds(gsrc, ldst, 16, 0, 2);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt"
+               :
+               : "v"(gsrc), "s"((unsigned)(uintptr_t)ldst)
+               : "memory", "m0");
 }
 
 constexpr int vmcnt_only(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | (7 << 4) | (15 << 8); }
@@ -263,57 +285,83 @@ __device__ __forceinline__ void advance(const pa_mla_decode_args& a, Cursor& c, 
   if (++c.wi < we) c.w = load_work(a, c.wi);
 }
 
-// Pages of this lane's two tokens of the wave's 32 (l / 4 and 16 + l / 4)
-// for unit c.
+// Pages of the tokens this lane DMAs for unit c.  Four waves: wave w DMAs
+// the 32-token group w, the lane tokens l / 4 and 16 + l / 4 of it.  Eight
+// waves: wave w DMAs half w % 2 of group w / 2, the lane token
+// 16 (w % 2) + l / 4 (returned twice).
+template <int NHT>
 __device__ __forceinline__ i32x2 unit_pages(const pa_mla_decode_args& a, const Cursor& c, int w) {
   if (c.w.kv1 <= c.w.kv0) return i32x2{0, 0};
-  const int pos = c.w.kv0 + c.blk * kBlock + 32 * w + (lane_id() >> 2);
-  return i32x2{a.kv_page_indices[min(pos, c.w.kv1 - 1)], a.kv_page_indices[min(pos + 16, c.w.kv1 - 1)]};
+  const int last = c.w.kv1 - 1;
+  if constexpr (NHT == 2) {
+    const int pos = c.w.kv0 + c.blk * kBlock + 32 * w + (lane_id() >> 2);
+    return i32x2{a.kv_page_indices[min(pos, last)], a.kv_page_indices[min(pos + 16, last)]};
+  } else {
+    const int pos = c.w.kv0 + c.blk * kBlock + 16 * w + (lane_id() >> 2);
+    const int p = a.kv_page_indices[min(pos, last)];
+    return i32x2{p, p};
+  }
 }
 
-// DMA of one wave's 32 tokens of a block into a stage.  Group layout:
+// DMA of one wave's share of a block into a stage.  Group layout:
 // [9 quads of 4 column units][32 tokens][4 slots of 16 B]; slot s of token t
-// holds unit 4q + (s ^ swz(t)), swz(t) = ((t >> 2) ^ (t >> 3 & 2)) & 3: an
-// XOR swizzle that spreads the 16 rows of a key read and the 8 rows (two
-// tiles) of a transpose read over distinct bank groups.  Instruction n fills quad n / 2 for tokens
-// 16 (n % 2) .. +15: each lane reads 16 B and four lanes read 64
-// consecutive bytes of one row.
+// holds unit 4q + (s ^ swz(t)), swz(t) = (t >> 4 & 1) | (t >> 2 & 1) << 1:
+// an XOR swizzle under which both the key reads (ds_read_b128, 16 rows of
+// one unit) and the value transpose reads (ds_read_b64_tr_b8) run at the
+// full LDS rate on gfx950 (measured against every XOR swizzle of the token
+// bits; the lane grouping of a 16-byte read is not that of 16 consecutive
+// lanes, and simpler swizzles cost a 2-way bank conflict).  Instruction n of a
+// group fills quad n / 2 for tokens 16 (n % 2) .. +15: each lane reads 16 B
+// and four lanes read 64 consecutive bytes of one row.  Four waves: wave w
+// issues the 18 instructions of group w; eight waves: wave w issues the 9
+// instructions n = 2k + w % 2 of group w / 2.
+template <int NHT>
 __device__ __forceinline__ void issue_block(const pa_mla_decode_args& a, LDS_AS unsigned char* stage, int w,
                                            i32x2 pages) {
   const int np = (int)(a.num_pages - 1);
   const int l = lane_id();
-  const int sx0 = (l & 3) ^ ((l >> 4) & 3);  // tokens l / 4:      swz = (l >> 4) & 3
-  const int sx1 = sx0 ^ 2;                   // tokens 16 + l / 4: swz ^ 2
+  const int sx0 = (l & 3) ^ (((l >> 4) & 1) << 1);  // tokens l / 4:      swz = 2 (l / 16 % 2)
   const unsigned char* kvb = (const unsigned char*)a.kv_buffer;
-  const unsigned char* src0 = kvb + (int64_t)min(max(pages[0], 0), np) * kQkDim + 16 * sx0;
-  const unsigned char* src1 = kvb + (int64_t)min(max(pages[1], 0), np) * kQkDim + 16 * sx1;
-  LDS_AS unsigned char* dst = stage + w * kGroupBytes;
+  if constexpr (NHT == 2) {
+    const int sx1 = sx0 ^ 1;  // tokens 16 + l / 4: swz ^ 1
+    const unsigned char* src0 = kvb + (int64_t)min(max(pages[0], 0), np) * kQkDim + 16 * sx0;
+    const unsigned char* src1 = kvb + (int64_t)min(max(pages[1], 0), np) * kQkDim + 16 * sx1;
+    LDS_AS unsigned char* dst = stage + w * kGroupBytes;
 #pragma unroll
-  for (int n = 0; n < kDmaPerWave; ++n) lds_dma16(((n & 1) ? src1 : src0) + 64 * (n >> 1), dst + 1024 * n);
+    for (int n = 0; n < Shape<NHT>::dma; ++n) lds_dma16(((n & 1) ? src1 : src0) + 64 * (n >> 1), dst + 1024 * n);
+  } else {
+    const int hf = w & 1;
+    const unsigned char* src = kvb + (int64_t)min(max(pages[0], 0), np) * kQkDim + 16 * (sx0 ^ hf);
+    LDS_AS unsigned char* dst = stage + (w >> 1) * kGroupBytes + 1024 * hf;
+#pragma unroll
+    for (int k = 0; k < Shape<NHT>::dma; ++k) lds_dma16(src + 64 * k, dst + 2048 * k);
+  }
 }
 
-// Q^T B operands of the wave's two 16-head tiles for query row qo: slot
-// order per latent block kb: 16 dims at 128kb + 16g, then 16 at
-// 128kb + 64 + 16g; the rope block's 16 dims 512 + 16g sit in both halves
-// of its operand (with the key's rope dims likewise doubled and a B scale
-// of 1/2, which is exact).
+// Q^T B operands of the wave's 16-head tiles for query row qo: slot order
+// per latent block kb: 16 dims at 128kb + 16g, then 16 at 128kb + 64 + 16g;
+// the rope block's 16 dims 512 + 16g sit in both halves of its operand (the
+// key operand's high half is zero, so the copy adds nothing).
+template <int NHT>
 struct QTile {
-  i32x8 b[2][4];  // latent blocks
-  i32x4 r[2];     // rope dims 512 + 16g .. +15
+  i32x8 b[NHT][4];  // latent blocks
+  i32x8 r[NHT];     // rope dims 512 + 16g .. +15, twice
 };
 
-__device__ __forceinline__ void load_query(const pa_mla_decode_args& a, int qo, int w, int c, int g, QTile& q) {
+template <int NHT>
+__device__ __forceinline__ void load_query(const pa_mla_decode_args& a, int qo, int w, int c, int g, QTile<NHT>& q) {
 #pragma unroll
-  for (int ht = 0; ht < 2; ++ht) {
+  for (int ht = 0; ht < NHT; ++ht) {
     const unsigned char* row =
-        (const unsigned char*)a.query + ((int64_t)qo * kHeads + 32 * w + 16 * ht + c) * kQkDim + 16 * g;
+        (const unsigned char*)a.query + ((int64_t)qo * kHeads + 16 * NHT * w + 16 * ht + c) * kQkDim + 16 * g;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       const i32x4 lo = *(const i32x4*)(row + 128 * kb);
       const i32x4 hi = *(const i32x4*)(row + 128 * kb + 64);
       q.b[ht][kb] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
-    q.r[ht] = *(const i32x4*)(row + 512);
+    const i32x4 r = *(const i32x4*)(row + 512);
+    q.r[ht] = i32x8{r[0], r[1], r[2], r[3], r[0], r[1], r[2], r[3]};
   }
 }
 
@@ -345,14 +393,14 @@ __device__ __forceinline__ i32x8 read_tr_operand(const unsigned (&base)[4]) {
 // dims, eight transpose reads give the A operands of two 16-dim row tiles.
 // Software pipelined by hand: the reads of block db + 1 are issued before
 // the MFMAs of block db, which wait only for their own eight reads.
-template <bool FIRST, bool PRECISE>
-__device__ __forceinline__ void pv_block(const LDS_AS unsigned char* sb, f32x4 (&o)[16][2][2], const i32x8 (&phi)[2],
-                                         const i32x8 (&plo)[2], const int (&sbs)[2], const int (&sbl)[2], int sa,
-                                         int vbase) {
+template <bool FIRST, bool PRECISE, int NHT>
+__device__ __forceinline__ void pv_block(const LDS_AS unsigned char* sb, f32x4 (&o)[16][2][NHT],
+                                         const i32x8 (&phi)[NHT], const i32x8 (&plo)[NHT], const int (&sbs)[NHT],
+                                         const int (&sbl)[NHT], int sa, int vbase) {
   // unit u = 2db + rt sits in quad u / 4, slot (u % 4) ^ swz of the lane's
-  // rows 16(c / 8) + 4g + ..: swz = g ^ 2(c / 8)
+  // row 16(c / 8) + 4g + ..: swz = c / 8 + 2 (g % 2)
   const int l = lane_id();
-  const int g = (l >> 4) ^ (((l >> 3) & 1) << 1);
+  const int g = ((l >> 3) & 1) | (((l >> 4) & 1) << 1);
   unsigned base[4][4];
 #pragma unroll
   for (int sl = 0; sl < 4; ++sl)
@@ -375,7 +423,7 @@ __device__ __forceinline__ void pv_block(const LDS_AS unsigned char* sb, f32x4 (
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
 #pragma unroll
-    for (int ht = 0; ht < 2; ++ht)
+    for (int ht = 0; ht < NHT; ++ht)
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
         pv_mfma<FIRST>(o[db][rt][ht], va[db & 1][rt], phi[ht], sa, sbs[ht]);
@@ -384,8 +432,8 @@ __device__ __forceinline__ void pv_block(const LDS_AS unsigned char* sb, f32x4 (
   });
 }
 
-template <bool PRECISE>
-__global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_mla_decode_args a) {
+template <bool PRECISE, int NHT>
+__global__ __launch_bounds__(Shape<NHT>::threads, 1) void mla_fp8_decode_kernel(const pa_mla_decode_args a) {
   __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[2 * kStageBytes];
   LDS_AS unsigned char* lds = (LDS_AS unsigned char*)lds_raw;
 
@@ -412,35 +460,42 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
   Cursor c2 = c1;
   advance(a, c2, we);
 
-  QTile q;
+  QTile<NHT> q;
   load_query(a, cur.w.qo, w, c, g, q);
-  issue_block(a, lds, w, unit_pages(a, cur, w));
-  i32x2 pg1 = valid(c1, we) ? unit_pages(a, c1, w) : i32x2{0, 0};
+  issue_block<NHT>(a, lds, w, unit_pages<NHT>(a, cur, w));
+  i32x2 pg1 = valid(c1, we) ? unit_pages<NHT>(a, c1, w) : i32x2{0, 0};
 
   // O^T accumulators: [32-dim block][16-dim row tile][head tile].
-  f32x4 o[16][2][2];
-  float m0[2] = {0.f, 0.f};      // reference exponent of each head (set on a work's first block)
-  float lsum[2] = {0.f, 0.f};    // this lane's share of the denominator, in units of 2^m0
+  f32x4 o[16][2][NHT];
+  float m0[NHT], lsum[NHT];
+#pragma unroll
+  for (int ht = 0; ht < NHT; ++ht) {
+    m0[ht] = 0.f;    // reference exponent of each head (set on a work's first block)
+    lsum[ht] = 0.f;  // this lane's share of the denominator, in units of 2^m0
+  }
 
   // Lane bases inside a stage.  Keys: token row 16T + c, unit 8kb + g
   // (+4 for the upper 64 dims).  Values (transpose reads): lanes c < 8
   // address tile 2k, lanes c >= 8 tile 2k+1, row 4g + (c / 2) % 4 of the
   // tile, unit 2db + rt, byte 8 (c % 2); the low dword then holds tile 2k
   // and the high dword tile 2k+1 of value dim 32db + 16rt + c.
-  // key rows 16(T % 2) + c: swz = (c / 4) ^ 2(T % 2)
-  const int kbase0 = c * 64 + 16 * (g ^ ((c >> 2) & 3));
-  const int kbase1 = c * 64 + 16 * (g ^ ((c >> 2) & 3) ^ 2);
+  // key rows 16(T % 2) + c: swz = T % 2 + 2 (c / 4 % 2)
+  const int kbase0 = c * 64 + 16 * (g ^ (((c >> 2) & 1) << 1));
+  const int kbase1 = c * 64 + 16 * (g ^ (((c >> 2) & 1) << 1) ^ 1);
   const int vbase = (16 * (c >> 3) + 4 * g + ((c >> 1) & 3)) * 64 + (c & 1) * 8;
   const int unit_scale = 127;  // e8m0 2^0
-  const int half_scale = 126;  // e8m0 2^-1
 
   int st = 0;
   while (true) {
-    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    // vmcnt(0): this block's DMA (and the queries) have landed; lgkmcnt(0)
+    // as a builtin also tells the compiler's wait insertion that no scalar
+    // load is outstanding, so the key reads below are awaited by count
+    // rather than with lgkmcnt(0).
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0) & ~(15 << 8));
     asm volatile("s_barrier" ::: "memory");
     if (valid(c1, we)) {
-      issue_block(a, lds + (st ^ 1) * kStageBytes, w, pg1);
-      if (valid(c2, we)) pg1 = unit_pages(a, c2, w);
+      issue_block<NHT>(a, lds + (st ^ 1) * kStageBytes, w, pg1);
+      if (valid(c2, we)) pg1 = unit_pages<NHT>(a, c2, w);
     }
     const LDS_AS unsigned char* sb = lds + st * kStageBytes;
 
@@ -456,57 +511,64 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
     const bool first = cur.blk == 0;
     const bool last = cur.blk == cur.w.nblk - 1;
     const int len = cur.w.kv1 - cur.w.kv0 - cur.blk * kBlock;  // valid tokens from this block on
-    i32x8 phi[2], plo[2];
-    int kexp[2][2];  // [half][head tile]: block exponent - m0
+    i32x8 phi[NHT], plo[NHT];
+    int kexp[2][NHT];  // [half][head tile]: block exponent - m0
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      f32x4 s[4][2];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
+      f32x4 s[4][NHT];
+      // Key operand of product j = 5t + kb of the half block: tile
+      // T = 4 half + t, latent block kb < 4 (two 16-byte reads), or kb = 4:
+      // the rope dims in the low half, zeros in the high half.
+      auto key_operand = [&](auto jc, i32x8& dst) {
+        constexpr int j = decltype(jc)::value, t = j / 5, kb = j % 5;
         const int T = 4 * half + t;
         const LDS_AS unsigned char* kr = sb + (T >> 1) * kGroupBytes + (T & 1) * 1024 + ((T & 1) ? kbase1 : kbase0);
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
+        if constexpr (kb < 4) {
           const i32x4 lo = *(const LDS_AS i32x4*)(kr + 2 * kb * kQuadBytes);
           const i32x4 hi = *(const LDS_AS i32x4*)(kr + (2 * kb + 1) * kQuadBytes);
-          const i32x8 ka = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          if (kb == 0) {
-            qk_mfma<true>(s[t][0], ka, q.b[0][kb]);
-            qk_mfma<true>(s[t][1], ka, q.b[1][kb]);
-          } else {
-            qk_mfma<false>(s[t][0], ka, q.b[0][kb]);
-            qk_mfma<false>(s[t][1], ka, q.b[1][kb]);
-          }
+          dst = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        } else {
+          const i32x4 r4 = *(const LDS_AS i32x4*)(kr + 8 * kQuadBytes);
+          dst = i32x8{r4[0], r4[1], r4[2], r4[3], 0, 0, 0, 0};
         }
-        // rope: both operands carry the 16 dims twice; the B scale 2^-1
-        // undoes the doubling exactly
-        const i32x4 kr4 = *(const LDS_AS i32x4*)(kr + 8 * kQuadBytes);
-        const i32x8 ka = {kr4[0], kr4[1], kr4[2], kr4[3], kr4[0], kr4[1], kr4[2], kr4[3]};
+      };
+      // Software pipeline: the reads of product j + 2 are issued before
+      // product j (the scheduling barriers keep that order; the compiler's
+      // own schedule reads each operand just before its product and waits).
+      i32x8 kq[3];
+      key_operand(std::integral_constant<int, 0>{}, kq[0]);
+      key_operand(std::integral_constant<int, 1>{}, kq[1]);
+      static_for<20>([&](auto jc) {
+        constexpr int j = decltype(jc)::value, t = j / 5, kb = j % 5;
+        if constexpr (j + 2 < 20) key_operand(std::integral_constant<int, j + 2>{}, kq[(j + 2) % 3]);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int ht = 0; ht < 2; ++ht) {
-          const i32x8 qb = {q.r[ht][0], q.r[ht][1], q.r[ht][2], q.r[ht][3],
-                            q.r[ht][0], q.r[ht][1], q.r[ht][2], q.r[ht][3]};
-          qk_rope_mfma(s[t][ht], ka, qb, unit_scale, half_scale);
+        for (int ht = 0; ht < NHT; ++ht) {
+          if constexpr (kb == 0)
+            qk_mfma<true>(s[t][ht], kq[j % 3], q.b[ht][0]);
+          else if constexpr (kb < 4)
+            qk_mfma<false>(s[t][ht], kq[j % 3], q.b[ht][kb]);
+          else
+            qk_mfma<false>(s[t][ht], kq[j % 3], q.r[ht]);
         }
-      }
-      logits_settle(s);
+        __builtin_amdgcn_sched_barrier(0);
+      });
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        s[t][0] *= scale2;
-        s[t][1] *= scale2;
-      }
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int ht = 0; ht < NHT; ++ht) s[t][ht] *= scale2;
       if (len < (half + 1) * (kBlock / 2)) {
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const bool keep = 16 * (4 * half + t) + 4 * g + i < len;
-            s[t][0][i] = keep ? s[t][0][i] : kNegInf;
-            s[t][1][i] = keep ? s[t][1][i] : kNegInf;
+#pragma unroll
+            for (int ht = 0; ht < NHT; ++ht) s[t][ht][i] = keep ? s[t][ht][i] : kNegInf;
           }
       }
 #pragma unroll
-      for (int ht = 0; ht < 2; ++ht) {
+      for (int ht = 0; ht < NHT; ++ht) {
         float x = kNegInf;
 #pragma unroll
         for (int t = 0; t < 4; ++t) x = fmaxf(x, fmaxf(fmaxf(s[t][ht][0], s[t][ht][1]), fmaxf(s[t][ht][2], s[t][ht][3])));
@@ -552,9 +614,9 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
     }
     // Scale VGPR of lane group g = exponent of block g: (half 0, pair {0,1}),
     // (half 0, pair {2,3}), (half 1, pair {0,1}), (half 1, pair {2,3}).
-    int sbv[2][2];  // [hi, lo term][head tile]
+    int sbv[2][NHT];  // [hi, lo term][head tile]
 #pragma unroll
-    for (int ht = 0; ht < 2; ++ht) {
+    for (int ht = 0; ht < NHT; ++ht) {
       const int t0 = other_half_wave(kexp[0][ht]);  // group 1 <- group 3
       const int t1 = other_half_wave(kexp[1][ht]);  // group 2 <- group 0
       const int k = g == 0 ? kexp[0][ht] : g == 1 ? t0 : g == 2 ? t1 : kexp[1][ht];
@@ -566,9 +628,9 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
     // ---- O^T += V^T P^T: 16 blocks of 32 value dims ----
     probs_ready<PRECISE>(phi, plo);
     if (first)
-      pv_block<true, PRECISE>(sb, o, phi, plo, sbv[0], sbv[1], unit_scale, vbase);
+      pv_block<true, PRECISE, NHT>(sb, o, phi, plo, sbv[0], sbv[1], unit_scale, vbase);
     else
-      pv_block<false, PRECISE>(sb, o, phi, plo, sbv[0], sbv[1], unit_scale, vbase);
+      pv_block<false, PRECISE, NHT>(sb, o, phi, plo, sbv[0], sbv[1], unit_scale, vbase);
 
     if (last) {
       // ---- epilogue: normalise and store the work's rows ----
@@ -577,13 +639,15 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
       agpr_settle();
       const bool direct = cur.w.pql < 0;
 #pragma unroll
-      for (int ht = 0; ht < 2; ++ht) {
+      for (int ht = 0; ht < NHT; ++ht) {
         const float l = sum_over_groups(lsum[ht]);
         const float inv = l > 0.f ? 1.f / l : 0.f;
-        const int head = 32 * w + 16 * ht + c;
+        const int head = 16 * NHT * w + 16 * ht + c;
         const int64_t prow = direct ? (int64_t)cur.w.qo * kHeads + head : (int64_t)cur.w.pql * kHeads + head;
-        unsigned char* orow = direct ? (unsigned char*)a.final_output + prow * (kVDim * 2)
-                                     : (unsigned char*)(a.split_output + prow * kVDim);
+        // the lane's value dims 4g .. 4g+3 of each 16-dim tile: one pointer,
+        // constant offsets per tile
+        unsigned char* lrow = direct ? (unsigned char*)a.final_output + prow * (kVDim * 2) + 8 * g
+                                     : (unsigned char*)(a.split_output + prow * kVDim) + 16 * g;
 #pragma unroll
         for (int db = 0; db < 16; ++db)
 #pragma unroll
@@ -592,13 +656,13 @@ __global__ __launch_bounds__(kThreads, 1) void mla_fp8_decode_kernel(const pa_ml
             // an empty range (l = 0) stores zeros whatever its page held
 #pragma unroll
             for (int i = 0; i < 4; ++i) v[i] = l > 0.f ? v[i] : 0.f;
-            const int d = 32 * db + 16 * rt + 4 * g;
+            const int d0 = 32 * db + 16 * rt;
             if (direct) {
               const uint32_t lo = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
               const uint32_t hi = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
-              *(i32x2*)(orow + 2 * d) = i32x2{(int)lo, (int)hi};
+              *(i32x2*)(lrow + 2 * d0) = i32x2{(int)lo, (int)hi};
             } else {
-              *(f32x4*)(orow + 4 * d) = v;
+              *(f32x4*)(lrow + 4 * d0) = v;
             }
             __builtin_amdgcn_sched_barrier(0);
           }
@@ -690,10 +754,13 @@ extern "C" int pa_fp8_mla_decode(const pa_mla_decode_args* a, void* stream) {
       (a->split_output && !aligned16(a->split_output)))
     return PA_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
+  constexpr int kNht = MLA_HEAD_TILES;
   if (a->precise_p)
-    hipLaunchKernelGGL(mla_fp8_decode_kernel<true>, dim3(a->num_workers), dim3(kThreads), 0, s, *a);
+    hipLaunchKernelGGL((mla_fp8_decode_kernel<true, kNht>), dim3(a->num_workers), dim3(Shape<kNht>::threads), 0, s,
+                       *a);
   else
-    hipLaunchKernelGGL(mla_fp8_decode_kernel<false>, dim3(a->num_workers), dim3(kThreads), 0, s, *a);
+    hipLaunchKernelGGL((mla_fp8_decode_kernel<false, kNht>), dim3(a->num_workers), dim3(Shape<kNht>::threads), 0, s,
+                       *a);
   return (int)hipGetLastError();
 }
 
