@@ -175,14 +175,18 @@ __device__ __forceinline__ void rescale_acc(f32x4 (&o)[16][2][NHT], int ht, floa
 }
 
 // 16 bytes per lane from global memory straight into LDS (M0 = the wave's
-// LDS destination, lane l writing 16 l bytes past it), non-temporal.
+// LDS destination, lane l writing 16 l bytes past it), with the default
+// cache policy: a 576-byte row is read as nine 64-byte pieces by nine
+// instructions, and keeping the 128-byte lines in L2 lets the second piece
+// of each line hit there (measured: the non-temporal hint makes this DMA
+// pattern about 10% slower).
 // Inline assembly rather than __builtin_amdgcn_global_load_lds: while the
 // builtin's DMA is in flight, the compiler's wait insertion takes every LDS
 // read to be unordered behind it and waits for each with lgkmcnt(0), which
 // serialises the pipelined key reads.  The DMA is awaited explicitly
 // (vmcnt(0) and a barrier before its stage is read).
 __device__ __forceinline__ void lds_dma16(const void* gsrc, LDS_AS void* ldst) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt"
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
                :
                : "v"(gsrc), "s"((unsigned)(uintptr_t)ldst)
                : "memory", "m0");
@@ -363,6 +367,17 @@ __device__ __forceinline__ void load_query(const pa_mla_decode_args& a, int qo, 
     const i32x4 r = *(const i32x4*)(row + 512);
     q.r[ht] = i32x8{r[0], r[1], r[2], r[3], r[0], r[1], r[2], r[3]};
   }
+  // A negative softmax scale: the queries' signs are flipped (exact in
+  // fp8) and the kernel scales by |softmax_scale|, so the softmax can take
+  // its maxima on the raw logits.
+  if (a.softmax_scale < 0.f) {
+#pragma unroll
+    for (int ht = 0; ht < NHT; ++ht) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) q.b[ht][kb] ^= (int)0x80808080u;
+      q.r[ht] ^= (int)0x80808080u;
+    }
+  }
 }
 
 // ds_read_b64_tr_b8 as inline assembly: the compiler's own intrinsic makes it
@@ -447,7 +462,7 @@ __global__ __launch_bounds__(Shape<NHT>::threads, 1) void mla_fp8_decode_kernel(
   we = min(max(we, ws), a.num_works);
   if (ws >= we) return;
 
-  const float scale2 = a.softmax_scale * kLog2e;
+  const float scale2 = __builtin_fabsf(a.softmax_scale) * kLog2e;  // the query signs carry a negative scale's
 
   // Unit cursors: cur (computed now), c1 (DMA issued this step), c2 (page
   // index prefetched this step).
@@ -512,51 +527,42 @@ __global__ __launch_bounds__(Shape<NHT>::threads, 1) void mla_fp8_decode_kernel(
     const bool last = cur.blk == cur.w.nblk - 1;
     const int len = cur.w.kv1 - cur.w.kv0 - cur.blk * kBlock;  // valid tokens from this block on
     i32x8 phi[NHT], plo[NHT];
-    int kexp[2][NHT];  // [half][head tile]: block exponent - m0
+    int kexp[2][NHT];     // [half][head tile]: block exponent - m0
+    float hmax[2][NHT];   // [half][head tile]: the head's maximum raw logit
+    float bexp[2][NHT];   // [half][head tile]: block exponent e of the lane pair
+    float psum[2][NHT];   // [half][head tile]: the lane's sum of p = 2^(x - e)
+    f32x4 s0[4][NHT], s1[4][NHT];
+
+    // Key operand of product j = 5t + kb of a half block: tile
+    // T = 4 half + t, latent block kb < 4 (two 16-byte reads), or kb = 4:
+    // the rope dims in the low half, zeros in the high half.
+    auto key_operand = [&](auto jc, int half, i32x8& dst) {
+      constexpr int j = decltype(jc)::value, t = j / 5, kb = j % 5;
+      const int T = 4 * half + t;
+      const LDS_AS unsigned char* kr = sb + (T >> 1) * kGroupBytes + (T & 1) * 1024 + ((T & 1) ? kbase1 : kbase0);
+      if constexpr (kb < 4) {
+        const i32x4 lo = *(const LDS_AS i32x4*)(kr + 2 * kb * kQuadBytes);
+        const i32x4 hi = *(const LDS_AS i32x4*)(kr + (2 * kb + 1) * kQuadBytes);
+        dst = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      } else {
+        const i32x4 r4 = *(const LDS_AS i32x4*)(kr + 8 * kQuadBytes);
+        dst = i32x8{r4[0], r4[1], r4[2], r4[3], 0, 0, 0, 0};
+      }
+    };
+    auto key_product = [&](auto jc, f32x4 (&s)[4][NHT], const i32x8& ka) {
+      constexpr int j = decltype(jc)::value, t = j / 5, kb = j % 5;
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      f32x4 s[4][NHT];
-      // Key operand of product j = 5t + kb of the half block: tile
-      // T = 4 half + t, latent block kb < 4 (two 16-byte reads), or kb = 4:
-      // the rope dims in the low half, zeros in the high half.
-      auto key_operand = [&](auto jc, i32x8& dst) {
-        constexpr int j = decltype(jc)::value, t = j / 5, kb = j % 5;
-        const int T = 4 * half + t;
-        const LDS_AS unsigned char* kr = sb + (T >> 1) * kGroupBytes + (T & 1) * 1024 + ((T & 1) ? kbase1 : kbase0);
-        if constexpr (kb < 4) {
-          const i32x4 lo = *(const LDS_AS i32x4*)(kr + 2 * kb * kQuadBytes);
-          const i32x4 hi = *(const LDS_AS i32x4*)(kr + (2 * kb + 1) * kQuadBytes);
-          dst = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        } else {
-          const i32x4 r4 = *(const LDS_AS i32x4*)(kr + 8 * kQuadBytes);
-          dst = i32x8{r4[0], r4[1], r4[2], r4[3], 0, 0, 0, 0};
-        }
-      };
-      // Software pipeline: the reads of product j + 2 are issued before
-      // product j (the scheduling barriers keep that order; the compiler's
-      // own schedule reads each operand just before its product and waits).
-      i32x8 kq[3];
-      key_operand(std::integral_constant<int, 0>{}, kq[0]);
-      key_operand(std::integral_constant<int, 1>{}, kq[1]);
-      static_for<20>([&](auto jc) {
-        constexpr int j = decltype(jc)::value, t = j / 5, kb = j % 5;
-        if constexpr (j + 2 < 20) key_operand(std::integral_constant<int, j + 2>{}, kq[(j + 2) % 3]);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int ht = 0; ht < NHT; ++ht) {
-          if constexpr (kb == 0)
-            qk_mfma<true>(s[t][ht], kq[j % 3], q.b[ht][0]);
-          else if constexpr (kb < 4)
-            qk_mfma<false>(s[t][ht], kq[j % 3], q.b[ht][kb]);
-          else
-            qk_mfma<false>(s[t][ht], kq[j % 3], q.r[ht]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      });
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int ht = 0; ht < NHT; ++ht) s[t][ht] *= scale2;
+      for (int ht = 0; ht < NHT; ++ht) {
+        if constexpr (kb == 0)
+          qk_mfma<true>(s[t][ht], ka, q.b[ht][0]);
+        else if constexpr (kb < 4)
+          qk_mfma<false>(s[t][ht], ka, q.b[ht][kb]);
+        else
+          qk_mfma<false>(s[t][ht], ka, q.r[ht]);
+      }
+    };
+    // Logits of positions past the range -> -inf (only a work's last block).
+    auto mask = [&](f32x4 (&s)[4][NHT], int half) {
       if (len < (half + 1) * (kBlock / 2)) {
 #pragma unroll
         for (int t = 0; t < 4; ++t)
@@ -567,35 +573,27 @@ __global__ __launch_bounds__(Shape<NHT>::threads, 1) void mla_fp8_decode_kernel(
             for (int ht = 0; ht < NHT; ++ht) s[t][ht][i] = keep ? s[t][ht][i] : kNegInf;
           }
       }
+    };
+    // Softmax, branch-free part: maxima of the raw logits (the scale is
+    // positive), the lane pair's block exponent e = ceil(scaled pair max),
+    // p = 2^(x scale - e) packed to fp8, and the lane's sum of p.
+    auto softmax_probs = [&](const f32x4 (&s)[4][NHT], int half) {
 #pragma unroll
       for (int ht = 0; ht < NHT; ++ht) {
         float x = kNegInf;
 #pragma unroll
         for (int t = 0; t < 4; ++t) x = fmaxf(x, fmaxf(fmaxf(s[t][ht][0], s[t][ht][1]), fmaxf(s[t][ht][2], s[t][ht][3])));
-        const float hm = max_over_groups(x);  // the head's maximum over this half block
-        if (half == 0 && first) m0[ht] = hm == kNegInf ? 0.f : __builtin_ceilf(hm) + 40.f;
-        const bool up = hm > m0[ht] + kRescaleMargin;
-        if (__builtin_expect(__ballot(up) != 0, 0)) {
-          // move m0: the denominator, the first half's block exponents and
-          // (past the work's first block) the accumulators follow it
-          const float mn = up ? __builtin_ceilf(hm) + 40.f : m0[ht];
-          const float f = __builtin_amdgcn_exp2f(m0[ht] - mn);
-          lsum[ht] *= f;
-          if (half == 1) kexp[0][ht] = max(kexp[0][ht] + (int)(m0[ht] - mn), -127);
-          m0[ht] = mn;
-          if (!first) rescale_acc(o, ht, f);
-        }
+        hmax[half][ht] = max_over_groups(x);
         const float xp = max_over_pair(x);
-        // exponents beyond m0 +- 127 leave the e8m0 range
-        const float eh = fminf(fmaxf(xp == kNegInf ? m0[ht] : __builtin_ceilf(xp), m0[ht] - 127.f), m0[ht] + 127.f);
-        kexp[half][ht] = (int)(eh - m0[ht]);
+        const float e = xp == kNegInf ? 0.f : __builtin_ceilf(xp * scale2);
+        bexp[half][ht] = e;
         float acc = 0.f;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           float pv[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            pv[i] = __builtin_amdgcn_exp2f(s[t][ht][i] - eh);
+            pv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][ht][i], scale2, -e));
             acc += pv[i];
           }
           const uint32_t h = pack4_fp8(pv[0], pv[1], pv[2], pv[3]);
@@ -609,9 +607,60 @@ __global__ __launch_bounds__(Shape<NHT>::threads, 1) void mla_fp8_decode_kernel(
                                                    16.f * (pv[2] - b1[0]), 16.f * (pv[3] - b1[1]));
           }
         }
-        lsum[ht] += __builtin_ldexpf(acc, kexp[half][ht]);
+        psum[half][ht] = acc;
       }
-    }
+    };
+    // Softmax, the rest: the reference exponent m0 (set on a work's first
+    // block, moved in the rare case the head maximum outgrows it), the block
+    // scale exponent e - m0 (clamped to the e8m0 range: a block more than 127
+    // below m0 counts as 2^-127 of m0, i.e. nothing) and the denominator.
+    auto softmax_scales = [&](int half) {
+#pragma unroll
+      for (int ht = 0; ht < NHT; ++ht) {
+        const float hm = hmax[half][ht] == kNegInf ? kNegInf : hmax[half][ht] * scale2;
+        if (half == 0 && first) m0[ht] = hm == kNegInf ? 0.f : __builtin_ceilf(hm) + 40.f;
+        const bool up = hm > m0[ht] + kRescaleMargin;
+        if (__builtin_expect(__ballot(up) != 0, 0)) {
+          // move m0: the denominator, the first half's block exponents and
+          // (past the work's first block) the accumulators follow it
+          const float mn = up ? __builtin_ceilf(hm) + 40.f : m0[ht];
+          const float f = __builtin_amdgcn_exp2f(m0[ht] - mn);
+          lsum[ht] *= f;
+          if (half == 1) kexp[0][ht] = max(kexp[0][ht] + (int)(m0[ht] - mn), -127);
+          m0[ht] = mn;
+          if (!first) rescale_acc(o, ht, f);
+        }
+        kexp[half][ht] = (int)fminf(fmaxf(bexp[half][ht] - m0[ht], -127.f), 127.f);
+        lsum[ht] += __builtin_ldexpf(psum[half][ht], kexp[half][ht]);
+      }
+    };
+
+    // Key products of both halves, software pipelined: the reads of product
+    // j + 2 are issued before product j (the scheduling barriers keep that
+    // order; the compiler's own schedule reads each operand just before its
+    // product and waits for it).  Interleaving the softmax VALU work into
+    // these products measured slower: the other wave on the SIMD already
+    // fills the matrix core's gaps.
+    auto key_half = [&](int half, f32x4 (&s)[4][NHT]) {
+      i32x8 kq[3];
+      key_operand(std::integral_constant<int, 0>{}, half, kq[0]);
+      key_operand(std::integral_constant<int, 1>{}, half, kq[1]);
+      static_for<20>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        if constexpr (j + 2 < 20) key_operand(std::integral_constant<int, j + 2>{}, half, kq[(j + 2) % 3]);
+        __builtin_amdgcn_sched_barrier(0);
+        key_product(jc, s, kq[j % 3]);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    };
+    key_half(0, s0);
+    key_half(1, s1);
+    mask(s0, 0);
+    softmax_probs(s0, 0);
+    softmax_scales(0);
+    mask(s1, 1);
+    softmax_probs(s1, 1);
+    softmax_scales(1);
     // Scale VGPR of lane group g = exponent of block g: (half 0, pair {0,1}),
     // (half 0, pair {2,3}), (half 1, pair {0,1}), (half 1, pair {2,3}).
     int sbv[2][NHT];  // [hi, lo term][head tile]
