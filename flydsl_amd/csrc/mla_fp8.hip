@@ -462,7 +462,10 @@ __global__ __launch_bounds__(Shape<NHT>::threads, 1) void mla_fp8_decode_kernel(
   we = min(max(we, ws), a.num_works);
   if (ws >= we) return;
 
-  const float scale2 = __builtin_fabsf(a.softmax_scale) * kLog2e;  // the query signs carry a negative scale's
+  // |scale| log2(e): a negative scale's sign is carried by the queries.  A
+  // zero scale is taken as the smallest normal float, the same uniform
+  // softmax, but masked logits stay -inf (-inf x 0 would be NaN).
+  const float scale2 = fmaxf(__builtin_fabsf(a.softmax_scale) * kLog2e, 0x1p-126f);
 
   // Unit cursors: cur (computed now), c1 (DMA issued this step), c2 (page
   // index prefetched this step).

@@ -80,7 +80,7 @@ def make_case(lens, seed, extra_pages=7, wide=None, nan_page0=False):
     return q, kv, qo_indptr, kv_indptr, kv_indices, last
 
 
-def run(lens, seed=0, num_cu=None, precise=False, fnuz=False, **case_kw):
+def run(lens, seed=0, num_cu=None, precise=False, fnuz=False, sm=None, **case_kw):
     q, kv, qo_indptr, kv_indptr, kv_indices, last = make_case(lens, seed, **case_kw)
     q_val, kv_val = om.fp8_to_f64(q), om.fp8_to_f64(kv.view(-1, QK_HEAD_DIM))
     if fnuz:  # the same values as float8_e4m3fnuz tensors (every e4m3fn value below 240 is one)
@@ -99,7 +99,7 @@ def run(lens, seed=0, num_cu=None, precise=False, fnuz=False, **case_kw):
     split_o = torch.full((npart, 1, 128, V_HEAD_DIM), float("nan"), dtype=torch.float32, device=DEV)
     split_l = torch.full((npart, 1, 128, 1), float("nan"), dtype=torch.float32, device=DEV)
     final_lse = torch.full((B, 128), float("nan"), dtype=torch.float32, device=DEV)
-    sm = 1.0 / QK_HEAD_DIM ** 0.5
+    sm = 1.0 / QK_HEAD_DIM ** 0.5 if sm is None else float(sm)
     qd, kvd, kid = q.to(DEV), kv.to(DEV), kv_indices.to(DEV)
     print(f"mla case lens={lens[:4]}{'...' if len(lens) > 4 else ''} B={B} seed={seed} num_cu={num_cu} "
           f"precise={precise}", flush=True)
@@ -206,3 +206,51 @@ def test_wide_logits_with_late_maxima(precise):
     want, want_lse, _ = om.mla_decode_ref(r["q"], r["kv"], r["qo"], r["kvp"], r["kvi"], r["sm"])
     assert float(np.min(want_lse)) > 120.0  # the boosted rows dominate every head
     check(r, precise=precise)
+
+
+@pytest.mark.parametrize("sm", [-1.0 / QK_HEAD_DIM ** 0.5, 0.0])
+def test_softmax_scales(sm):
+    """Negative (carried by the query signs) and zero (a uniform softmax)
+    scales: the kernel takes its maxima on the raw logits and folds the
+    scale into the exponent."""
+    check(run([1500, 64, 3000], seed=23, num_cu=4, sm=sm))
+
+
+def _quantized_softmax_out(q, kv, kvp, kvi, sm, b):
+    """float64 model of the kernel's fp8 probabilities for row b: one block
+    exponent e = ceil(max) per 32-token group (tokens 16t + 0..7 or
+    16t + 8..15 of the four 16-token tiles of a 64-token half block),
+    p = 2^(x - e) rounded to e4m3fn in the numerator, exact p in the
+    denominator."""
+    idx = kvi[kvp[b]:kvp[b + 1]]
+    K = kv[idx]
+    V = K[:, :V_HEAD_DIM]
+    x = (K @ q[b].T) * sm * np.log2(np.e)  # [tokens, heads]
+    pos = np.arange(len(idx))
+    grp = (pos // 64) * 2 + (pos % 16) // 8
+    num = np.zeros((q.shape[1], V_HEAD_DIM))
+    den = np.zeros(q.shape[1])
+    for G in np.unique(grp):
+        m = grp == G
+        e = np.ceil(x[m].max(axis=0))
+        p = 2.0 ** (x[m] - e)
+        pq = torch.from_numpy(p.astype(np.float32)).to(FP8).to(torch.float64).numpy()
+        num += (pq * 2.0 ** e).T @ V[m]
+        den += (p * 2.0 ** e).sum(axis=0)
+    return num / den[:, None]
+
+
+def test_large_softmax_scale():
+    """Scale 0.5 (12x the usual): a very peaked softmax.  Probabilities more
+    than 2^6 below their 32-token group's maximum fall in the fp8 subnormal
+    range, where rounding is absolute (2^-10 of the group's block exponent),
+    so an element whose |v|-weight sits on such tokens can be far off in
+    relative terms -- the arithmetic of one fp8 term per probability (the
+    reference's), not a fault.  The bound: the distance of a float64 model
+    of that quantization from the exact result, plus the usual bound."""
+    r = run([1500, 64, 3000], seed=23, num_cu=4, sm=0.5)
+    want, _, wabs = om.mla_decode_ref(r["q"], r["kv"], r["qo"], r["kvp"], r["kvi"], r["sm"])
+    for b in range(3):
+        model = _quantized_softmax_out(r["q"], r["kv"], r["kvp"], r["kvi"], r["sm"], b)
+        tol = np.abs(model - want[b]) + tolerance(wabs[b], want[b], False)
+        assert np.all(np.abs(r["out"][b] - want[b]) <= tol), f"row {b}"
