@@ -175,18 +175,16 @@ __device__ __forceinline__ void rescale_acc(f32x4 (&o)[16][2][NHT], int ht, floa
 }
 
 // 16 bytes per lane from global memory straight into LDS (M0 = the wave's
-// LDS destination, lane l writing 16 l bytes past it), with the default
-// cache policy: a 576-byte row is read as nine 64-byte pieces by nine
-// instructions, and keeping the 128-byte lines in L2 lets the second piece
-// of each line hit there (measured: the non-temporal hint makes this DMA
-// pattern about 10% slower).
+// LDS destination, lane l writing 16 l bytes past it), non-temporal: with
+// the default cache policy the kernel fetches about 1.5x the bytes from
+// HBM (measured with FETCH_SIZE), at no gain in time.
 // Inline assembly rather than __builtin_amdgcn_global_load_lds: while the
 // builtin's DMA is in flight, the compiler's wait insertion takes every LDS
 // read to be unordered behind it and waits for each with lgkmcnt(0), which
 // serialises the pipelined key reads.  The DMA is awaited explicitly
 // (vmcnt(0) and a barrier before its stage is read).
 __device__ __forceinline__ void lds_dma16(const void* gsrc, LDS_AS void* ldst) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt"
                :
                : "v"(gsrc), "s"((unsigned)(uintptr_t)ldst)
                : "memory", "m0");
