@@ -255,6 +255,14 @@ __device__ __forceinline__ int lane_id() {
   return r;
 }
 
+// Zero the compiler cannot see through (keeps two loads of one address
+// apart).
+__device__ __forceinline__ int opaque_zero() {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
+}
+
 __device__ __forceinline__ Work load_work(const pa_mla_decode_args& a, int wi) {
   const int32_t* w = a.work_info + 8 * (int64_t)wi;
   Work r;
@@ -362,19 +370,26 @@ __device__ __forceinline__ void load_query(const pa_mla_decode_args& a, int qo, 
       const i32x4 hi = *(const i32x4*)(row + 128 * kb + 64);
       q.b[ht][kb] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
-    const i32x4 r = *(const i32x4*)(row + 512);
-    q.r[ht] = i32x8{r[0], r[1], r[2], r[3], r[0], r[1], r[2], r[3]};
+    // the rope dims loaded twice, straight into both halves: a register
+    // copy would wait for the load (vmcnt counts in order, so also for the
+    // next block's DMA in flight) at the end of every block
+    const i32x4 r0 = *(const i32x4*)(row + 512);
+    const i32x4 r1 = *(const i32x4*)(row + 512 + opaque_zero());
+    q.r[ht] = i32x8{r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
   }
-  // A negative softmax scale: the queries' signs are flipped (exact in
-  // fp8) and the kernel scales by |softmax_scale|, so the softmax can take
-  // its maxima on the raw logits.
-  if (a.softmax_scale < 0.f) {
+}
+
+// A negative softmax scale: the queries' signs are flipped (exact in fp8)
+// and the kernel scales by |softmax_scale|, so the softmax can take its
+// maxima on the raw logits.  Applied after the loop top's wait (applied at
+// the load it would wait there for the next block's DMA).
+template <int NHT>
+__device__ __forceinline__ void flip_query_signs(QTile<NHT>& q) {
 #pragma unroll
-    for (int ht = 0; ht < NHT; ++ht) {
+  for (int ht = 0; ht < NHT; ++ht) {
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) q.b[ht][kb] ^= (int)0x80808080u;
-      q.r[ht] ^= (int)0x80808080u;
-    }
+    for (int kb = 0; kb < 4; ++kb) q.b[ht][kb] ^= (int)0x80808080u;
+    q.r[ht] ^= (int)0x80808080u;
   }
 }
 
@@ -509,6 +524,7 @@ __global__ __launch_bounds__(Shape<NHT>::threads, 1) void mla_fp8_decode_kernel(
     // rather than with lgkmcnt(0).
     __builtin_amdgcn_s_waitcnt(vmcnt_only(0) & ~(15 << 8));
     asm volatile("s_barrier" ::: "memory");
+    if (a.softmax_scale < 0.f) flip_query_signs(q);
     if (valid(c1, we)) {
       issue_block<NHT>(a, lds + (st ^ 1) * kStageBytes, w, pg1);
       if (valid(c2, we)) pg1 = unit_pages<NHT>(a, c2, w);
