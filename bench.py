@@ -54,7 +54,7 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--config", default="c2_llama8b",
                    help="c1_tiny|c2_llama8b|c3_ragged|c4_window|c5_mtp|all (decode), c3_ragged_p1024 "
-                        "(work-list route), "
+                        "(work-list route), c2_d64|c2_d256 (head sizes 64 and 256), "
                         "rope_decode_llama8b|rope_prefill_llama8b (KV-cache writer), "
                         "qknr_prefill_v4|qknr_decode_v4 (fused RMSNorm + GPT-J RoPE + fp8 quant), "
                         "mla_b32_c8192|mla_b128_c8192 (MLA fp8 decode)")
@@ -236,7 +236,7 @@ def run_config(name: str, args) -> dict:
         P = args.partitions
     es = torch.empty((B, hkv, P, eq), device=dev)
     ml = torch.empty_like(es)
-    tmp = torch.empty((B, hkv, P, eq, 128), device=dev, dtype=torch.bfloat16)
+    tmp = torch.empty((B, hkv, P, eq, cfg.head_size), device=dev, dtype=torch.bfloat16)
     out = torch.empty(case["query"].shape, device=dev, dtype=torch.bfloat16)
 
     # The call the reference's own harness makes for this route
@@ -335,7 +335,7 @@ def run_config(name: str, args) -> dict:
             "query_length": ql,
             "num_query_heads": cfg.num_query_heads,
             "num_kv_heads": hkv,
-            "head_size": 128,
+            "head_size": cfg.head_size,
             "block_size": cfg.block_size,
             "sliding_window": cfg.sliding_window,
             "kv_scales": "per_token" if cfg.per_token else "per_tensor",

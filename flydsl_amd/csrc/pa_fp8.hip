@@ -2951,124 +2951,186 @@ __device__ __forceinline__ uint32_t gen_keep4(int t, int lo, int hi) {
   return below_u & ~below_l;
 }
 
-// Online softmax of the lane's column over keys [t0, t1) into st.
+// One 32-token chunk's operands in registers: the lane's key pieces for the
+// two 16-token tiles, its value words for every 16-dim output tile and its
+// tokens' scales.  Loaded a chunk ahead of their use (gen_range), so a
+// chunk's memory latency overlaps the previous chunk's arithmetic.  With
+// VPF false (D >= 192, for registers) the values are loaded at the start of
+// their own chunk instead, still ahead of its key product.
+template <int D, bool PER_TOKEN>
+struct GenChunk {
+  static constexpr bool VPF = D <= 128;
+  long kr[2][D / 32];
+  uint32_t vw[D / 16][2];
+  float ks[8], vs[8];
+  int pg[2], sb[2];
+};
+
+template <int D, bool PER_TOKEN>
+__device__ __forceinline__ void gen_load_values(GenChunk<D, PER_TOKEN>& ch, const GenCtx<D>& c, const GenArgs& a,
+                                                int grp, int c16) {
+  const int bs = a.block_size;
+#pragma unroll
+  for (int j = 0; j < D / 16; ++j) {
+    const int d = 16 * j + c16;
+#pragma unroll
+    for (int tau = 0; tau < 2; ++tau) {
+      const int sv = ch.sb[tau] + 4 * grp;
+      const int64_t off = a.trans_v ? ((int64_t)(sv >> 4) * D + d) * 16 + (sv & 15) : (int64_t)d * bs + sv;
+      ch.vw[j][tau] = *(const uint32_t*)(c.vbase + (int64_t)ch.pg[tau] * a.stride_v_block + off);
+    }
+  }
+}
+
+template <int D, bool PER_TOKEN>
+__device__ __forceinline__ void gen_load(GenChunk<D, PER_TOKEN>& ch, const GenCtx<D>& c, const GenArgs& a, int tc,
+                                         int grp, int c16) {
+  const int bs = a.block_size;
+#pragma unroll
+  for (int tau = 0; tau < 2; ++tau) {
+    ch.pg[tau] = gen_page(a, c.pages, c.last_page, tc + 16 * tau);
+    ch.sb[tau] = (tc + 16 * tau) % bs;
+  }
+#pragma unroll
+  for (int tau = 0; tau < 2; ++tau) {
+    const uint8_t* kp = c.kbase + (int64_t)ch.pg[tau] * a.stride_k_block + (ch.sb[tau] + c16) * 16 + 8 * (grp & 1);
+#pragma unroll
+    for (int blk = 0; blk < D / 32; ++blk)
+      ch.kr[tau][blk] = *(const long*)(kp + (int64_t)(2 * blk + (grp >> 1)) * bs * 16);
+  }
+  if (PER_TOKEN) {
+#pragma unroll
+    for (int tau = 0; tau < 2; ++tau) {
+      const int64_t so = (int64_t)ch.pg[tau] * a.stride_ks_block + ch.sb[tau] + 4 * grp;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ch.ks[4 * tau + i] = c.ksbase[so + i];
+        ch.vs[4 * tau + i] = c.vsbase[so + i];
+      }
+    }
+  }
+  if constexpr (GenChunk<D, PER_TOKEN>::VPF) gen_load_values(ch, c, a, grp, c16);
+}
+
+// Online softmax of the lane's column over the chunk at tc (keys [A, B) used;
+// t0, t1 bound the visible ones).
+template <int D, bool PER_TOKEN>
+__device__ __forceinline__ void gen_chunk(GenState<D>& st, GenChunk<D, PER_TOKEN>& ch, const GenCtx<D>& c,
+                                          const GenArgs& a, int tc, int t0, int t1, int A, int B, int vis_lo,
+                                          int vis_hi, int grp, int c16) {
+  if constexpr (!GenChunk<D, PER_TOKEN>::VPF) gen_load_values(ch, c, a, grp, c16);
+  // ---- logits of tokens tc + 16 tau + 4 grp + i ----
+  f32x4 lt[2];
+#pragma unroll
+  for (int tau = 0; tau < 2; ++tau) {
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int blk = 0; blk < D / 32; ++blk) {
+      acc = mfma_fp8(ch.kr[tau][blk], c.qhi[blk], acc);
+      acc = mfma_fp8(ch.kr[tau][blk], c.qlo[blk], acc);
+    }
+    lt[tau] = acc;
+  }
+  float x[8], vs[8];
+#pragma unroll
+  for (int tau = 0; tau < 2; ++tau)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[4 * tau + i] = lt[tau][i];
+      vs[4 * tau + i] = 1.0f;
+    }
+  if (PER_TOKEN) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      x[k] *= ch.ks[k];
+      vs[k] = ch.vs[k];
+    }
+  }
+  // ---- masks (edge chunks only) ----
+  const bool all_vis = tc >= pa_max(t0, c.lo_max) && tc + 32 <= pa_min(t1, c.hi_min);
+  if (!all_vis) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int t = tc + 16 * (k >> 2) + 4 * grp + (k & 3);
+      x[k] = (t >= vis_lo && t < vis_hi) ? x[k] : kNegInf;
+      if (PER_TOKEN) vs[k] = (t >= A && t < B) ? vs[k] : 0.0f;
+    }
+  }
+  // ---- online softmax ----
+  float cmax = kNegInf;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) cmax = fmaxf(cmax, x[k]);
+  cmax = max_over_groups(cmax) * c.fac;
+  const float mnew = fmaxf(st.m2, cmax);
+  const float muse = mnew == kNegInf ? 0.0f : mnew;
+  const float alpha = __builtin_amdgcn_exp2f(st.m2 - muse);
+  float vratio = 1.0f, vinv = 1.0f;
+  if (PER_TOKEN) {
+    float vmax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) vmax = fmaxf(vmax, vs[k]);
+    vmax = max_over_groups(vmax);
+    const float vnew = fmaxf(st.vsref, vmax);
+    vratio = st.vsref > 0.0f ? st.vsref / vnew : 1.0f;
+    vinv = vnew > 0.0f ? 1.0f / vnew : 0.0f;
+    st.vsref = vnew;
+  }
+  st.m2 = mnew;
+  const float f = alpha * vratio;
+  if (__ballot(f != 1.0f)) {
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) st.acc[j] *= f;
+  }
+  const float bias = kGenPBias - muse;
+  float psum = 0.0f, pr[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(x[k], c.fac, bias));
+    psum += p;
+    pr[k] = PER_TOKEN ? p * (vs[k] * vinv) : p;
+  }
+  st.lsum = st.lsum * alpha + psum;
+  long phi, plo;
+  split8_fp8(pr, phi, plo);
+  // ---- value product: tokens 4 grp .. +3 and 16 + 4 grp .. +3 ----
+  uint32_t keep[2] = {~0u, ~0u};
+  const bool stale = tc < A || tc + 32 > B;
+  if (stale) {
+#pragma unroll
+    for (int tau = 0; tau < 2; ++tau) keep[tau] = gen_keep4(tc + 16 * tau + 4 * grp, A, B);
+  }
+#pragma unroll
+  for (int j = 0; j < D / 16; ++j) {
+    const long vv = (long)((uint64_t)(ch.vw[j][0] & keep[0]) | ((uint64_t)(ch.vw[j][1] & keep[1]) << 32));
+    st.acc[j] = mfma_fp8(vv, phi, st.acc[j]);
+    st.acc[j] = mfma_fp8(vv, plo, st.acc[j]);
+  }
+}
+
+// Online softmax of the lane's column over keys [t0, t1) into st: chunks in
+// pairs through two operand buffers (no register copies, whose waits would
+// also wait for the next chunk's loads), each chunk's loads issued before
+// the previous chunk's arithmetic.
 template <int D, bool PER_TOKEN>
 __device__ void gen_range(GenState<D>& st, const GenCtx<D>& c, const GenArgs& a, int t0, int t1, int grp,
                           int c16) {
   // keys any column may use, and the stale-byte bound
   const int A = pa_max(t0, c.lo_all), B = pa_min(t1, c.hi_all);
   if (B <= A) return;
-  const int bs = a.block_size;
   const int vis_lo = pa_max(c.vis_lo, t0), vis_hi = pa_min(c.vis_hi, t1);
-  for (int tc = A & ~31; tc < B; tc += 32) {
-    int pg[2], sb[2];
-#pragma unroll
-    for (int tau = 0; tau < 2; ++tau) {
-      pg[tau] = gen_page(a, c.pages, c.last_page, tc + 16 * tau);
-      sb[tau] = (tc + 16 * tau) % bs;
-    }
-    // ---- logits of tokens tc + 16 tau + 4 grp + i ----
-    f32x4 lt[2];
-#pragma unroll
-    for (int tau = 0; tau < 2; ++tau) {
-      const uint8_t* kp = c.kbase + (int64_t)pg[tau] * a.stride_k_block + (sb[tau] + c16) * 16 + 8 * (grp & 1);
-      long kr[D / 32];
-#pragma unroll
-      for (int blk = 0; blk < D / 32; ++blk) kr[blk] = *(const long*)(kp + (int64_t)(2 * blk + (grp >> 1)) * bs * 16);
-      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int blk = 0; blk < D / 32; ++blk) {
-        acc = mfma_fp8(kr[blk], c.qhi[blk], acc);
-        acc = mfma_fp8(kr[blk], c.qlo[blk], acc);
-      }
-      lt[tau] = acc;
-    }
-    float x[8], vs[8];
-#pragma unroll
-    for (int tau = 0; tau < 2; ++tau)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x[4 * tau + i] = lt[tau][i];
-        vs[4 * tau + i] = 1.0f;
-      }
-    if (PER_TOKEN) {
-#pragma unroll
-      for (int tau = 0; tau < 2; ++tau) {
-        const int64_t so = (int64_t)pg[tau] * a.stride_ks_block + sb[tau] + 4 * grp;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          x[4 * tau + i] *= c.ksbase[so + i];
-          vs[4 * tau + i] = c.vsbase[so + i];
-        }
-      }
-    }
-    // ---- masks (edge chunks only) ----
-    const bool all_vis = tc >= pa_max(t0, c.lo_max) && tc + 32 <= pa_min(t1, c.hi_min);
-    if (!all_vis) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int t = tc + 16 * (k >> 2) + 4 * grp + (k & 3);
-        x[k] = (t >= vis_lo && t < vis_hi) ? x[k] : kNegInf;
-        if (PER_TOKEN) vs[k] = (t >= A && t < B) ? vs[k] : 0.0f;
-      }
-    }
-    // ---- online softmax ----
-    float cmax = kNegInf;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) cmax = fmaxf(cmax, x[k]);
-    cmax = max_over_groups(cmax) * c.fac;
-    const float mnew = fmaxf(st.m2, cmax);
-    const float muse = mnew == kNegInf ? 0.0f : mnew;
-    const float alpha = __builtin_amdgcn_exp2f(st.m2 - muse);
-    float vratio = 1.0f, vinv = 1.0f;
-    if (PER_TOKEN) {
-      float vmax = 0.0f;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) vmax = fmaxf(vmax, vs[k]);
-      vmax = max_over_groups(vmax);
-      const float vnew = fmaxf(st.vsref, vmax);
-      vratio = st.vsref > 0.0f ? st.vsref / vnew : 1.0f;
-      vinv = vnew > 0.0f ? 1.0f / vnew : 0.0f;
-      st.vsref = vnew;
-    }
-    st.m2 = mnew;
-    const float f = alpha * vratio;
-    if (__ballot(f != 1.0f)) {
-#pragma unroll
-      for (int j = 0; j < D / 16; ++j) st.acc[j] *= f;
-    }
-    const float bias = kGenPBias - muse;
-    float psum = 0.0f, pr[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(x[k], c.fac, bias));
-      psum += p;
-      pr[k] = PER_TOKEN ? p * (vs[k] * vinv) : p;
-    }
-    st.lsum = st.lsum * alpha + psum;
-    long phi, plo;
-    split8_fp8(pr, phi, plo);
-    // ---- value product: tokens 4 grp .. +3 and 16 + 4 grp .. +3 ----
-    uint32_t keep[2] = {~0u, ~0u};
-    const bool stale = tc < A || tc + 32 > B;
-    if (stale) {
-#pragma unroll
-      for (int tau = 0; tau < 2; ++tau) keep[tau] = gen_keep4(tc + 16 * tau + 4 * grp, A, B);
-    }
-#pragma unroll
-    for (int j = 0; j < D / 16; ++j) {
-      const int d = 16 * j + c16;
-      uint32_t w[2];
-#pragma unroll
-      for (int tau = 0; tau < 2; ++tau) {
-        const int s = sb[tau] + 4 * grp;
-        const int64_t off = a.trans_v ? ((int64_t)(s >> 4) * D + d) * 16 + (s & 15) : (int64_t)d * bs + s;
-        w[tau] = *(const uint32_t*)(c.vbase + (int64_t)pg[tau] * a.stride_v_block + off) & keep[tau];
-      }
-      const long vv = (long)((uint64_t)w[0] | ((uint64_t)w[1] << 32));
-      st.acc[j] = mfma_fp8(vv, phi, st.acc[j]);
-      st.acc[j] = mfma_fp8(vv, plo, st.acc[j]);
-    }
+  GenChunk<D, PER_TOKEN> ch0, ch1;
+  int tc = A & ~31;
+  gen_load(ch0, c, a, tc, grp, c16);
+  while (true) {
+    const bool more1 = tc + 32 < B;
+    if (more1) gen_load(ch1, c, a, tc + 32, grp, c16);
+    gen_chunk(st, ch0, c, a, tc, t0, t1, A, B, vis_lo, vis_hi, grp, c16);
+    if (!more1) break;
+    const bool more2 = tc + 64 < B;
+    if (more2) gen_load(ch0, c, a, tc + 64, grp, c16);
+    gen_chunk(st, ch1, c, a, tc + 32, t0, t1, A, B, vis_lo, vis_hi, grp, c16);
+    if (!more2) break;
+    tc += 64;
   }
 }
 
