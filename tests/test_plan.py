@@ -65,7 +65,8 @@ def test_recommended_splits_for_benchmark_configs():
                                                     query_length=c.query_length)
         else:
             got[name] = plan.get_recommended_splits(c.batch, c.num_kv_heads, 256 // c.block_size, num_cu=256)
-    assert got == {"c1_tiny": 8, "c2_llama8b": 8, "c3_ragged": 8, "c4_window": 17, "c5_mtp": 4}
+    assert got == {"c1_tiny": 8, "c2_llama8b": 8, "c3_ragged": 8, "c4_window": 17, "c5_mtp": 4,
+                   "c2_d64": 8, "c2_d256": 8}
 
 
 @pytest.mark.parametrize("P", [1, 3, 4, 8])
