@@ -3184,7 +3184,7 @@ __device__ __forceinline__ void gen_store4(void* base, int dtype, int64_t off, f
 // and column block 4 * blockIdx.y + wave.  A slot stores exp_sums /
 // max_logits / tmp_out for its columns; an owner walks every slot (storing
 // its partials when the buffers are given), folds them and writes `output`.
-template <int D, bool PER_TOKEN>
+template <int D, bool PER_TOKEN, bool OWNER>
 __global__ __launch_bounds__(256) void pa_fp8_generic_partition_kernel(const GenArgs a) {
   const int lane = threadIdx.x & 63, grp = lane >> 4, c16 = lane & 15;
   const int wave = threadIdx.x >> 6;
@@ -3192,17 +3192,17 @@ __global__ __launch_bounds__(256) void pa_fp8_generic_partition_kernel(const Gen
   const int e0 = (4 * (int)blockIdx.y + wave) * 16;
   if (e0 >= eq) return;
   const int P = a.num_partitions;
-  const int per = a.owner ? 1 : P;
-  const int z0 = a.owner ? 0 : (int)(blockIdx.x % per);
+  const int per = OWNER ? 1 : P;
+  const int z0 = OWNER ? 0 : (int)(blockIdx.x % per);
   const int bh = (int)(blockIdx.x / per);
   const int h = bh % a.num_kv_heads, b = bh / a.num_kv_heads;
   GenCtx<D> c;
   gen_setup<D, PER_TOKEN>(c, a, b, h, b * a.query_length, e0, grp, c16);
   const int e = e0 + c16;
   const bool valid = e < eq;
-  GenState<D> fin;
-  fin.reset(PER_TOKEN);
-  const int z1 = a.owner ? P : z0 + 1;
+  GenState<D> fin;  // owner: the slots folded so far (unused otherwise)
+  if (OWNER) fin.reset(PER_TOKEN);
+  const int z1 = OWNER ? P : z0 + 1;
   for (int z = z0; z < z1; ++z) {
     int t0, t1;
     pa_plan_slot_tokens(c.ctx, P, z, a.sliding_window, a.query_length, &t0, &t1);
@@ -3224,9 +3224,10 @@ __global__ __launch_bounds__(256) void pa_fp8_generic_partition_kernel(const Gen
         for (int j = 0; j < D / 16; ++j) gen_store4(a.tmp_out, a.tmp_dtype, to + 16 * j, st.acc[j] * sc);
       }
     }
-    if (a.owner) gen_merge<D, PER_TOKEN>(fin, st);
+    if constexpr (OWNER) gen_merge<D, PER_TOKEN>(fin, st);
   }
-  if (a.owner && valid) {
+  if constexpr (OWNER) {
+    if (!valid) return;
     float sc, es, ml;
     gen_finish<D, PER_TOKEN>(fin, a, sc, es, ml);
     const int qi = e / a.query_group_size, g = e - qi * a.query_group_size;
@@ -3385,7 +3386,10 @@ static bool generic_head_ok(int d) { return d == 64 || d == 128 || d == 192 || d
 
 template <int D, bool PT>
 static hipError_t launch_generic_partition(const GenArgs& g, dim3 grid, dim3 block, hipStream_t s) {
-  hipLaunchKernelGGL((pa_fp8_generic_partition_kernel<D, PT>), grid, block, 0, s, g);
+  if (g.owner)
+    hipLaunchKernelGGL((pa_fp8_generic_partition_kernel<D, PT, true>), grid, block, 0, s, g);
+  else
+    hipLaunchKernelGGL((pa_fp8_generic_partition_kernel<D, PT, false>), grid, block, 0, s, g);
   return hipGetLastError();
 }
 template <int D, bool PT>

@@ -242,6 +242,18 @@ STREAM_MAX_COLUMNS = 16
 COOP_MAX_COLUMNS = 64
 
 
+# A generic-kernel owner launch runs one wave per (sequence, kv head,
+# 16-column block), each walking every slot in turn; with fewer waves than
+# this per CU it leaves SIMDs idle and the slot launch (a workgroup per slot)
+# plus the LSE reduce is faster (C2's batch at head size 64: 119 -> 57 us).
+GENERIC_OWNER_MIN_WAVES_PER_CU = 8
+
+
+def _generic_owner_ok(batch: int, kv_heads: int, eqgs: int, num_cu: int) -> bool:
+    """Whether a generic-kernel owner launch fills the GPU."""
+    return batch * kv_heads * -(-eqgs // 16) >= GENERIC_OWNER_MIN_WAVES_PER_CU * num_cu
+
+
 def _balanced_ok(route: str, batch: int, eqgs: int, user_partials: bool, owner: bool) -> bool:
     """Balanced stream split for a call whose slot partials nobody reads:
     every wave (or, for more than 16 query columns, every cooperative
@@ -483,6 +495,10 @@ def prepare_pa_decode(
     spw = _schedule(route, batch_size, num_kv_heads, P, eqgs, capacity, _cu_count(dev) if P > 1 else 1)
     owner = spw >= P
     user_partials = exp_sums is not None or max_logits is not None or temporary_output is not None
+    have_partials = exp_sums is not None and max_logits is not None and temporary_output is not None
+    if (generic and owner and P > 1 and not (is_graph_capturing and not have_partials)
+            and not _generic_owner_ok(batch_size, num_kv_heads, eqgs, _cu_count(dev))):
+        spw, owner = 1, False
     if not generic and _balanced_ok(route, batch_size, eqgs, user_partials, owner):
         route_name = "ps_small_block" if route == "small" else "ps_split_reduce"
         sa = _stream_args(output, query, key_cache, value_cache, context_lengths,

@@ -49,15 +49,17 @@ SCHEDULES = {
 @contextlib.contextmanager
 def schedule(name):
     """Force the launcher's slots-per-workgroup choice (and, for a forced
-    choice, keep the partition pass: no balanced stream split)."""
-    saved = pd._schedule, pd._balanced_ok
+    choice, keep the partition pass: no balanced stream split, and no switch
+    of a generic-kernel owner launch to slots)."""
+    saved = pd._schedule, pd._balanced_ok, pd._generic_owner_ok
     if SCHEDULES[name] is not None:
         pd._schedule = SCHEDULES[name]
         pd._balanced_ok = lambda *args: False
+        pd._generic_owner_ok = lambda *args: True
     try:
         yield
     finally:
-        pd._schedule, pd._balanced_ok = saved
+        pd._schedule, pd._balanced_ok, pd._generic_owner_ok = saved
 
 
 def launch(case, *, P=0, out_dtype=torch.bfloat16, tmp_dtype=torch.bfloat16, flat=False, partials=False,

@@ -226,6 +226,25 @@ def test_generic_shapes_take_the_partition_routes(d, ql, hq, hkv):
     assert call.route in ("ps_sw_partitioned", "ps_sw_fused_partitioned") and call._pa.head_size == d
 
 
+def test_generic_owner_needs_enough_waves(monkeypatch):
+    """The generic kernels' owner launch runs one wave per (sequence, kv head,
+    16-column block); below 8 such waves per CU the launcher takes slot mode
+    plus the reduce instead, even where the D = 128 kernels would take owner."""
+    assert not pd._generic_owner_ok(64, 8, 4, 256)  # C2's batch: 512 waves on 256 CUs
+    assert pd._generic_owner_ok(256, 8, 4, 256)
+    assert pd._generic_owner_ok(128, 8, 32, 256)  # 2 column blocks per pair
+    # 512 (sequence, kv head) pairs with short contexts: owner for D = 128
+    case = make_case(batch=64, ctx=[40] * 64, num_query_heads=32, num_kv_heads=8, seed=4, head_size=128)
+    call = prep(case, max_context_partition_num=4)
+    assert call._ra is None
+    case = make_case(batch=64, ctx=[40] * 64, num_query_heads=32, num_kv_heads=8, seed=4, head_size=64)
+    call = prep(case, max_context_partition_num=4)
+    assert call._pa.head_size == 64 and call._ra is not None and call._ra.head_size == 64
+    monkeypatch.setattr(pd, "_generic_owner_ok", lambda *args: True)
+    call = prep(case, max_context_partition_num=4)
+    assert call._ra is None
+
+
 def test_unbuilt_head_size_is_not_implemented():
     case = make_case(batch=1, ctx=[10], seed=5, head_size=64)
     c = dict(case)
