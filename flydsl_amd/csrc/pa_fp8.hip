@@ -2851,7 +2851,7 @@ struct GenArgs {
   int64_t stride_es_seq, stride_es_head, stride_es_part;
   int64_t stride_to_seq, stride_to_head, stride_to_part, stride_to_group;
   int num_partitions;
-  int owner;  // one workgroup walks every slot and writes `output`
+  int owner;  // kGenSlot, kGenOwnerSlots or kGenOwnerRange
   // work list
   const int32_t* work_indptr;
   const int32_t* work_info;
@@ -3180,12 +3180,21 @@ __device__ __forceinline__ void gen_store4(void* base, int dtype, int64_t off, f
   }
 }
 
-// Partition launches: workgroup (b, h, slot) -- or (b, h) when `owner` --
-// and column block 4 * blockIdx.y + wave.  A slot stores exp_sums /
-// max_logits / tmp_out for its columns; an owner walks every slot (storing
-// its partials when the buffers are given), folds them and writes `output`.
-template <int D, bool PER_TOKEN, bool OWNER>
+// Partition launch modes (GenArgs::owner).
+enum : int {
+  kGenSlot = 0,        // workgroup (b, h, slot): the slot's partials
+  kGenOwnerSlots = 1,  // workgroup (b, h): every slot's partials, folded into `output`
+  kGenOwnerRange = 2,  // workgroup (b, h): one pass over every visible key into `output`
+};
+
+// Partition launches: workgroup (b, h, slot) -- or (b, h) in the owner
+// modes -- and column block 4 * blockIdx.y + wave.  A slot stores exp_sums /
+// max_logits / tmp_out for its columns.  kGenOwnerSlots walks every slot,
+// stores its partials, folds them and writes `output`; kGenOwnerRange (no
+// partials asked for) streams the whole visible range with one state.
+template <int D, bool PER_TOKEN, int MODE>
 __global__ __launch_bounds__(256) void pa_fp8_generic_partition_kernel(const GenArgs a) {
+  constexpr bool OWNER = MODE != kGenSlot;
   const int lane = threadIdx.x & 63, grp = lane >> 4, c16 = lane & 15;
   const int wave = threadIdx.x >> 6;
   const int eq = a.query_length * a.query_group_size;
@@ -3200,7 +3209,24 @@ __global__ __launch_bounds__(256) void pa_fp8_generic_partition_kernel(const Gen
   gen_setup<D, PER_TOKEN>(c, a, b, h, b * a.query_length, e0, grp, c16);
   const int e = e0 + c16;
   const bool valid = e < eq;
-  GenState<D> fin;  // owner: the slots folded so far (unused otherwise)
+  auto write_output = [&](const GenState<D>& s) {
+    float sc, es, ml;
+    gen_finish<D, PER_TOKEN>(s, a, sc, es, ml);
+    const int qi = e / a.query_group_size, g = e - qi * a.query_group_size;
+    const int64_t off = (int64_t)(b * a.query_length + qi) * a.stride_out_tok +
+                        (int64_t)(h * a.query_group_size + g) * a.stride_out_head + 4 * grp;
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) gen_store4(a.output, a.output_dtype, off + 16 * j, s.acc[j] * sc);
+  };
+  if constexpr (MODE == kGenOwnerRange) {
+    // gen_range clips [0, ctx) to the keys some column sees (window included)
+    GenState<D> st;
+    st.reset(PER_TOKEN);
+    gen_range<D, PER_TOKEN>(st, c, a, 0, c.ctx, grp, c16);
+    if (valid) write_output(st);
+    return;
+  }
+  GenState<D> fin;  // kGenOwnerSlots: the slots folded so far (unused otherwise)
   if (OWNER) fin.reset(PER_TOKEN);
   const int z1 = OWNER ? P : z0 + 1;
   for (int z = z0; z < z1; ++z) {
@@ -3227,14 +3253,7 @@ __global__ __launch_bounds__(256) void pa_fp8_generic_partition_kernel(const Gen
     if constexpr (OWNER) gen_merge<D, PER_TOKEN>(fin, st);
   }
   if constexpr (OWNER) {
-    if (!valid) return;
-    float sc, es, ml;
-    gen_finish<D, PER_TOKEN>(fin, a, sc, es, ml);
-    const int qi = e / a.query_group_size, g = e - qi * a.query_group_size;
-    const int64_t off = (int64_t)(b * a.query_length + qi) * a.stride_out_tok +
-                        (int64_t)(h * a.query_group_size + g) * a.stride_out_head + 4 * grp;
-#pragma unroll
-    for (int j = 0; j < D / 16; ++j) gen_store4(a.output, a.output_dtype, off + 16 * j, fin.acc[j] * sc);
+    if (valid) write_output(fin);
   }
 }
 
@@ -3386,10 +3405,12 @@ static bool generic_head_ok(int d) { return d == 64 || d == 128 || d == 192 || d
 
 template <int D, bool PT>
 static hipError_t launch_generic_partition(const GenArgs& g, dim3 grid, dim3 block, hipStream_t s) {
-  if (g.owner)
-    hipLaunchKernelGGL((pa_fp8_generic_partition_kernel<D, PT, true>), grid, block, 0, s, g);
+  if (g.owner == kGenOwnerRange)
+    hipLaunchKernelGGL((pa_fp8_generic_partition_kernel<D, PT, kGenOwnerRange>), grid, block, 0, s, g);
+  else if (g.owner == kGenOwnerSlots)
+    hipLaunchKernelGGL((pa_fp8_generic_partition_kernel<D, PT, kGenOwnerSlots>), grid, block, 0, s, g);
   else
-    hipLaunchKernelGGL((pa_fp8_generic_partition_kernel<D, PT, false>), grid, block, 0, s, g);
+    hipLaunchKernelGGL((pa_fp8_generic_partition_kernel<D, PT, kGenSlot>), grid, block, 0, s, g);
   return hipGetLastError();
 }
 template <int D, bool PT>
@@ -3470,7 +3491,7 @@ int generic_partition(const pa_fp8_partition_args& a, bool owner, hipStream_t s)
   g.stride_to_part = a.stride_to_part;
   g.stride_to_group = a.stride_to_group;
   g.num_partitions = a.num_partitions;
-  g.owner = owner ? 1 : 0;
+  g.owner = !owner ? kGenSlot : a.exp_sums ? kGenOwnerSlots : kGenOwnerRange;
   const int ncg = pa_cdiv(a.query_length * a.query_group_size, 16);
   const int64_t gx = (int64_t)a.num_seqs * a.num_kv_heads * (owner ? 1 : a.num_partitions);
   const int gy = pa_cdiv(ncg, 4);
