@@ -1608,8 +1608,20 @@ __device__ __forceinline__ void store_piece(const pa_fp8_stream_args& a, void* _
       pl = (int64_t)p.target * eq + e;
       po = pl * kHead;
     }
+    if constexpr (WORKLIST) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) *(f32x4*)(part_out + po + 16 * j + 4 * grp) = acc[j] * sc;
+      for (int j = 0; j < 8; ++j) *(f32x4*)(part_out + po + 16 * j + 4 * grp) = acc[j] * sc;
+    } else {
+      // The balanced split's partial rows are internal to the call: bf16
+      // halves their write and merge traffic (about 2^-9 relative, twice).
+      uint16_t* pb = (uint16_t*)part_out;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const f32x4 v = acc[j] * sc;
+        *(uint2*)(pb + po + 16 * j + 4 * grp) = uint2{f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16),
+                                                      f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16)};
+      }
+    }
     if (grp == 0) part_lse[pl] = L > 0.0f ? kLn2 * (m + __builtin_amdgcn_logf(L) - pbias) : kNegInf;
   }
 }
@@ -2585,11 +2597,12 @@ __device__ __forceinline__ void store_out2(void* out, int dtype, int64_t off, fl
 // first run's) and the first piece (id 2r) of each following run r.
 template <int LPC>
 __global__ __launch_bounds__(256) void pa_fp8_segment_merge_kernel(const pa_fp8_stream_args a,
-                                                                   const int32_t* segdesc, const float* part_out,
+                                                                   const int32_t* segdesc, const uint16_t* part_out,
                                                                    const float* part_lse) {
   constexpr int kCols = 64 / LPC;       // columns per wave
-  constexpr int kVec = 128 / LPC / 4;   // f32x4 per lane per piece
-  constexpr int kBatch = 16 / kVec;     // pieces whose loads are in flight together
+  constexpr int kVec = 128 / LPC / 4;   // 4-dim groups per lane per piece
+  constexpr int kBatch = 32 / kVec;     // pieces whose loads are in flight together
+  static_assert(kVec % 2 == 0, "a lane reads whole 16-byte pieces of a bf16 row");
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int ql = a.query_length, gqa = a.query_group_size, eq = ql * gqa;
@@ -2619,15 +2632,15 @@ __global__ __launch_bounds__(256) void pa_fp8_segment_merge_kernel(const pa_fp8_
       float M = kNegInf, tot = 0.0f;
       for (int i0 = 0; i0 < cnt; i0 += kBatch) {
         float l[kBatch];
-        f32x4 x[kBatch][kVec];
+        uint4 x[kBatch][kVec / 2];  // bf16 rows (store_piece)
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
           const int i = i0 + k < cnt ? i0 + k : cnt - 1;
           const int64_t pid = i == 0 ? pid0 : 2 * (int64_t)(w0 + i);
           l[k] = part_lse[pid * eq + e];
-          const f32x4* src = (const f32x4*)(part_out + (pid * eq + e) * kHead + d0);
+          const uint4* src = (const uint4*)(part_out + (pid * eq + e) * kHead + d0);
 #pragma unroll
-          for (int j = 0; j < kVec; ++j) x[k][j] = src[j];
+          for (int j = 0; j < kVec / 2; ++j) x[k][j] = src[j];
         }
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
@@ -2637,7 +2650,15 @@ __global__ __launch_bounds__(256) void pa_fp8_segment_merge_kernel(const pa_fp8_
           const float w = __expf(l[k] - Mn);
           tot = tot * fold + w;
 #pragma unroll
-          for (int j = 0; j < kVec; ++j) o[j] = o[j] * fold + x[k][j] * w;
+          for (int j = 0; j < kVec / 2; ++j) {
+            const uint4 u = x[k][j];
+            const f32x4 lo = {__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                              __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u)};
+            const f32x4 hi = {__uint_as_float(u.z << 16), __uint_as_float(u.z & 0xffff0000u),
+                              __uint_as_float(u.w << 16), __uint_as_float(u.w & 0xffff0000u)};
+            o[2 * j] = o[2 * j] * fold + lo * w;
+            o[2 * j + 1] = o[2 * j + 1] * fold + hi * w;
+          }
           M = Mn;
         }
       }
@@ -3700,7 +3721,8 @@ int check_stream_args(const pa_fp8_stream_args* a, bool generic_ok = false) {
   return PA_OK;
 }
 
-// Balanced workspace: pair descriptors, then partial lse, then partial rows.
+// Balanced workspace: pair descriptors, then partial lse (float32), then
+// partial rows (bf16), two of each per run.
 struct BalancedLayout {
   int64_t desc, lse, out, total;
 };
@@ -3710,7 +3732,7 @@ BalancedLayout balanced_layout(int B, int H, int eq, int nw) {
   l.desc = 0;
   l.lse = up((int64_t)B * H * 2 * 4);
   l.out = l.lse + up((int64_t)2 * nw * eq * 4);
-  l.total = l.out + (int64_t)2 * nw * eq * kHead * 4;
+  l.total = l.out + (int64_t)2 * nw * eq * kHead * 2;  // bf16 rows
   return l;
 }
 
@@ -3884,7 +3906,7 @@ int pa_fp8_decode_balanced(const pa_fp8_stream_args* a, void* workspace, int64_t
   unsigned char* ws = (unsigned char*)workspace;
   int32_t* desc = (int32_t*)(ws + l.desc);
   float* pl = (float*)(ws + l.lse);
-  float* po = (float*)(ws + l.out);
+  float* po = (float*)(ws + l.out);  // bf16 rows: store_piece<false> writes them as such
   hipError_t err = dispatch_balanced(*a, (hipStream_t)stream, desc, po, pl);
   return err == hipSuccess ? PA_OK : (int)err;
 }
@@ -3908,10 +3930,10 @@ int pa_fp8_merge_balanced(const pa_fp8_stream_args* a, const void* workspace, in
   const dim3 grid((unsigned)((rows + 3) / 4));
   if (narrow)
     hipLaunchKernelGGL(pa_fp8_segment_merge_kernel<16>, grid, dim3(256), 0, (hipStream_t)stream, *a,
-                       (const int32_t*)(ws + l.desc), (const float*)(ws + l.out), (const float*)(ws + l.lse));
+                       (const int32_t*)(ws + l.desc), (const uint16_t*)(ws + l.out), (const float*)(ws + l.lse));
   else
     hipLaunchKernelGGL(pa_fp8_segment_merge_kernel<4>, grid, dim3(256), 0, (hipStream_t)stream, *a,
-                       (const int32_t*)(ws + l.desc), (const float*)(ws + l.out), (const float*)(ws + l.lse));
+                       (const int32_t*)(ws + l.desc), (const uint16_t*)(ws + l.out), (const float*)(ws + l.lse));
   hipError_t err = hipGetLastError();
   return err == hipSuccess ? PA_OK : (int)err;
 }

@@ -113,7 +113,8 @@ def test_stream_worker_counts():
     with pytest.raises(RuntimeError):
         _lib.stream_workers(256, 4, 32, True)  # 128 columns: not supported
     ws = _lib.balanced_workspace_bytes(128, 8, 1, 4, 2048)
-    assert ws >= 128 * 8 * 8 + 2 * 2048 * 4 * 4 + 2 * 2048 * 4 * 128 * 4
+    # pair descriptors, float32 lse and bf16 partial rows, two of each per run
+    assert ws >= 128 * 8 * 8 + 2 * 2048 * 4 * 4 + 2 * 2048 * 4 * 128 * 2
 
 
 @pytest.mark.parametrize("struct,cname", [(_lib.PartitionArgs, "pa_fp8_partition_args"),
@@ -158,7 +159,7 @@ def test_static_scratch_entry_checks_before_any_gpu_call():
     sa.query_dtype = sa.output_dtype = _lib.DTYPE_BF16
     sa.stride_q_tok, sa.stride_q_head, sa.stride_out_tok, sa.stride_out_head = 64 * 128, 128, 64 * 128, 128
     sa.stride_k_block, sa.stride_k_head, sa.stride_v_block, sa.stride_v_head = 4 * 2048, 2048, 4 * 2048, 2048
-    sa.num_workers = 2048  # 64 columns x 2048 runs: 128 MiB of partial rows
+    sa.num_workers = 2048  # 64 columns x 2048 runs: 64 MiB of bf16 partial rows, plus their lse
     need = _lib.balanced_workspace_bytes(8, 4, 4, 16, 2048)
     assert need > 64 << 20
     assert lib.pa_fp8_decode_balanced_static(ctypes.byref(sa), None) == -9
