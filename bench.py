@@ -47,6 +47,22 @@ MALL_BYTES = 256 * 1024 * 1024
 WARMUP_SECONDS = 0.2  # minimum untimed warm-up before each timed loop
 
 
+def warm_up(run, min_steps: int) -> int:
+    """Untimed run(i) calls: at least min_steps of them and at least
+    WARMUP_SECONDS of GPU work (the clocks take a few milliseconds of load to
+    settle, longer than a few short steps).  Returns the number of calls."""
+    import torch
+
+    i, t0 = 0, time.perf_counter()
+    while i < min_steps or time.perf_counter() - t0 < WARMUP_SECONDS:
+        run(i)
+        i += 1
+        if i % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return i
+
+
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -263,16 +279,8 @@ def run_config(name: str, args) -> dict:
                                    case["softmax_scale"], ks, vs, sliding_window=cfg.sliding_window,
                                    block_tables=bt_arg, max_context_partition_num=P, **sw_scratch)
 
-    route, warm = None, 0
-    t_warm = time.perf_counter()
-    # W warm-up steps, and at least WARMUP_SECONDS of them: the GPU's clocks
-    # take a few milliseconds of load to settle, longer than W short steps.
-    while warm < args.warmup or time.perf_counter() - t_warm < WARMUP_SECONDS:
-        route = step(warm)
-        warm += 1
-        if warm % 8 == 0:
-            torch.cuda.synchronize()
-    torch.cuda.synchronize()
+    route = step(0)
+    warm = 1 + warm_up(step, args.warmup)
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -293,13 +301,7 @@ def run_config(name: str, args) -> dict:
                                        block_tables=bt_arg, max_context_partition_num=P, **sw_scratch))
     kernel_name, _ = calls[0].kernels()[0]
     decode = [c.kernels()[0][1] for c in calls]
-    t_warm = time.perf_counter()
-    i = 0
-    while i < max(3, args.warmup) or time.perf_counter() - t_warm < WARMUP_SECONDS:
-        calls[i % copies].launch()
-        i += 1
-        if i % 8 == 0:
-            torch.cuda.synchronize()
+    warm_up(lambda i: calls[i % copies].launch(), max(3, args.warmup))
     k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     k0.record(stream)
@@ -441,8 +443,7 @@ def run_rope_config(name: str, args) -> dict:
     calls = [launch.prepare(q, k, v, case["positions"], case["cos"], case["sin"], case["slot_mapping"],
                             case["key_cache"], case["value_cache"], q_out, k_out, cfg.num_tokens, case["k_scale"],
                             case["v_scale"]) for q, k, v in ins]
-    for i in range(max(3, args.warmup)):
-        calls[i % copies].launch()
+    warm = warm_up(lambda i: calls[i % copies].launch(), max(3, args.warmup))
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -459,7 +460,7 @@ def run_rope_config(name: str, args) -> dict:
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": warm,
         "ms_per_step": round(ms, 5),
         "us_per_step": round(ms * 1e3, 2),
         "pct_of_peak": round(100.0 * value / PEAK_HBM_GBPS, 2),
@@ -575,8 +576,7 @@ def run_qknr_config(name: str, args) -> dict:
     calls = [launcher.prepare(q.view(T, H, D), kv, case["kv_weight"], case["kv_weight"], case["cos_cache"],
                               case["sin_cache"], case["positions"], q_out, kv_out, q_scale, kv_scale, kv.stride(0), T)
              for q, kv in ins]
-    for i in range(max(3, args.warmup)):
-        calls[i % copies].launch()
+    warm = warm_up(lambda i: calls[i % copies].launch(), max(3, args.warmup))
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -593,7 +593,7 @@ def run_qknr_config(name: str, args) -> dict:
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": warm,
         "ms_per_step": round(ms, 5),
         "us_per_step": round(ms * 1e3, 2),
         "pct_of_peak": round(100.0 * value / PEAK_HBM_GBPS, 2),
@@ -699,8 +699,7 @@ def run_mla_config(name: str, args) -> dict:
         decode(i)
         mla_reduce_v1(so, sl, ri, rf, rp, 1, out)
 
-    for i in range(max(3, args.warmup)):
-        step(i)
+    warm = warm_up(step, max(3, args.warmup))
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -728,7 +727,7 @@ def run_mla_config(name: str, args) -> dict:
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": warm,
         "ms_per_step": round(ms, 5),
         "us_per_step": round(ms * 1e3, 2),
         "pct_of_peak": round(100.0 * value / PEAK_HBM_GBPS, 2),
