@@ -203,7 +203,8 @@ int pa_fp8_decode_reduce(const pa_fp8_reduce_args* args, void* hip_stream);
  * and workspace, merges the pieces of the pairs that were cut (and writes
  * zeros for pairs with no visible key).  The workspace
  * (pa_fp8_balanced_workspace_bytes bytes, 256-byte aligned) holds the
- * pieces' partials; it needs no initialisation.  num_seqs <= 1024.  No
+ * pieces' partials (pair descriptors, float32 lse, bf16 normalised rows:
+ * internal to the call); it needs no initialisation.  num_seqs <= 1024.  No
  * reference counterpart: it serves the small-block and flat-page routes of
  * pa_decode_ps_launch when the caller does not ask for the slot partials.
  */
