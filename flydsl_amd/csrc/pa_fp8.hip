@@ -1579,9 +1579,9 @@ __device__ __forceinline__ void zero_stale_values(LDS_AS unsigned char* v, int t
 
 // A finished piece's result for query column e (lane (grp, e % 16) holds
 // head dims 16 j + 4 grp .. + 3 in acc[j]): the output rows when the piece
-// is a whole (sequence, kv head), else a float32 partial row and its
-// natural-log lse (work list: rows target + qi; balanced split: partial id
-// target).  m is the column's base-2 maximum, L its sum of 2^(pbias + l - m),
+// is a whole (sequence, kv head), else a partial row and its natural-log
+// lse (work list: float32 rows target + qi; balanced split: bf16 row of
+// partial id target).  m is the column's base-2 maximum, L its sum of 2^(pbias + l - m),
 // and acc * vfin / L the normalised output.
 template <bool WORKLIST>
 __device__ __forceinline__ void store_piece(const pa_fp8_stream_args& a, void* __restrict__ output,
