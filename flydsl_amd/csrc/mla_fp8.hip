@@ -765,30 +765,50 @@ __global__ __launch_bounds__(256) void mla_fp8_reduce_kernel(const pa_mla_reduce
   if (p0 >= p1) return;
   const int row0 = min(max(a.reduce_final_map[2 * gidx], 0), a.num_rows);
   const int row1 = min(max(a.reduce_final_map[2 * gidx + 1], row0), a.num_rows);
+  // Pieces are merged in batches of kBatch whose loads (lse and the lane's
+  // 8 value dims) are all in flight together, with an online log-sum-exp:
+  // one round trip per batch instead of two per piece.  Pieces outside the
+  // split buffers or with lse -inf (no visible key) are skipped.
+  constexpr int kBatch = 8;
   for (int row = row0; row < row1; ++row) {
     const int r = row - row0;
-    float mx = kNegInf;
-    for (int i = p0; i < p1; ++i) {
-      const int pr = a.reduce_partial_map[i] + r;
-      if (pr < 0 || pr >= a.num_partial) continue;
-      mx = fmaxf(mx, a.split_lse[(int64_t)pr * kHeads + head]);
-    }
+    float mx = kNegInf, wsum = 0.f;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    float wsum = 0.f;
-    if (mx != kNegInf) {
-      for (int i = p0; i < p1; ++i) {
-        const int pr = a.reduce_partial_map[i] + r;
-        if (pr < 0 || pr >= a.num_partial) continue;
-        const int64_t prow = (int64_t)pr * kHeads + head;
-        const float wgt = __expf(a.split_lse[prow] - mx);
-        const f32x4* src = (const f32x4*)(a.split_output + prow * kVDim + 8 * lane);
-        const f32x4 x0 = src[0], x1 = src[1];
+    for (int i0 = p0; i0 < p1; i0 += kBatch) {
+      int64_t prow[kBatch];
+      bool ok[kBatch];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          acc[k] += wgt * x0[k];
-          acc[4 + k] += wgt * x1[k];
+      for (int k = 0; k < kBatch; ++k) {
+        const int pr = i0 + k < p1 ? a.reduce_partial_map[i0 + k] + r : -1;
+        ok[k] = pr >= 0 && pr < a.num_partial;
+        prow[k] = (int64_t)(ok[k] ? pr : 0) * kHeads + head;
+      }
+      float l[kBatch];
+      f32x4 x0[kBatch], x1[kBatch];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        l[k] = kNegInf;
+        x0[k] = x1[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (ok[k]) {  // wave-uniform
+          const f32x4* src = (const f32x4*)(a.split_output + prow[k] * kVDim + 8 * lane);
+          l[k] = a.split_lse[prow[k]];
+          x0[k] = src[0];
+          x1[k] = src[1];
         }
-        wsum += wgt;
+      }
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        if (l[k] == kNegInf) continue;
+        const float mn = fmaxf(mx, l[k]);
+        const float fold = mx == kNegInf ? 0.f : __expf(mx - mn);
+        const float w = __expf(l[k] - mn);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[j] = acc[j] * fold + w * x0[k][j];
+          acc[4 + j] = acc[4 + j] * fold + w * x1[k][j];
+        }
+        wsum = wsum * fold + w;
+        mx = mn;
       }
     }
     const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
