@@ -3339,24 +3339,41 @@ __global__ __launch_bounds__(256) void pa_fp8_generic_lse_reduce_kernel(const pa
   const int b = (int)(row / ((int64_t)eq * a.num_kv_heads));
   const int64_t sbase = (int64_t)b * a.stride_es_seq + (int64_t)h * a.stride_es_head + e;
   const int64_t tbase = (int64_t)b * a.stride_to_seq + (int64_t)h * a.stride_to_head + (int64_t)e * a.stride_to_group + lane;
-  float M = kNegInf;
-  for (int p = 0; p < a.num_partitions; ++p) M = fmaxf(M, a.max_logits[sbase + p * a.stride_es_part]);
-  float tot = 0.0f, o[NK];
+  // Slots in batches of kBatch whose loads are all in flight together,
+  // folded with a running maximum (empty slots, max -inf, are skipped).
+  constexpr int kBatch = 8;
+  float M = kNegInf, tot = 0.0f, o[NK];
 #pragma unroll
   for (int k = 0; k < NK; ++k) o[k] = 0.0f;
-  if (M != kNegInf) {
-    for (int p = 0; p < a.num_partitions; ++p) {
-      const float m = a.max_logits[sbase + p * a.stride_es_part];
-      if (m == kNegInf) continue;
-      const float w = a.exp_sums[sbase + p * a.stride_es_part] * __expf(m - M);
-      tot += w;
-      const int64_t off = tbase + (int64_t)p * a.stride_to_part;
+  for (int p0 = 0; p0 < a.num_partitions; p0 += kBatch) {
+    float m[kBatch], es[kBatch], x[kBatch][NK];
 #pragma unroll
-      for (int k = 0; k < NK; ++k) {
-        const float x = a.tmp_dtype == PA_DTYPE_F32 ? ((const float*)a.tmp_out)[off + 64 * k]
-                                                    : bf16_bits_to_f32(((const uint16_t*)a.tmp_out)[off + 64 * k]);
-        o[k] += w * x;
+    for (int i = 0; i < kBatch; ++i) {
+      const int p = p0 + i;
+      m[i] = kNegInf;
+      es[i] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < NK; ++k) x[i][k] = 0.0f;
+      if (p < a.num_partitions) {  // wave-uniform
+        m[i] = a.max_logits[sbase + p * a.stride_es_part];
+        es[i] = a.exp_sums[sbase + p * a.stride_es_part];
+        const int64_t off = tbase + (int64_t)p * a.stride_to_part;
+#pragma unroll
+        for (int k = 0; k < NK; ++k)
+          x[i][k] = a.tmp_dtype == PA_DTYPE_F32 ? ((const float*)a.tmp_out)[off + 64 * k]
+                                                : bf16_bits_to_f32(((const uint16_t*)a.tmp_out)[off + 64 * k]);
       }
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      if (m[i] == kNegInf) continue;
+      const float Mn = fmaxf(M, m[i]);
+      const float fold = M == kNegInf ? 0.0f : __expf(M - Mn);
+      const float w = es[i] * __expf(m[i] - Mn);
+      tot = tot * fold + w;
+#pragma unroll
+      for (int k = 0; k < NK; ++k) o[k] = o[k] * fold + w * x[i][k];
+      M = Mn;
     }
   }
   const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
