@@ -3408,20 +3408,38 @@ __global__ __launch_bounds__(256) void pa_fp8_generic_worklist_reduce_kernel(con
   if (qi >= qo1 - qo0) return;
   const int32_t* pmap = a.reduce_partial_map + p0;
   const int D = 64 * NK;
-  float M = kNegInf;
-  for (int i = 0; i < p1 - p0; ++i) M = fmaxf(M, a.partial_lse[(int64_t)(pmap[i] + qi) * a.stride_pl_row + qh]);
-  float tot = 0.0f, o[NK];
+  // Pieces in batches of kBatch whose loads are all in flight together,
+  // folded with a running maximum (pieces with lse -inf are skipped).
+  constexpr int kBatch = 8;
+  const int n = p1 - p0;
+  float M = kNegInf, tot = 0.0f, o[NK];
 #pragma unroll
   for (int k = 0; k < NK; ++k) o[k] = 0.0f;
-  if (M != kNegInf) {
-    for (int i = 0; i < p1 - p0; ++i) {
-      const float l = a.partial_lse[(int64_t)(pmap[i] + qi) * a.stride_pl_row + qh];
-      if (l == kNegInf) continue;
-      const float w = __expf(l - M);
-      tot += w;
-      const float* r = a.partial_output + (int64_t)(pmap[i] + qi) * a.stride_po_row + (int64_t)qh * D + lane;
+  for (int i0 = 0; i0 < n; i0 += kBatch) {
+    float l[kBatch], x[kBatch][NK];
 #pragma unroll
-      for (int k = 0; k < NK; ++k) o[k] += w * r[64 * k];
+    for (int j = 0; j < kBatch; ++j) {
+      l[j] = kNegInf;
+#pragma unroll
+      for (int k = 0; k < NK; ++k) x[j][k] = 0.0f;
+      if (i0 + j < n) {  // wave-uniform
+        const int64_t prow = (int64_t)pmap[i0 + j] + qi;
+        l[j] = a.partial_lse[prow * a.stride_pl_row + qh];
+        const float* r = a.partial_output + prow * a.stride_po_row + (int64_t)qh * D + lane;
+#pragma unroll
+        for (int k = 0; k < NK; ++k) x[j][k] = r[64 * k];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      if (l[j] == kNegInf) continue;
+      const float Mn = fmaxf(M, l[j]);
+      const float fold = M == kNegInf ? 0.0f : __expf(M - Mn);
+      const float w = __expf(l[j] - Mn);
+      tot = tot * fold + w;
+#pragma unroll
+      for (int k = 0; k < NK; ++k) o[k] = o[k] * fold + w * x[j][k];
+      M = Mn;
     }
   }
   const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
