@@ -66,7 +66,7 @@ def test_small_block_route_every_schedule(name):
 
 
 @pytest.mark.parametrize("name", ["d64_mtp_pt", "d256", "eq128", "eq128_d64_pt"])
-@pytest.mark.parametrize("P", [1, 3, 8])
+@pytest.mark.parametrize("P", [1, 3, 8, 13])
 def test_any_partition_count(name, P):
     case = build(name, block_size=64, ctx=[5, 64, 1000, 2049, 3000])
     ref = torch_oracle(case, float_out=False)
