@@ -166,3 +166,55 @@ def test_window_plan_matches_for_generic_heads():
     ref = torch_oracle(case, float_out=False)
     assert_parity(out, ref, "d256 window plan")
     assert plan.sw_partition_count(300, query_length=1) >= 2
+
+
+@pytest.mark.parametrize("name", ["d64_mtp_pt", "d256"])
+@pytest.mark.parametrize("partials", [False, True])
+def test_graph_capture_replays(name, partials):
+    """Graph replays of the generic kernels equal the eager call, with caller
+    partials (slot launch + reduce) and without them (owner launch, one pass
+    over each (sequence, kv head); capture without partials needs the owner
+    schedule, so it is forced for this small batch, otherwise the launcher
+    raises as the reference does); eager calls run between the replays."""
+    with tp.schedule("owner") if not partials else contextlib.nullcontext():
+        _graph_replays(name, partials)
+
+
+def _graph_replays(name, partials):
+    case = to_dev(build(name))
+    q = case["query"]
+    B, Hkv, D = len(case["context_lengths"]), case["key_cache"].shape[1], q.shape[-1]
+    eq = (q.shape[0] // B) * (q.shape[1] // Hkv)
+    P = 5
+    kw = {}
+    if partials:
+        kw = dict(exp_sums=torch.empty((B, Hkv, P, eq), device=q.device),
+                  max_logits=torch.empty((B, Hkv, P, eq), device=q.device),
+                  temporary_output=torch.empty((B, Hkv, P, eq, D), device=q.device, dtype=torch.bfloat16))
+    out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+    s = torch.cuda.Stream()
+
+    def call():
+        return pd.pa_decode_ps_launch(out, q, case["key_cache"], case["value_cache"], case["context_lengths"], None,
+                                      None, case["softmax_scale"], case["key_scale"], case["value_scale"],
+                                      block_tables=case["block_tables"], max_context_partition_num=P, **kw)
+
+    with torch.cuda.stream(s):
+        call()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            call()
+    torch.cuda.synchronize()
+    for i in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"{name} replay {i}"
+        with torch.cuda.stream(s):
+            call()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"{name} eager after replay {i}"
