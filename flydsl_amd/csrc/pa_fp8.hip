@@ -2886,6 +2886,14 @@ struct GenArgs {
 // list, bounds, and the query columns as fp8 hi + lo B operands scaled by a
 // power of two (prepare_query's scheme, for D dims).  Query row of column e:
 // orow + e / gqa.
+// First head dim of the 8 that lane group grp supplies to K-block blk of the
+// key product (v_mfma_f32_16x16x32_fp8_fp8, head dims along K).  The dot
+// product does not depend on how dims are dealt to the K slots, as long as
+// queries and keys agree: K-blocks 2 j and 2 j + 1 take the two halves of
+// 16-dim chunk 4 j + grp, so a lane reads each key row's chunk with one
+// 16-byte load.  D / 32 is even for every head size served here.
+__device__ __forceinline__ int gen_qk_dim(int blk, int grp) { return 64 * (blk >> 1) + 16 * grp + 8 * (blk & 1); }
+
 template <int D, bool PER_TOKEN>
 __device__ __forceinline__ bool gen_setup(GenCtx<D>& c, const GenArgs& a, int b, int h, int orow, int e0,
                                           int grp, int c16) {
@@ -2919,7 +2927,7 @@ __device__ __forceinline__ bool gen_setup(GenCtx<D>& c, const GenArgs& a, int b,
     i32x4 w = i32x4{0, 0, 0, 0};
     if (valid)
       w = *(const i32x4*)((const uint16_t*)a.query + (int64_t)(orow + qi) * a.stride_q_tok +
-                          (int64_t)(h * gqa + g) * a.stride_q_head + 32 * blk + 8 * grp);
+                          (int64_t)(h * gqa + g) * a.stride_q_head + gen_qk_dim(blk, grp));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t u = (uint32_t)w[i];
@@ -3012,12 +3020,18 @@ __device__ __forceinline__ void gen_load(GenChunk<D, PER_TOKEN>& ch, const GenCt
     ch.pg[tau] = gen_page(a, c.pages, c.last_page, tc + 16 * tau);
     ch.sb[tau] = (tc + 16 * tau) % bs;
   }
+  // key row c16 of each 16-token tile: the lane's 16-dim chunk 4 j + grp,
+  // one 16-byte load for K-blocks 2 j and 2 j + 1 (gen_qk_dim)
 #pragma unroll
   for (int tau = 0; tau < 2; ++tau) {
-    const uint8_t* kp = c.kbase + (int64_t)ch.pg[tau] * a.stride_k_block + (ch.sb[tau] + c16) * 16 + 8 * (grp & 1);
+    const uint8_t* kp = c.kbase + (int64_t)ch.pg[tau] * a.stride_k_block + (ch.sb[tau] + c16) * 16 +
+                        (int64_t)grp * bs * 16;
 #pragma unroll
-    for (int blk = 0; blk < D / 32; ++blk)
-      ch.kr[tau][blk] = *(const long*)(kp + (int64_t)(2 * blk + (grp >> 1)) * bs * 16);
+    for (int j = 0; j < D / 64; ++j) {
+      const i32x4 w = *(const i32x4*)(kp + (int64_t)(4 * j) * bs * 16);
+      ch.kr[tau][2 * j] = (long)((uint64_t)(uint32_t)w[0] | ((uint64_t)(uint32_t)w[1] << 32));
+      ch.kr[tau][2 * j + 1] = (long)((uint64_t)(uint32_t)w[2] | ((uint64_t)(uint32_t)w[3] << 32));
+    }
   }
   if (PER_TOKEN) {
 #pragma unroll
