@@ -2973,6 +2973,17 @@ __device__ __forceinline__ int gen_page(const GenArgs& a, const int32_t* pages, 
 }
 
 // Byte mask keeping the bytes of tokens [lo, hi) among the 4 tokens t .. t + 3.
+// Probability bytes of the key product's layout -- lane group g holds
+// tokens 4 g .. 4 g + 3 of each 16-token half, half 0 in the low word --
+// reordered to the value product's: lane group g supplies tokens
+// 8 (g >> 1) .. +7 of half g & 1.  Groups 0 and 1 (and 2 and 3) trade one
+// word: v_permlane16_swap leaves group 2k + h with (half h of group 2k,
+// half h of group 2k + 1).
+__device__ __forceinline__ long gen_pv_order(long p) {
+  const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)(uint64_t)p, (uint32_t)((uint64_t)p >> 32), false, false);
+  return (long)((uint64_t)r[0] | ((uint64_t)r[1] << 32));
+}
+
 __device__ __forceinline__ uint32_t gen_keep4(int t, int lo, int hi) {
   const int l = pa_min(pa_max(lo - t, 0), 4), u = pa_min(pa_max(hi - t, l), 4);
   const uint32_t below_u = u >= 4 ? ~0u : (1u << (8 * u)) - 1;
@@ -2990,7 +3001,7 @@ template <int D, bool PER_TOKEN>
 struct GenChunk {
   static constexpr bool VPF = D <= 128;
   long kr[2][D / 32];
-  uint32_t vw[D / 16][2];
+  uint64_t vw[D / 16];
   float ks[8], vs[8];
   int pg[2], sb[2];
 };
@@ -2998,16 +3009,17 @@ struct GenChunk {
 template <int D, bool PER_TOKEN>
 __device__ __forceinline__ void gen_load_values(GenChunk<D, PER_TOKEN>& ch, const GenCtx<D>& c, const GenArgs& a,
                                                 int grp, int c16) {
+  // head dim 16 j + c16, tokens 8 (grp >> 1) .. +7 of the chunk's half
+  // grp & 1: one 8-byte load per output tile (gen_pv_order)
   const int bs = a.block_size;
+  const bool half = grp & 1;  // selects, not indices (a runtime index would put ch in scratch)
+  const int sv = (half ? ch.sb[1] : ch.sb[0]) + 8 * (grp >> 1);
+  const uint8_t* vp = c.vbase + (int64_t)(half ? ch.pg[1] : ch.pg[0]) * a.stride_v_block;
 #pragma unroll
   for (int j = 0; j < D / 16; ++j) {
     const int d = 16 * j + c16;
-#pragma unroll
-    for (int tau = 0; tau < 2; ++tau) {
-      const int sv = ch.sb[tau] + 4 * grp;
-      const int64_t off = a.trans_v ? ((int64_t)(sv >> 4) * D + d) * 16 + (sv & 15) : (int64_t)d * bs + sv;
-      ch.vw[j][tau] = *(const uint32_t*)(c.vbase + (int64_t)ch.pg[tau] * a.stride_v_block + off);
-    }
+    const int64_t off = a.trans_v ? ((int64_t)(sv >> 4) * D + d) * 16 + (sv & 15) : (int64_t)d * bs + sv;
+    ch.vw[j] = *(const uint64_t*)(vp + off);
   }
 }
 
@@ -3127,18 +3139,20 @@ __device__ __forceinline__ void gen_chunk(GenState<D>& st, GenChunk<D, PER_TOKEN
   st.lsum = st.lsum * alpha + psum;
   long phi, plo;
   split8_fp8(pr, phi, plo);
-  // ---- value product: tokens 4 grp .. +3 and 16 + 4 grp .. +3 ----
-  uint32_t keep[2] = {~0u, ~0u};
+  // ---- value product: the lane supplies tokens 8 (grp >> 1) .. +7 of half
+  // grp & 1 (its value words), so the probabilities move to that order ----
+  uint64_t keep = ~0ull;
   const bool stale = tc < A || tc + 32 > B;
   if (stale) {
-#pragma unroll
-    for (int tau = 0; tau < 2; ++tau) keep[tau] = gen_keep4(tc + 16 * tau + 4 * grp, A, B);
+    const int t = tc + 16 * (grp & 1) + 8 * (grp >> 1);
+    keep = (uint64_t)gen_keep4(t, A, B) | ((uint64_t)gen_keep4(t + 4, A, B) << 32);
   }
+  const long ph = gen_pv_order(phi), pl = gen_pv_order(plo);
 #pragma unroll
   for (int j = 0; j < D / 16; ++j) {
-    const long vv = (long)((uint64_t)(ch.vw[j][0] & keep[0]) | ((uint64_t)(ch.vw[j][1] & keep[1]) << 32));
-    st.acc[j] = mfma_fp8(vv, phi, st.acc[j]);
-    st.acc[j] = mfma_fp8(vv, plo, st.acc[j]);
+    const long vv = (long)(ch.vw[j] & keep);
+    st.acc[j] = mfma_fp8(vv, ph, st.acc[j]);
+    st.acc[j] = mfma_fp8(vv, pl, st.acc[j]);
   }
 }
 
