@@ -3019,7 +3019,7 @@ __device__ __forceinline__ void gen_load_values(GenChunk<D, PER_TOKEN>& ch, cons
   for (int j = 0; j < D / 16; ++j) {
     const int d = 16 * j + c16;
     const int64_t off = a.trans_v ? ((int64_t)(sv >> 4) * D + d) * 16 + (sv & 15) : (int64_t)d * bs + sv;
-    ch.vw[j] = *(const uint64_t*)(vp + off);
+    ch.vw[j] = __builtin_nontemporal_load((const uint64_t*)(vp + off));
   }
 }
 
@@ -3040,7 +3040,7 @@ __device__ __forceinline__ void gen_load(GenChunk<D, PER_TOKEN>& ch, const GenCt
                         (int64_t)grp * bs * 16;
 #pragma unroll
     for (int j = 0; j < D / 64; ++j) {
-      const i32x4 w = *(const i32x4*)(kp + (int64_t)(4 * j) * bs * 16);
+      const i32x4 w = __builtin_nontemporal_load((const i32x4*)(kp + (int64_t)(4 * j) * bs * 16));
       ch.kr[tau][2 * j] = (long)((uint64_t)(uint32_t)w[0] | ((uint64_t)(uint32_t)w[1] << 32));
       ch.kr[tau][2 * j + 1] = (long)((uint64_t)(uint32_t)w[2] | ((uint64_t)(uint32_t)w[3] << 32));
     }
