@@ -185,7 +185,7 @@ __global__ __launch_bounds__(kRcThreads) void pa_rope_cache_kernel(const pa_fp8_
       p = p < 0 ? 0 : (p >= a.max_pos ? a.max_pos - 1 : p);  // never read outside the tables
       cs[j] = *(const i32x4*)((const uint16_t*)a.cos_cache + (int64_t)p * a.stride_cos_pos + cidx);
       sn[j] = *(const i32x4*)((const uint16_t*)a.sin_cache + (int64_t)p * a.stride_sin_pos + cidx);
-      x[j] = *(const i32x4*)((const uint16_t*)a.q + (int64_t)tc * a.stride_q_tok + (int64_t)rc * a.stride_q_head + 8 * l);
+      x[j] = __builtin_nontemporal_load((const i32x4*)((const uint16_t*)a.q + (int64_t)tc * a.stride_q_tok + (int64_t)rc * a.stride_q_head + 8 * l));
     }
     asm volatile("" ::: "memory");  // every load above is issued before the first wait
 #pragma unroll
@@ -223,9 +223,9 @@ __global__ __launch_bounds__(kRcThreads) void pa_rope_cache_kernel(const pa_fp8_
     slot = i64 ? ((const int32_t*)a.slot_mapping)[2 * (int64_t)tok] : ((const int32_t*)a.slot_mapping)[tok];
   }
   i32x4 x = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
-  if (live) {
-    x = *(const i32x4*)((const uint16_t*)a.k + (int64_t)tok * a.stride_k_tok + (int64_t)kh * a.stride_k_head + d0);
-    vv = *(const i32x4*)((const uint16_t*)a.v + (int64_t)tok * a.stride_v_tok + (int64_t)kh * a.stride_v_head + d0);
+  if (live) {  // rows are read once (non-temporal); the tables stay cached for other rows
+    x = __builtin_nontemporal_load((const i32x4*)((const uint16_t*)a.k + (int64_t)tok * a.stride_k_tok + (int64_t)kh * a.stride_k_head + d0));
+    vv = __builtin_nontemporal_load((const i32x4*)((const uint16_t*)a.v + (int64_t)tok * a.stride_v_tok + (int64_t)kh * a.stride_v_head + d0));
   }
   asm volatile("" ::: "memory");  // row loads issued before the tables wait on the positions
   p = p < 0 ? 0 : (p >= a.max_pos ? a.max_pos - 1 : p);
