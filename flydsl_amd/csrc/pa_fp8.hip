@@ -213,15 +213,17 @@ __device__ __forceinline__ float sum_over_groups(float v) {
 }
 
 // 16 bytes per lane from global memory straight into LDS (lane l fills
-// bytes 16l .. 16l+15 of ldst).  KV-cache pages and their scales are read
-// once per decode step: the loads carry the non-temporal hint (nt), which
-// streams them past the caches -- about 15% more HBM throughput for random
-// 2 KiB pages on MI355X than loads with the default policy.
+// bytes 16l .. 16l+15 of ldst).  KV-cache pages are read once per decode
+// step: the loads carry the non-temporal hint (nt), which streams them past
+// the caches -- about 15% more HBM throughput for random 2 KiB pages on
+// MI355X than loads with the default policy.
 __device__ __forceinline__ void lds_dma16(const void* gsrc, LDS_AS void* ldst) {
   __builtin_amdgcn_global_load_lds(gsrc, ldst, 16, 0, 2);
 }
 // Default cache policy: query rows, which several workgroups of one launch
-// may read.
+// may read, and per-token scales (at page size 16 a page-head's 64 bytes of
+// scales share a 128-byte line with the next kv head's, which another wave
+// reads; cached loads let that read hit).
 __device__ __forceinline__ void lds_dma16_cached(const void* gsrc, LDS_AS void* ldst) {
   __builtin_amdgcn_global_load_lds(gsrc, ldst, 16, 0, 0);
 }
@@ -1084,7 +1086,7 @@ __global__ __launch_bounds__(64 * WAVES) void pa_fp8_partition_kernel(const pa_f
         const int pg2 = BS16 ? (tt >= 16 ? p1 : p0) : p0;
         const int sidx = BS16 ? (tt & 15) : (tb & (bs - 1)) + tt;
         const float* base = lane < 8 ? ksbase : vsbase;
-        lds_dma16(base + (int64_t)pg2 * a.stride_ks_block + sidx, ss);
+        lds_dma16_cached(base + (int64_t)pg2 * a.stride_ks_block + sidx, ss);
       }
     }
   };
@@ -1550,7 +1552,7 @@ __device__ __forceinline__ void dma_chunk(const pa_fp8_stream_args& a, const flo
       const int pg2 = BS16 ? (tt >= 16 ? p1 : p0) : p0;
       const int sidx = BS16 ? (tt & 15) : (tb & (bs - 1)) + tt;
       const float* base = (lane < 8 ? key_scale : value_scale) + (int64_t)ih * a.stride_ks_head;
-      lds_dma16(base + (int64_t)pg2 * a.stride_ks_block + sidx, ss);
+      lds_dma16_cached(base + (int64_t)pg2 * a.stride_ks_block + sidx, ss);
     }
   }
 }
@@ -2376,7 +2378,7 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
     if (scale_wave && lane < 16) {
       const int pg = BS16 ? (tt >= 16 ? p1 : p0) : p0;
       const int sidx = BS16 ? 0 : (itb & (bs - 1));
-      lds_dma16(sbase + (uint64_t)(uint32_t)pg * ssb + sidx, sk + kKBytes + kVBytes);
+      lds_dma16_cached(sbase + (uint64_t)(uint32_t)pg * ssb + sidx, sk + kKBytes + kVBytes);
     }
     ++issued;
     ++ipos;
