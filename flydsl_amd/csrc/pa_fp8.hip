@@ -2591,20 +2591,20 @@ __device__ __forceinline__ void store_out2(void* out, int dtype, int64_t off, fl
 }
 
 // Merge of a balanced launch: one wave per (sequence, kv head, block of
-// 64 / LPC query columns); lane l takes column l % (64 / LPC) of the block
-// and 128 / LPC head dims, and folds that column's pieces itself (running
-// log-sum-exp), with every load of a batch of pieces issued before use.
-// Pairs a single run held whole were written by the decode; pairs with no
-// visible key get zeros; a cut pair's pieces are partial id segdesc[0] (the
-// first run's) and the first piece (id 2r) of each following run r.
-template <int LPC>
+// 4J query columns).  Load j of a piece reads columns 4j .. 4j+3 of the
+// block, 1 KiB of consecutive bf16 rows: lane l takes column 4j + l / 16 and
+// head dims 8(l % 16) .. +7.  Each lane folds the pieces of its J columns
+// (running log-sum-exp), with every load of a batch of pieces issued before
+// use.  Pairs a single run held whole were written by the decode; pairs with
+// no visible key get zeros; a cut pair's pieces are partial id segdesc[0]
+// (the first run's) and the first piece (id 2r) of each following run r.
+template <int J>
 __global__ __launch_bounds__(256) void pa_fp8_segment_merge_kernel(const pa_fp8_stream_args a,
                                                                    const int32_t* segdesc, const uint16_t* part_out,
                                                                    const float* part_lse) {
-  constexpr int kCols = 64 / LPC;       // columns per wave
-  constexpr int kVec = 128 / LPC / 4;   // 4-dim groups per lane per piece
-  constexpr int kBatch = 32 / kVec;     // pieces whose loads are in flight together
-  static_assert(kVec % 2 == 0, "a lane reads whole 16-byte pieces of a bf16 row");
+  constexpr int kCols = 4 * J;      // columns per wave
+  constexpr int kBatch = 16 / J;    // pieces whose loads are in flight together
+  static_assert(kHead == 128, "16 lanes cover one 256-byte bf16 row");
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int ql = a.query_length, gqa = a.query_group_size, eq = ql * gqa;
@@ -2621,59 +2621,79 @@ __global__ __launch_bounds__(256) void pa_fp8_segment_merge_kernel(const pa_fp8_
   int rl = 1;
   if (a.kv_indptr) rl = a.kv_indptr[b + 1] - a.kv_indptr[b];
   const int nb = rl > 0 ? pa_plan_seq_chunks(ctx, ql, a.sliding_window) : 0;
-  const int e = blk * kCols + lane % kCols;
-  const int d0 = 4 * kVec * (lane / kCols);
-  f32x4 o[kVec];
+  const int d0 = 8 * (lane & 15);
+  int e[J], ec[J];  // column, and the column whose row a lane past eq reads instead
 #pragma unroll
-  for (int i = 0; i < kVec; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < J; ++j) {
+    e[j] = blk * kCols + 4 * j + (lane >> 4);
+    ec[j] = e[j] < eq ? e[j] : eq - 1;
+  }
+  f32x4 o[J][2];
+#pragma unroll
+  for (int j = 0; j < J; ++j) o[j][0] = o[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   if (nb > 0) {
     const int pid0 = d[0], cnt = d[1];
     if (cnt <= 1) return;  // written by the decode
-    if (e < eq) {
-      const int w0 = pid0 >> 1;
-      float M = kNegInf, tot = 0.0f;
-      for (int i0 = 0; i0 < cnt; i0 += kBatch) {
-        float l[kBatch];
-        uint4 x[kBatch][kVec / 2];  // bf16 rows (store_piece)
+    const int w0 = pid0 >> 1;
+    float M[J], tot[J];
 #pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-          const int i = i0 + k < cnt ? i0 + k : cnt - 1;
-          const int64_t pid = i == 0 ? pid0 : 2 * (int64_t)(w0 + i);
-          l[k] = part_lse[pid * eq + e];
-          const uint4* src = (const uint4*)(part_out + (pid * eq + e) * kHead + d0);
+    for (int j = 0; j < J; ++j) {
+      M[j] = kNegInf;
+      tot[j] = 0.0f;
+    }
+    for (int i0 = 0; i0 < cnt; i0 += kBatch) {
+      float l[kBatch][J];
+      uint4 x[kBatch][J];  // bf16 rows (store_piece)
 #pragma unroll
-          for (int j = 0; j < kVec / 2; ++j) x[k][j] = src[j];
-        }
+      for (int k = 0; k < kBatch; ++k) {
+        const int i = i0 + k < cnt ? i0 + k : cnt - 1;
+        const int64_t pid = i == 0 ? pid0 : 2 * (int64_t)(w0 + i);
 #pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-          if (i0 + k >= cnt || l[k] == kNegInf) continue;
-          const float Mn = fmaxf(M, l[k]);
-          const float fold = M == kNegInf ? 0.0f : __expf(M - Mn);
-          const float w = __expf(l[k] - Mn);
-          tot = tot * fold + w;
-#pragma unroll
-          for (int j = 0; j < kVec / 2; ++j) {
-            const uint4 u = x[k][j];
-            const f32x4 lo = {__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
-                              __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u)};
-            const f32x4 hi = {__uint_as_float(u.z << 16), __uint_as_float(u.z & 0xffff0000u),
-                              __uint_as_float(u.w << 16), __uint_as_float(u.w & 0xffff0000u)};
-            o[2 * j] = o[2 * j] * fold + lo * w;
-            o[2 * j + 1] = o[2 * j + 1] * fold + hi * w;
-          }
-          M = Mn;
+        for (int j = 0; j < J; ++j) {
+          l[k][j] = part_lse[pid * eq + ec[j]];
+          x[k][j] = *(const uint4*)(part_out + (pid * eq + ec[j]) * kHead + d0);
         }
       }
-      const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
+      // Branch-free fold: a piece past cnt or with no visible key gets
+      // weight 0 (and fold 1 once the column has a maximum), which leaves the
+      // state unchanged.
 #pragma unroll
-      for (int j = 0; j < kVec; ++j) o[j] *= inv;
+      for (int k = 0; k < kBatch; ++k) {
+        const bool in = i0 + k < cnt;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          const float lk = in ? l[k][j] : kNegInf;
+          const float Mn = fmaxf(M[j], lk);
+          const float fold = M[j] == kNegInf ? 0.0f : __expf(M[j] - Mn);
+          const float w = lk == kNegInf ? 0.0f : __expf(lk - Mn);
+          tot[j] = tot[j] * fold + w;
+          const uint4 u = lk == kNegInf ? uint4{0u, 0u, 0u, 0u} : x[k][j];
+          const f32x4 lo = {__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                            __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u)};
+          const f32x4 hi = {__uint_as_float(u.z << 16), __uint_as_float(u.z & 0xffff0000u),
+                            __uint_as_float(u.w << 16), __uint_as_float(u.w & 0xffff0000u)};
+          o[j][0] = o[j][0] * fold + lo * w;
+          o[j][1] = o[j][1] * fold + hi * w;
+          M[j] = Mn;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const float inv = tot[j] > 0.0f ? 1.0f / tot[j] : 0.0f;
+      o[j][0] *= inv;
+      o[j][1] *= inv;
     }
   }
-  if (e >= eq) return;
-  const int qi = e / gqa, g = e - qi * gqa;
-  const int64_t off = (int64_t)(b * ql + qi) * a.stride_out_tok + (int64_t)(h * gqa + g) * a.stride_out_head + d0;
 #pragma unroll
-  for (int j = 0; j < kVec; ++j) store_out4(a.output, a.output_dtype, off + 4 * j, o[j]);
+  for (int j = 0; j < J; ++j) {
+    if (e[j] >= eq) continue;
+    const int qi = e[j] / gqa, g = e[j] - qi * gqa;
+    const int64_t off =
+        (int64_t)(b * ql + qi) * a.stride_out_tok + (int64_t)(h * gqa + g) * a.stride_out_head + d0;
+    store_out4(a.output, a.output_dtype, off, o[j][0]);
+    store_out4(a.output, a.output_dtype, off + 4, o[j][1]);
+  }
 }
 
 // Merge of work-list partials: one wave per (group, query, query head).
@@ -3986,7 +4006,8 @@ int pa_fp8_merge_balanced(const pa_fp8_stream_args* a, const void* workspace, in
   const int eq = a->query_length * a->query_group_size;
   const BalancedLayout l = balanced_layout(a->num_seqs, a->num_kv_heads, eq, a->num_workers);
   if (workspace_bytes < l.total) return PA_ERR_SHAPE;
-  // Up to 4 columns: 16 lanes per column (all lanes busy); else 4.
+  // Up to 4 columns: one load per piece covers them (all lanes busy); else
+  // 16 columns per wave, four loads per piece.
   const bool narrow = eq <= 4;
   const int cols = narrow ? 4 : 16;
   const int64_t rows = (int64_t)a->num_seqs * a->num_kv_heads * ((eq + cols - 1) / cols);
@@ -3994,7 +4015,7 @@ int pa_fp8_merge_balanced(const pa_fp8_stream_args* a, const void* workspace, in
   const unsigned char* ws = (const unsigned char*)workspace;
   const dim3 grid((unsigned)((rows + 3) / 4));
   if (narrow)
-    hipLaunchKernelGGL(pa_fp8_segment_merge_kernel<16>, grid, dim3(256), 0, (hipStream_t)stream, *a,
+    hipLaunchKernelGGL(pa_fp8_segment_merge_kernel<1>, grid, dim3(256), 0, (hipStream_t)stream, *a,
                        (const int32_t*)(ws + l.desc), (const uint16_t*)(ws + l.out), (const float*)(ws + l.lse));
   else
     hipLaunchKernelGGL(pa_fp8_segment_merge_kernel<4>, grid, dim3(256), 0, (hipStream_t)stream, *a,
