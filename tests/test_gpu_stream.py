@@ -108,6 +108,11 @@ BALANCED_CASES = {
     "gqa1": dict(batch=5, num_query_heads=8, num_kv_heads=8, ctx_range=(1, 2500)),
     "page64_ragged": dict(batch=7, block_size=64, ctx=[1, 64, 65, 900, 4000, 130, 2049], per_token=True),
     "uniform_data": dict(batch=6, dist="uniform", ctx_range=(1, 3000)),
+    # 6, 12 and 24 query columns: the merge's last 16-column block is part-filled
+    "mtp_ql3_gqa2": dict(batch=6, query_length=3, num_query_heads=4, num_kv_heads=2, ctx_range=(3, 3000)),
+    "mtp_ql3_gqa4_pt": dict(batch=6, query_length=3, num_query_heads=8, num_kv_heads=2, per_token=True,
+                            ctx=[3, 17, 300, 1900, 4100, 6000]),
+    "mtp_ql3_gqa8": dict(batch=5, query_length=3, num_query_heads=16, num_kv_heads=2, ctx_range=(3, 3500)),
     # cooperative workgroups (17..64 query columns per kv head)
     "coop_ql4_gqa16_pt_page64": dict(batch=6, query_length=4, num_query_heads=64, num_kv_heads=4, block_size=64,
                                      per_token=True, ctx_range=(4, 3000)),
