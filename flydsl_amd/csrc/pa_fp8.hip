@@ -709,11 +709,13 @@ __device__ __forceinline__ void unit_softmax_pv(WaveState<1>& s, const QueryTile
   };
   i32x8 VA[2];
   VA[0] = value_tile(0);
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     if (j + 1 < 8) VA[(j + 1) & 1] = value_tile(j + 1);
     mfma_k128_pair(s.acc[0][j], VA[j & 1], PH, PL);
   }
+  __builtin_amdgcn_s_setprio(0);
   s.lsum[0] = s.lsum[0] * alpha + psum * vmul;
 }
 
@@ -761,6 +763,10 @@ __device__ __forceinline__ void unit4_softmax_pv(WaveState<1>& s, const QueryTil
   f32x4 lg4[8];
   i32x8 KA[2];
   KA[0] = key_tile(0);
+  // The matrix blocks run at raised wave priority, so a wave that reaches
+  // them issues its MFMAs back to back while the other wave of the SIMD
+  // works through its softmax on the VALU.
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     if (t + 1 < 8) KA[(t + 1) & 1] = key_tile(t + 1);
@@ -768,6 +774,7 @@ __device__ __forceinline__ void unit4_softmax_pv(WaveState<1>& s, const QueryTil
     lg4[t] = mfma_fp8_k128(KA[t & 1], q.hi[0], zz);
     lg4[t] = mfma_fp8_k128(KA[t & 1], q.lo[0], lg4[t]);
   }
+  __builtin_amdgcn_s_setprio(0);
   float lg[32];
 #pragma unroll
   for (int t = 0; t < 8; ++t)
@@ -860,11 +867,13 @@ __device__ __forceinline__ void unit4_softmax_pv(WaveState<1>& s, const QueryTil
   };
   i32x8 VA[2];
   VA[0] = value_tile(0);
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     if (j + 1 < 8) VA[(j + 1) & 1] = value_tile(j + 1);
     mfma_k128_pair(s.acc[0][j], VA[j & 1], PH, PL);
   }
+  __builtin_amdgcn_s_setprio(0);
   s.lsum[0] = s.lsum[0] * alpha + psum * vmul;
 }
 
