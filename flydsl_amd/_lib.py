@@ -59,6 +59,7 @@ EXPORTED_SYMBOLS = (
     "pa_fp8_mla_reduce",
     "pa_fp8_mla_plan_sizes",
     "pa_fp8_mla_plan",
+    "pa_fp8_fnuz_to_fn",
 )
 
 _i32 = ctypes.c_int32
@@ -407,6 +408,8 @@ def load(path: Optional[str] = None) -> ctypes.CDLL:
     lib.pa_fp8_mla_plan_sizes.restype = ctypes.c_int
     lib.pa_fp8_mla_plan.argtypes = [_vp, _vp] + [ctypes.c_int] * 4 + [_vp] * 5 + [ctypes.POINTER(ctypes.c_int)] * 2
     lib.pa_fp8_mla_plan.restype = ctypes.c_int
+    lib.pa_fp8_fnuz_to_fn.argtypes = [_vp, _vp, _i64, _i64, _i64, _vp, _vp]
+    lib.pa_fp8_fnuz_to_fn.restype = ctypes.c_int
     if path is None:
         _LIB = lib
     return lib

@@ -825,7 +825,56 @@ __global__ __launch_bounds__(256) void mla_fp8_reduce_kernel(const pa_mla_reduce
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// One e4m3fnuz byte to e4m3fn by value.  fnuz(x) = fn(x) / 2 for every
+// non-special code, so a magnitude field >= 16 (exponent >= 2) loses one
+// exponent step, exact; below 16 both formats are linear in the field
+// (fnuz m * 2^-10, fn m * 2^-9), so the field halves, ties to even.
+__device__ __forceinline__ uint32_t fnuz_byte_to_fn(uint32_t b) {
+  const uint32_t mag = b & 0x7fu;
+  const uint32_t half = (mag >> 1) + (mag & (mag >> 1) & 1u);
+  const uint32_t out = (mag >= 16u ? mag - 8u : half) | (b & 0x80u);
+  return b == 0x80u ? 0x7fu : out;
+}
+
+// Thread t converts 16 bytes: chunk t % (row_bytes / 16) of destination row
+// t / (row_bytes / 16).
+__global__ __launch_bounds__(256) void fnuz_to_fn_kernel(const unsigned char* __restrict__ src,
+                                                         const int32_t* __restrict__ rows, int64_t num_rows,
+                                                         int64_t num_src_rows, int64_t row_bytes,
+                                                         unsigned char* __restrict__ dst) {
+  const int64_t chunks = row_bytes >> 4;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= num_rows * chunks) return;
+  const int64_t r = t / chunks, c = t - r * chunks;
+  int64_t sr = rows ? (int64_t)rows[r] : r;
+  sr = sr < 0 ? 0 : (sr >= num_src_rows ? num_src_rows - 1 : sr);
+  const i32x4 v = *(const i32x4*)(src + sr * row_bytes + 16 * c);
+  i32x4 o;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t w = (uint32_t)v[k];
+    o[k] = (int)(fnuz_byte_to_fn(w & 0xffu) | fnuz_byte_to_fn((w >> 8) & 0xffu) << 8 |
+                 fnuz_byte_to_fn((w >> 16) & 0xffu) << 16 | fnuz_byte_to_fn(w >> 24) << 24);
+  }
+  *(i32x4*)(dst + r * row_bytes + 16 * c) = o;
+}
+
 }  // namespace
+
+extern "C" int pa_fp8_fnuz_to_fn(const void* src, const int32_t* rows, int64_t num_rows, int64_t num_src_rows,
+                                 int64_t row_bytes, void* dst, void* stream) {
+  if (num_rows < 0 || num_src_rows < 0 || row_bytes <= 0 || row_bytes % 16) return PA_ERR_SHAPE;
+  if (num_rows == 0) return 0;
+  if (num_src_rows == 0) return PA_ERR_SHAPE;
+  if (!src || !dst) return PA_ERR_NULL_ARG;
+  if (!aligned16(src) || !aligned16(dst)) return PA_ERR_ALIGN;
+  const int64_t threads = num_rows * (row_bytes / 16);
+  const int64_t blocks = (threads + 255) / 256;
+  if (blocks > 0x7fffffffLL) return PA_ERR_SHAPE;
+  hipLaunchKernelGGL(fnuz_to_fn_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                     (const unsigned char*)src, rows, num_rows, num_src_rows, row_bytes, (unsigned char*)dst);
+  return (int)hipGetLastError();
+}
 
 extern "C" int pa_fp8_mla_decode(const pa_mla_decode_args* a, void* stream) {
   if (!a) return PA_ERR_NULL_ARG;

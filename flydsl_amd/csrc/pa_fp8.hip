@@ -3658,15 +3658,30 @@ hipError_t dispatch_ncg(const pa_fp8_partition_args& a, unsigned grid, hipStream
               : launch_partition<NCG, false, false, MULTI, WAVES>(a, grid, s);
 }
 
-// Compute units of the current device (cached per device; -1 if unknown).
-int device_cu_count() {
+// Device a launch on stream s runs on: the stream's own device, or the
+// current device for the null stream.
+hipError_t stream_device(hipStream_t s, int* dev) {
+  if (s == nullptr) return hipGetDevice(dev);
+  return hipStreamGetDevice(s, dev);
+}
+
+constexpr int kMaxDevices = 64;
+// Compute-unit counts by device, filled on first use.  Every writer stores
+// the same value for a device, so relaxed atomics suffice.
+std::atomic<int> g_cu_count[kMaxDevices];
+
+// Compute units of the device stream s runs on (-1 if unknown).
+int device_cu_count(hipStream_t s) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return -1;
-  static int cache[64];
-  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
+  if (stream_device(s, &dev) != hipSuccess) return -1;
+  const bool cached = dev >= 0 && dev < kMaxDevices;
+  if (cached) {
+    const int n = g_cu_count[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+  }
   int n = 0;
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return -1;
-  if (dev >= 0 && dev < 64) cache[dev] = n;
+  if (cached) g_cu_count[dev].store(n, std::memory_order_relaxed);
   return n;
 }
 
@@ -3742,8 +3757,8 @@ int coop_per_cu(int nw) { return coop_wgs_per_cu(nw, false); }
 
 // Workgroups of a work-list launch: as many as fit on the GPU at once (one
 // per CU for eight waves, three for three), at most one per bin.
-unsigned bin_workgroups(int bins) {
-  const int cus = device_cu_count();
+unsigned bin_workgroups(int bins, hipStream_t s) {
+  const int cus = device_cu_count(s);
   const int per_cu = kBinWaves >= 8 ? 1 : (kBinWaves >= 4 ? 2 : 3);
   const int fit = cus > 0 ? cus * per_cu : bins;
   return (unsigned)(bins < fit ? bins : fit);
@@ -3751,7 +3766,7 @@ unsigned bin_workgroups(int bins) {
 
 template <bool PT, bool BS16>
 hipError_t launch_bin(const pa_fp8_stream_args& a, hipStream_t s) {
-  hipLaunchKernelGGL((pa_fp8_bin_kernel<PT, BS16>), dim3(bin_workgroups(a.num_workers)), dim3(64 * kBinWaves), 0, s, a,
+  hipLaunchKernelGGL((pa_fp8_bin_kernel<PT, BS16>), dim3(bin_workgroups(a.num_workers, s)), dim3(64 * kBinWaves), 0, s, a,
                      a.block_tables, a.kv_indptr, a.context_lengths, a.key_scale, a.value_scale, a.work_indptr,
                      a.work_info, a.partition_indptr, a.partial_output, a.partial_lse, a.output);
   return hipGetLastError();
@@ -3838,15 +3853,15 @@ BalancedLayout balanced_layout(int B, int H, int eq, int nw) {
 constexpr int64_t kStaticScratchBytes = (int64_t)64 << 20;
 static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 
-constexpr int kMaxDevices = 64;
 std::atomic<void*> g_scratch_ptr[kMaxDevices];
 std::mutex g_scratch_mu;
 
-// Device address of the current device's scratch, looked up once per device
-// (with that device current) by its first call.
-int static_scratch(void** out) {
+// Device address of the scratch on the device stream s runs on, looked up
+// once per device with that device current (the caller's current device is
+// restored afterwards).
+int static_scratch(hipStream_t s, void** out) {
   int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
+  hipError_t e = stream_device(s, &dev);
   if (e != hipSuccess) return (int)e;
   if (dev < 0 || dev >= kMaxDevices) return PA_ERR_SHAPE;
   void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
@@ -3854,8 +3869,14 @@ int static_scratch(void** out) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
     if (p == nullptr) {
-      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      int cur = 0;
+      e = hipGetDevice(&cur);
       if (e != hipSuccess) return (int)e;
+      if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return (int)e;
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      const hipError_t back = cur != dev ? hipSetDevice(cur) : hipSuccess;
+      if (e != hipSuccess) return (int)e;
+      if (back != hipSuccess) return (int)back;
       if (p == nullptr) return PA_ERR_NULL_ARG;
       g_scratch_ptr[dev].store(p, std::memory_order_release);
     }
@@ -3920,7 +3941,7 @@ int pa_fp8_decode_partition(const pa_fp8_partition_args* a, void* stream) {
   hipError_t err;
   // A launch of at most one workgroup per CU runs 8-wave workgroups (one
   // per CU by LDS): twice the loads in flight per CU of a 4-wave one.
-  const int cus = ncg == 1 ? device_cu_count() : -1;
+  const int cus = ncg == 1 ? device_cu_count(s) : -1;
   if (cus > 0 && grid <= cus) {
     const bool multi8 = pa_min(spw, a->num_partitions) > 8;
     err = multi8 ? dispatch_ncg<1, true, 8>(*a, (unsigned)grid, s) : dispatch_ncg<1, false, 8>(*a, (unsigned)grid, s);
@@ -4042,7 +4063,7 @@ int pa_fp8_decode_balanced_static(const pa_fp8_stream_args* a, void* stream) {
   if (l.total > kStaticScratchBytes) return PA_ERR_SCRATCH;
   if (a->num_seqs == 0) return PA_OK;
   void* ws = nullptr;
-  rc = static_scratch(&ws);
+  rc = static_scratch((hipStream_t)stream, &ws);
   if (rc != PA_OK) return rc;
   rc = pa_fp8_decode_balanced(a, ws, l.total, stream);
   if (rc != PA_OK) return rc;
@@ -4141,7 +4162,9 @@ const char* pa_fp8_error_string(int code) {
     case PA_ERR_NULL_ARG: return "a required pointer is NULL";
     case PA_ERR_HEAD_SIZE: return "unsupported head_size (only 128)";
     case PA_ERR_BLOCK_SIZE: return "unsupported block_size (16 or a power of two in [32, 1024])";
-    case PA_ERR_GROUP: return "query_length * query_group_size must be in [1, 64]";
+    case PA_ERR_GROUP:
+      return "query_length * query_group_size above the entry point's limit (64 for the balanced decode and "
+             "pa_fp8_stream_workers; 16 for partition workgroups whose waves walk several slots)";
     case PA_ERR_DTYPE: return "unsupported dtype";
     case PA_ERR_SHAPE: return "invalid dimension";
     case PA_ERR_ALIGN: return "pointer or stride not 16-byte aligned";

@@ -121,19 +121,26 @@ def flydsl_mla_fwd_decode(
                     ("work_info_set", work_info_set)]:
         assert t.dtype == torch.int32, f"{name}: expected int32, got {t.dtype}"
     assert query.is_contiguous() and kv_buffer.is_contiguous(), "query and kv_buffer must be contiguous"
+    if num_seqs == 0:
+        return  # no query rows: nothing to decode or write
     if dev.type != "cuda":
         raise RuntimeError("flydsl_mla_fwd_decode: tensors must be on a GPU (the decode runs only in libpa_fp8.so)")
-    # gfx950's matrix cores read OCP e4m3fn only.  float8_e4m3fnuz inputs
-    # (gfx942's format, which the reference's launcher also accepts) are
-    # converted by value: exact for |x| >= 2^-6, smaller magnitudes rounded
-    # to a multiple of 2^-9 (e4m3fn's subnormal step; e4m3fnuz goes to
-    # 2^-10).  A compatibility path: the copy costs a pass over the tensor.
-    if query.dtype == _FNUZ:
-        query = query.to(torch.float32).to(torch.float8_e4m3fn)
-    if kv_buffer.dtype == _FNUZ:
-        kv_buffer = kv_buffer.to(torch.float32).to(torch.float8_e4m3fn)
 
     kv_idx = kv_page_indices.contiguous()
+    # gfx950's matrix cores read OCP e4m3fn only.  float8_e4m3fnuz inputs
+    # (gfx942's format, which the reference's launcher also accepts) are
+    # converted by value in one byte-wise pass of the library: exact for
+    # |x| >= 2^-6, smaller magnitudes rounded to a multiple of 2^-9 (e4m3fn's
+    # subnormal step; e4m3fnuz goes to 2^-10).  Only the kv rows the page
+    # list names are converted, into a buffer of that many rows that the
+    # decode then reads through the identity page list.
+    if query.dtype == _FNUZ:
+        query = _fnuz_rows_to_fn(query, None, query.shape)
+    if kv_buffer.dtype == _FNUZ:
+        n_idx = kv_idx.numel()
+        kv_buffer = _fnuz_rows_to_fn(kv_buffer, kv_idx, (max(n_idx, 1),) + tuple(kv_buffer.shape[1:]))
+        kv_idx = torch.arange(n_idx, dtype=torch.int32, device=dev)
+
     wi = work_info_set.contiguous().view(-1)
     wp = work_indptr.contiguous()
     a = _lib.MlaDecodeArgs()
@@ -156,6 +163,21 @@ def flydsl_mla_fwd_decode(
     a.precise_p = 1 if precise_p else 0
     rc = _lib.load().pa_fp8_mla_decode(ctypes.byref(a), _stream_handle(dev))
     _lib.check(rc, "pa_fp8_mla_decode")
+
+
+def _fnuz_rows_to_fn(src: torch.Tensor, rows: Optional[torch.Tensor], shape) -> torch.Tensor:
+    """e4m3fn tensor of ``shape`` (dense 576-byte rows): row i = the 576-byte
+    row ``rows[i]`` of ``src`` (row i when ``rows`` is None), converted from
+    e4m3fnuz by the library's byte-wise kernel."""
+    dst = torch.empty(shape, dtype=torch.float8_e4m3fn, device=src.device)
+    n = dst.numel() // QK_HEAD_DIM
+    if rows is not None:
+        n = min(n, rows.numel())
+    rc = _lib.load().pa_fp8_fnuz_to_fn(src.data_ptr(), rows.data_ptr() if rows is not None else None, n,
+                                      src.numel() // QK_HEAD_DIM, QK_HEAD_DIM, dst.data_ptr(),
+                                      _stream_handle(src.device))
+    _lib.check(rc, "pa_fp8_fnuz_to_fn")
+    return dst
 
 
 def get_mla_metadata_info_v1(

@@ -284,10 +284,20 @@ class PreparedDecode:
         self._sa = stream_args
         self._wra = worklist_reduce_args
         self._ws = workspace
-        self._stream = ctypes.c_void_p(stream.cuda_stream)
         self._keep = keepalive
+        if stream is None:  # an empty batch: nothing to launch, no library needed
+            self._stream = self._lib = None
+            self._kernels = []
+            return
+        self._stream = ctypes.c_void_p(stream.cuda_stream)
         self._lib = _lib.load()
         self._kernels = self.kernels()
+
+    @classmethod
+    def empty(cls, route: str) -> "PreparedDecode":
+        """The call for a batch of zero sequences: ``launch()`` issues no
+        device work and returns the route the call would have taken."""
+        return cls(route, None, ())
 
     def kernels(self):
         """The call's kernel launches in order, as (C entry point, thunk);
@@ -394,9 +404,10 @@ def prepare_pa_decode(
     per_token_kv = key_scale.dim() > 1
 
     batch_size = int(context_lengths.shape[0])
-    if batch_size == 0:
-        return "ps_small_block"
-    query_length = query.shape[0] // batch_size
+    # A batch of zero sequences decodes nothing (the reference divides by the
+    # batch size here); it is validated like any other call, then launches
+    # no kernel.
+    query_length = query.shape[0] // batch_size if batch_size else 0
     if query_length * batch_size != query.shape[0]:
         raise ValueError(f"query rows ({query.shape[0]}) must be a multiple of the batch size ({batch_size})")
     if num_query_heads % num_kv_heads != 0:
@@ -434,6 +445,12 @@ def prepare_pa_decode(
             raise ValueError("key_scale and value_scale must share strides with a contiguous token dimension")
     output_dtype = _get_output_dtype_code(output)
     _check_int32("context_lengths", context_lengths, dev)
+    if batch_size == 0:
+        if sliding_window > 0:
+            return PreparedDecode.empty(
+                "ps_sw_fused_partitioned" if max_context_partition_num == 1 else "ps_sw_partitioned")
+        return PreparedDecode.empty(
+            "ps_small_block" if block_size in _PA_DECODE_PS_SMALL_BLOCK_SIZES else "ps_split_reduce")
 
     s = stream or torch.cuda.current_stream(dev)
 

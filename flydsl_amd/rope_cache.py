@@ -149,6 +149,8 @@ def build_fused_rope_cache_module(
         a.apply_scale = int(bool(apply_scale))
         a.reuse_freqs_front_part = int(bool(reuse_freqs_front_part))
         a.index_i64 = int(pos_dtype == "i64")
+        if T == 0:  # no tokens: validated, nothing to launch
+            return PreparedRopeCache(a, None, tuple(tensors))
         s = stream if stream is not None else torch.cuda.current_stream(dev)
         return PreparedRopeCache(a, s, tuple(tensors))
 
@@ -166,9 +168,14 @@ class PreparedRopeCache:
 
     def __init__(self, args, stream, keepalive):
         self.args = args
-        self._stream = ctypes.c_void_p(stream.cuda_stream)
         self._keep = keepalive
+        if stream is None:  # zero tokens: launch() does nothing
+            self._stream = self._lib = None
+            return
+        self._stream = ctypes.c_void_p(stream.cuda_stream)
         self._lib = _lib.load()
 
     def launch(self) -> None:
+        if self._lib is None:
+            return
         _lib.check(self._lib.pa_fp8_rope_cache(ctypes.byref(self.args), self._stream), "pa_fp8_rope_cache")

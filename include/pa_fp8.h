@@ -4,10 +4,13 @@
  * The library (libpa_fp8.so) exports hand-written HIP kernels for the
  * split-context decode of the reference's `pa_decode_ps_launch` routes and a
  * few host-side planning helpers.  Every tensor is passed as a raw device
- * pointer plus element strides; the library never allocates device memory
- * and keeps no mutable global state (except the per-device address of the
- * static scratch of pa_fp8_decode_balanced_static, looked up once), so calls
- * are re-entrant and may be captured into a HIP graph when the caller
+ * pointer plus element strides; the library never allocates device memory.
+ * Its only mutable global state is two per-device caches, each entry written
+ * once with one value: the compute-unit count of a device and the address of
+ * pa_fp8_decode_balanced_static's scratch on it.  Both are keyed on the
+ * device of the stream a call is launched on (hipStreamGetDevice; the
+ * current device for the null stream), so calls are re-entrant, may target
+ * any device's stream, and may be captured into a HIP graph when the caller
  * preallocates every buffer.
  *
  * Return codes: 0 on success, a positive hipError_t value when the HIP
@@ -56,7 +59,15 @@ enum pa_fp8_error {
   PA_ERR_NULL_ARG = -1,       /* a required pointer is NULL */
   PA_ERR_HEAD_SIZE = -2,      /* head_size not 64, 128, 192 or 256 (balanced decode: not 128) */
   PA_ERR_BLOCK_SIZE = -3,     /* page size not 16 or a multiple of 32 up to 1024 */
-  PA_ERR_GROUP = -4,          /* balanced decode: ql * gqa above 64 */
+  PA_ERR_GROUP = -4,          /* ql * gqa above an entry point's limit:
+                               *  - pa_fp8_decode_balanced, pa_fp8_merge_balanced,
+                               *    pa_fp8_decode_balanced_static and
+                               *    pa_fp8_stream_workers: above 64;
+                               *  - pa_fp8_decode_partition at head_size 128 with
+                               *    min(slots_per_workgroup, num_partitions) > 4
+                               *    (a wave walks several slots): above 16.
+                               * The partition, reduce and work-list entry points
+                               * take any ql * gqa otherwise. */
   PA_ERR_DTYPE = -5,          /* unsupported query / output / partial dtype */
   PA_ERR_SHAPE = -6,          /* non-positive dimension or partition count */
   PA_ERR_ALIGN = -7,          /* a pointer or stride breaks 16-byte alignment */
@@ -550,6 +561,20 @@ int pa_fp8_mla_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, int num_
                     int max_works, int max_partials, int32_t* work_indptr, int32_t* work_info,
                     int32_t* reduce_indptr, int32_t* reduce_final_map, int32_t* reduce_partial_map,
                     int* num_groups, int* num_partials);
+
+/*
+ * float8_e4m3fnuz rows to float8_e4m3fn by value, gathered.  No counterpart
+ * in the reference (its gfx942 kernels read fnuz directly); it serves
+ * flydsl_mla_fwd_decode's fnuz inputs (kernels/mla_fwd_decode.py:52-53) on
+ * gfx950, whose matrix cores read e4m3fn only.  dst row i (row_bytes bytes)
+ * = convert(src row rows[i]) for i < num_rows; rows == NULL means row i.
+ * Row indices are clamped into [0, num_src_rows).  Conversion per byte:
+ * magnitudes >= 2^-6 exactly (exponent - 1), smaller ones rounded to the
+ * nearest multiple of 2^-9 (ties to even), fnuz NaN (0x80) -> e4m3fn NaN.
+ * row_bytes must be a multiple of 16 and src/dst 16-byte aligned.
+ */
+int pa_fp8_fnuz_to_fn(const void* src, const int32_t* rows, int64_t num_rows, int64_t num_src_rows,
+                      int64_t row_bytes, void* dst, void* hip_stream);
 
 /* Library identification and error names. */
 const char* pa_fp8_version(void);

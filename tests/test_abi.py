@@ -236,3 +236,16 @@ def test_head_sizes_and_column_counts_without_gpu():
     for d, rc in ((64, 0), (256, 0), (320, -2)):
         wr.head_size = d
         assert lib.pa_fp8_reduce_worklist(ctypes.byref(wr), None) == rc, d
+
+
+@pytest.mark.skipif(__import__("torch").cuda.is_available(), reason="the stand-in pointers would be launched on a GPU")
+def test_static_entry_device_lookup_without_gpu():
+    """pa_fp8_decode_balanced_static finds its scratch on the device of the
+    stream it is given (the current device for the null stream).  Without a
+    GPU that lookup is where a valid call stops: the runtime's error comes
+    back as a positive hipError_t, not a crash and not success."""
+    lib = _lib.load()
+    sa = _stream_stub(128, 1, 4)
+    rc = lib.pa_fp8_decode_balanced_static(ctypes.byref(sa), None)
+    assert rc > 0, rc
+    assert lib.pa_fp8_error_string(rc) not in (b"ok", b"")

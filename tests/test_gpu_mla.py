@@ -254,3 +254,69 @@ def test_large_softmax_scale():
         model = _quantized_softmax_out(r["q"], r["kv"], r["kvp"], r["kvi"], r["sm"], b)
         tol = np.abs(model - want[b]) + tolerance(wabs[b], want[b], False)
         assert np.all(np.abs(r["out"][b] - want[b]) <= tol), f"row {b}"
+
+
+def test_fnuz_conversion_every_code():
+    """The library's byte-wise e4m3fnuz -> e4m3fn pass equals torch's
+    conversion through float32 for all 256 codes (NaN to NaN), gathering
+    rows by index with out-of-range indices clamped."""
+    from flydsl_amd import mla_decode as md
+
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    src = codes.repeat(9).view(4, 576)  # four rows, every code 2.25 times per row
+    src[1] = src[1].roll(37)
+    src[2] = src[2].flip(0)
+    src = src.view(torch.float8_e4m3fnuz)
+    rows = torch.tensor([3, 0, -5, 2, 99, 1], dtype=torch.int32)
+    got = md._fnuz_rows_to_fn(src.to(DEV), rows.to(DEV), (6, 576)).cpu()
+    want = src.float()[rows.clamp(0, 3).long()].to(torch.float8_e4m3fn)
+    g, w = got.view(torch.uint8), want.view(torch.uint8)
+    nan = torch.isnan(want.float())
+    assert torch.equal(torch.isnan(got.float()), nan)
+    assert torch.equal(g[~nan], w[~nan])
+
+
+def test_fnuz_large_pool_converts_only_used_pages():
+    """A pool far larger than the pages the call uses: the fnuz path converts
+    only the listed rows (memory bounded by them, not by the pool) and
+    decodes as the e4m3fn tensors of the same values do."""
+    lens = [300, 5, 1200]
+    q, kv, qo_indptr, kv_indptr, kv_indices, last = make_case(lens, 31)
+    n_used = kv.size(0)
+    pool_pages = 400_000  # 230 MB of fp8 rows
+    big = torch.zeros(pool_pages, 1, 1, QK_HEAD_DIM, dtype=torch.float8_e4m3fnuz, device=DEV)
+    where = torch.randperm(pool_pages, generator=torch.Generator().manual_seed(5))[:n_used].to(torch.int32)
+    big[where.long().to(DEV)] = kv.float().to(torch.float8_e4m3fnuz).to(DEV)
+    idx_big = where[kv_indices.long()].to(DEV)
+    B = len(lens)
+
+    def decode(qd, kvd, kid):
+        sizes = get_mla_metadata_info_v1(B, 1, 128, FP8, FP8)
+        bufs = [torch.empty(s, dtype=t, device=DEV) for s, t in sizes]
+        meta, work_indptr, work_info, reduce_indptr, reduce_final_map, reduce_partial_map = bufs
+        get_mla_metadata_v1(qo_indptr.to(DEV), kv_indptr.to(DEV), last.to(DEV), 128, 1, False, meta, work_info,
+                            work_indptr, reduce_indptr, reduce_final_map, reduce_partial_map)
+        out = torch.empty(B, 128, V_HEAD_DIM, dtype=torch.bfloat16, device=DEV)
+        npart = reduce_partial_map.size(0)
+        so = torch.empty(npart, 1, 128, V_HEAD_DIM, device=DEV)
+        sl = torch.empty(npart, 1, 128, 1, device=DEV)
+        flydsl_mla_fwd_decode(qd, kvd, kid, work_indptr, work_info, out, so, sl, 1.0 / QK_HEAD_DIM ** 0.5)
+        mla_reduce_v1(so, sl, reduce_indptr, reduce_final_map, reduce_partial_map, 1, out)
+        torch.cuda.synchronize()
+        return out.cpu()
+
+    def peak_extra(fn, *args):
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated()
+        torch.cuda.reset_peak_memory_stats()
+        r = fn(*args)
+        return r, torch.cuda.max_memory_allocated() - base
+
+    qd, kvd, kid = q.to(DEV), kv.to(DEV), kv_indices.to(DEV)
+    want, fn_extra = peak_extra(decode, qd, kvd, kid)
+    qz = q.float().to(torch.float8_e4m3fnuz).to(DEV)
+    got, fnuz_extra = peak_extra(decode, qz, big, idx_big)
+    assert torch.equal(got, want)
+    # the work list and split rows are the same for both; the conversion adds
+    # the query and the listed rows (about 1 MB here), not the 230 MB pool
+    assert fnuz_extra - fn_extra < 8 << 20, (fnuz_extra, fn_extra)

@@ -197,6 +197,31 @@ def test_balanced_graph_capture_replays():
         assert torch.equal(out, eager), f"eager after replay {i}"
 
 
+def test_balanced_prepared_inside_capture_replays():
+    """A call prepared while capturing, with no partial buffers, takes its
+    workspace from the graph's memory pool (the reference raises here); the
+    graph replays to the eager result."""
+    case = to_dev(make_case(batch=9, ctx_range=(1, 5000), per_token=False, seed=141))
+    out = torch.empty(case["query"].shape, dtype=torch.bfloat16, device=DEV)
+    args = (case["query"], case["key_cache"], case["value_cache"], case["context_lengths"], None, None,
+            case["softmax_scale"], case["key_scale"], case["value_scale"])
+    with balanced():
+        route = pa_decode_ps_launch(out, *args, block_tables=case["block_tables"])
+    torch.cuda.synchronize()
+    eager = out.clone()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with balanced(), torch.cuda.stream(s), torch.cuda.graph(g, stream=s):
+        assert pa_decode_ps_launch(out, *args, block_tables=case["block_tables"]) == route
+    torch.cuda.synchronize()
+    for i in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+
+
 WORKLIST_CASES = {
     "gqa4": dict(batch=6, ctx=[1, 300, 1025, 4096, 7000, 2500]),
     "gqa8_pt": dict(batch=5, num_query_heads=16, num_kv_heads=2, per_token=True, ctx_range=(1, 6000)),

@@ -251,3 +251,71 @@ def test_unbuilt_head_size_is_not_implemented():
     c["query"] = torch.zeros(1, 8, 320, dtype=torch.bfloat16)
     with pytest.raises(NotImplementedError, match="head_dim=320"):
         prep(c, output=torch.empty(1, 8, 320, dtype=torch.bfloat16))
+
+
+def _empty_case(**kw):
+    """A validated case with its batch cut to zero sequences."""
+    case = make_case(batch=1, ctx=[10], seed=8, **kw)
+    hq, d = case["query"].shape[1:]
+    case["query"] = torch.zeros(0, hq, d, dtype=torch.bfloat16)
+    case["context_lengths"] = case["context_lengths"][:0]
+    case["block_tables"] = case["block_tables"][:0]
+    return case
+
+
+@pytest.mark.parametrize("kw,route", [
+    ({}, "ps_small_block"),
+    ({"sliding_window": 100}, "ps_sw_partitioned"),
+    ({"sliding_window": 100, "max_context_partition_num": 1}, "ps_sw_fused_partitioned"),
+])
+def test_empty_batch_launches_nothing(kw, route):
+    """Zero sequences: validated as usual, no kernel, the route string back
+    (the reference's launcher divides by the batch size there)."""
+    case = _empty_case()
+    call = prep(case, **kw)
+    assert call.kernels() == [] if call._lib is not None else call._kernels == []
+    assert call.launch() == route
+    out = torch.empty(0, 8, 128, dtype=torch.bfloat16)
+    got = pd.pa_decode_ps_launch(out, case["query"], case["key_cache"], case["value_cache"],
+                                 case["context_lengths"], None, None, case["softmax_scale"], case["key_scale"],
+                                 case["value_scale"], block_tables=case["block_tables"], stream=StubStream(), **kw)
+    assert got == route
+    # still validated: a query with rows but no sequences is an error
+    c = dict(case)
+    c["query"] = torch.zeros(2, 8, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="multiple of the batch size"):
+        prep(c, output=torch.empty(2, 8, 128, dtype=torch.bfloat16))
+
+
+def test_empty_batch_flat_route():
+    case = _empty_case(block_size=1024)
+    call = prep(case, block_tables=None, kv_page_indices=torch.zeros(0, dtype=torch.int32),
+                kv_indptr=torch.zeros(1, dtype=torch.int32))
+    assert call.launch() == "ps_split_reduce"
+
+
+def test_empty_inputs_of_the_other_launchers():
+    """The MLA decode, the KV-cache writer and the fused RMSNorm + RoPE
+    return cleanly for zero rows / tokens, before touching a device."""
+    from flydsl_amd import build_fused_rope_cache_module, flydsl_mla_fwd_decode, flydsl_qk_norm_rope_quant
+
+    fp8 = torch.float8_e4m3fn
+    q = torch.zeros(0, 128, 576, dtype=fp8)
+    kv = torch.zeros(4, 1, 1, 576, dtype=fp8)
+    i32 = torch.int32
+    assert flydsl_mla_fwd_decode(q, kv, torch.zeros(0, dtype=i32), torch.zeros(2, dtype=i32),
+                                 torch.zeros(1, 8, dtype=i32), torch.zeros(0, 128, 512, dtype=torch.bfloat16),
+                                 torch.zeros(0, 1, 128, 512), torch.zeros(0, 1, 128, 1), 0.1) is None
+
+    launch = build_fused_rope_cache_module(head_dim=128, num_q_heads=4, num_kv_heads=1, block_size=16,
+                                           flash_layout=False, apply_scale=True)
+    bf = torch.bfloat16
+    z = lambda *s, dt=bf: torch.zeros(*s, dtype=dt)  # noqa: E731
+    kc, vc = z(8, 1, 8, 16, 16, dt=fp8), z(8, 1, 1, 128, 16, dt=fp8)
+    launch(z(0, 4, 128), z(0, 1, 128), z(0, 1, 128), z(0, dt=i32), z(64, 64), z(64, 64), z(0, dt=i32), kc, vc,
+           z(0, 4, 128), z(0, 1, 128), 0, torch.ones(1), torch.ones(1))
+
+    qo, kvo, qs, kvs = flydsl_qk_norm_rope_quant(
+        z(0, 2 * 512), z(0, 512), torch.ones(512, dtype=bf), z(16, 32), z(16, 32), z(0, dt=torch.int64),
+        num_q_heads=2, head_dim=512, rope_head_dim=64, quant=True, quant_group_size=128)
+    assert qo.shape == (0, 2, 512) and kvo.shape == (0, 512) and qs.shape == (0, 2, 4) and kvs.shape == (0, 4)

@@ -106,3 +106,29 @@ def test_slot_pages_follow_block_table():
     assert plan.slot_pages(row, 15, 33, 16) == [7, 3, 9]
     assert plan.slot_pages(row, 64, 80, 16) == [4]
     assert plan.slot_pages(row, 5, 5, 16) == []
+
+
+# Hand-computed from the reference's slot formula (kernels/pa_decode_fp8.py:
+# 2311-2320): nt = cdiv(ctx, 256) tiles in runs of pps = cdiv(nt, P), slot z
+# taking tiles [z*pps, min((z+1)*pps, nt)); trailing slots stay empty.  A
+# balanced split (nt // P tiles, one more for the first nt % P slots) gives
+# different ranges for each of these contexts.
+KNOWN_SLOTS = {
+    # 12 tiles, runs of 2: slots 0-5 two tiles each (the last ending at 3000), 6-7 empty
+    (3000, 8): [(0, 512), (512, 1024), (1024, 1536), (1536, 2048), (2048, 2560), (2560, 3000), (0, 0), (0, 0)],
+    # 5 tiles, runs of 1: five one-tile slots, three empty
+    (1027, 8): [(0, 256), (256, 512), (512, 768), (768, 1024), (1024, 1027), (0, 0), (0, 0), (0, 0)],
+    # 157 tiles, runs of 20: seven full runs, the last slot 17 tiles
+    (40000, 8): [(20 * 256 * z, 20 * 256 * (z + 1)) for z in range(7)] + [(35840, 40000)],
+    # 3 tiles over 2 slots: runs of 2, then one
+    (600, 2): [(0, 512), (512, 600)],
+    # 9 tiles over 4 slots: runs of 3, the last slot empty
+    (2100, 4): [(0, 768), (768, 1536), (1536, 2100), (0, 0)],
+}
+
+
+@pytest.mark.parametrize("ctx,P", sorted(KNOWN_SLOTS))
+def test_slot_ranges_known_answers(ctx, P):
+    want = KNOWN_SLOTS[(ctx, P)]
+    assert [plan.slot_token_range(ctx, P, z) for z in range(P)] == want
+    assert [_lib.plan_slot(ctx, P, z, 0, 1) for z in range(P)] == want

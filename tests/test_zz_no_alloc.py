@@ -77,3 +77,40 @@ def test_static_scratch_refuses_oversized_calls():
     sa.num_workers = 4096  # 64 columns: 256 MiB of partial rows
     rc = _lib.load().pa_fp8_decode_balanced_static(ctypes.byref(sa), None)
     assert rc == -9
+
+
+def test_static_scratch_on_a_side_stream_and_in_a_graph():
+    """The entry point keys its scratch on the stream's device (here a
+    non-default stream, so the library asks the stream), and a HIP graph
+    that captured it replays to the same bits.  The capture follows an
+    uncaptured call: a device's first call looks the scratch address up."""
+    case = make_case(num_query_heads=32, num_kv_heads=8, batch=6, per_token=True, ctx=[1, 40, 3000, 700, 5000, 2],
+                     seed=204)
+    want = _call(case, static=False)
+    d = {k: (v.to(DEV) if isinstance(v, torch.Tensor) else v) for k, v in case.items()}
+    out = torch.full(d["query"].shape, float("nan"), dtype=torch.bfloat16, device=DEV)
+    sa = pd._stream_args(out, d["query"], d["key_cache"], d["value_cache"], d["context_lengths"], d["block_tables"],
+                         None, d["softmax_scale"], d["key_scale"], d["value_scale"], True, True, "bf16",
+                         _lib.DTYPE_BF16)
+    sa.num_workers = _lib.stream_workers(pd._cu_count(), 1, 4, True)
+    lib = _lib.load()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    print("[no-alloc] side stream", flush=True)
+    with torch.cuda.stream(side):
+        _lib.check(lib.pa_fp8_decode_balanced_static(ctypes.byref(sa), ctypes.c_void_p(side.cuda_stream)),
+                   "pa_fp8_decode_balanced_static")
+    side.synchronize()
+    assert torch.equal(out.cpu(), want)
+    print("[no-alloc] graph capture", flush=True)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        rc = lib.pa_fp8_decode_balanced_static(ctypes.byref(sa), cap)
+    _lib.check(rc, "pa_fp8_decode_balanced_static (captured)")
+    for i in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), want), f"replay {i}"
