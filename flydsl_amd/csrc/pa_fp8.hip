@@ -3031,6 +3031,10 @@ __device__ __forceinline__ uint32_t gen_keep4(int t, int lo, int hi) {
 template <int D, bool PER_TOKEN>
 struct GenChunk {
   static constexpr bool VPF = D <= 128;
+  // Two chunk buffers (the next chunk's keys in flight during this one's
+  // arithmetic) up to D = 256; above, one buffer, so that the accumulators,
+  // query operands and one chunk's operands fit the register file.
+  static constexpr bool KPF = D <= 256;
   long kr[2][D / 32];
   uint64_t vw[D / 16];
   float ks[8], vs[8];
@@ -3198,8 +3202,16 @@ __device__ void gen_range(GenState<D>& st, const GenCtx<D>& c, const GenArgs& a,
   const int A = pa_max(t0, c.lo_all), B = pa_min(t1, c.hi_all);
   if (B <= A) return;
   const int vis_lo = pa_max(c.vis_lo, t0), vis_hi = pa_min(c.vis_hi, t1);
-  GenChunk<D, PER_TOKEN> ch0, ch1;
   int tc = A & ~31;
+  if constexpr (!GenChunk<D, PER_TOKEN>::KPF) {
+    GenChunk<D, PER_TOKEN> ch;
+    for (; tc < B; tc += 32) {
+      gen_load(ch, c, a, tc, grp, c16);
+      gen_chunk(st, ch, c, a, tc, t0, t1, A, B, vis_lo, vis_hi, grp, c16);
+    }
+    return;
+  }
+  GenChunk<D, PER_TOKEN> ch0, ch1;
   gen_load(ch0, c, a, tc, grp, c16);
   while (true) {
     const bool more1 = tc + 32 < B;
@@ -3515,8 +3527,9 @@ __global__ __launch_bounds__(256) void pa_fp8_generic_worklist_reduce_kernel(con
   }
 }
 
-// Host side: the generic path takes D = 64 .. 256 and any column count.
-static bool generic_head_ok(int d) { return d == 64 || d == 128 || d == 192 || d == 256; }
+// Host side: the generic path takes every multiple of 64 from 64 to 512 and
+// any column count.
+static bool generic_head_ok(int d) { return d >= 64 && d <= 512 && d % 64 == 0; }
 
 template <int D, bool PT>
 static hipError_t launch_generic_partition(const GenArgs& g, dim3 grid, dim3 block, hipStream_t s) {
@@ -3534,13 +3547,22 @@ static hipError_t launch_generic_worklist(const GenArgs& g, dim3 grid, dim3 bloc
   return hipGetLastError();
 }
 
+template <int D, typename F>
+static hipError_t generic_call(bool pt, F&& f) {
+  return pt ? f(std::integral_constant<int, D>{}, std::true_type{}) : f(std::integral_constant<int, D>{}, std::false_type{});
+}
+
 template <typename F>
 static hipError_t generic_dispatch(int d, bool pt, F&& f) {
   switch (d) {
-    case 64: return pt ? f(std::integral_constant<int, 64>{}, std::true_type{}) : f(std::integral_constant<int, 64>{}, std::false_type{});
-    case 128: return pt ? f(std::integral_constant<int, 128>{}, std::true_type{}) : f(std::integral_constant<int, 128>{}, std::false_type{});
-    case 192: return pt ? f(std::integral_constant<int, 192>{}, std::true_type{}) : f(std::integral_constant<int, 192>{}, std::false_type{});
-    default: return pt ? f(std::integral_constant<int, 256>{}, std::true_type{}) : f(std::integral_constant<int, 256>{}, std::false_type{});
+    case 64: return generic_call<64>(pt, f);
+    case 128: return generic_call<128>(pt, f);
+    case 192: return generic_call<192>(pt, f);
+    case 256: return generic_call<256>(pt, f);
+    case 320: return generic_call<320>(pt, f);
+    case 384: return generic_call<384>(pt, f);
+    case 448: return generic_call<448>(pt, f);
+    default: return generic_call<512>(pt, f);
   }
 }
 
@@ -3981,11 +4003,16 @@ int pa_fp8_decode_reduce(const pa_fp8_reduce_args* a, void* stream) {
   const int64_t grid = (rows + 3) / 4;
   if (grid > 0x7fffffffLL) return PA_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
+  const dim3 g1((unsigned)grid), b1(256);
   switch (a->head_size) {
-    case 64: hipLaunchKernelGGL(pa_fp8_generic_lse_reduce_kernel<1>, dim3((unsigned)grid), dim3(256), 0, s, *a); break;
-    case 192: hipLaunchKernelGGL(pa_fp8_generic_lse_reduce_kernel<3>, dim3((unsigned)grid), dim3(256), 0, s, *a); break;
-    case 256: hipLaunchKernelGGL(pa_fp8_generic_lse_reduce_kernel<4>, dim3((unsigned)grid), dim3(256), 0, s, *a); break;
-    default: hipLaunchKernelGGL(pa_fp8_lse_reduce_kernel, dim3((unsigned)grid), dim3(256), 0, s, *a); break;
+    case 64: hipLaunchKernelGGL(pa_fp8_generic_lse_reduce_kernel<1>, g1, b1, 0, s, *a); break;
+    case 192: hipLaunchKernelGGL(pa_fp8_generic_lse_reduce_kernel<3>, g1, b1, 0, s, *a); break;
+    case 256: hipLaunchKernelGGL(pa_fp8_generic_lse_reduce_kernel<4>, g1, b1, 0, s, *a); break;
+    case 320: hipLaunchKernelGGL(pa_fp8_generic_lse_reduce_kernel<5>, g1, b1, 0, s, *a); break;
+    case 384: hipLaunchKernelGGL(pa_fp8_generic_lse_reduce_kernel<6>, g1, b1, 0, s, *a); break;
+    case 448: hipLaunchKernelGGL(pa_fp8_generic_lse_reduce_kernel<7>, g1, b1, 0, s, *a); break;
+    case 512: hipLaunchKernelGGL(pa_fp8_generic_lse_reduce_kernel<8>, g1, b1, 0, s, *a); break;
+    default: hipLaunchKernelGGL(pa_fp8_lse_reduce_kernel, g1, b1, 0, s, *a); break;
   }
   hipError_t err = hipGetLastError();
   return err == hipSuccess ? PA_OK : (int)err;
@@ -4107,6 +4134,10 @@ int pa_fp8_reduce_worklist(const pa_fp8_worklist_reduce_args* a, void* stream) {
     case 64: hipLaunchKernelGGL(pa_fp8_generic_worklist_reduce_kernel<1>, grid, dim3(256), 0, s, *a); break;
     case 192: hipLaunchKernelGGL(pa_fp8_generic_worklist_reduce_kernel<3>, grid, dim3(256), 0, s, *a); break;
     case 256: hipLaunchKernelGGL(pa_fp8_generic_worklist_reduce_kernel<4>, grid, dim3(256), 0, s, *a); break;
+    case 320: hipLaunchKernelGGL(pa_fp8_generic_worklist_reduce_kernel<5>, grid, dim3(256), 0, s, *a); break;
+    case 384: hipLaunchKernelGGL(pa_fp8_generic_worklist_reduce_kernel<6>, grid, dim3(256), 0, s, *a); break;
+    case 448: hipLaunchKernelGGL(pa_fp8_generic_worklist_reduce_kernel<7>, grid, dim3(256), 0, s, *a); break;
+    case 512: hipLaunchKernelGGL(pa_fp8_generic_worklist_reduce_kernel<8>, grid, dim3(256), 0, s, *a); break;
     default: hipLaunchKernelGGL(pa_fp8_worklist_reduce_kernel, grid, dim3(256), 0, s, *a); break;
   }
   hipError_t err = hipGetLastError();
@@ -4160,7 +4191,7 @@ const char* pa_fp8_error_string(int code) {
   switch (code) {
     case PA_OK: return "ok";
     case PA_ERR_NULL_ARG: return "a required pointer is NULL";
-    case PA_ERR_HEAD_SIZE: return "unsupported head_size (only 128)";
+    case PA_ERR_HEAD_SIZE: return "unsupported head_size (a multiple of 64 in [64, 512]; the balanced decode: 128)";
     case PA_ERR_BLOCK_SIZE: return "unsupported block_size (16 or a power of two in [32, 1024])";
     case PA_ERR_GROUP:
       return "query_length * query_group_size above the entry point's limit (64 for the balanced decode and "

@@ -235,7 +235,7 @@ def _schedule(route: str, batch: int, kv_heads: int, P: int, eqgs: int, capacity
 BALANCED_MAX_COLUMNS = 4
 # Head sizes the library decodes (128 on the tuned kernels, the others and
 # more than COOP_MAX_COLUMNS columns per kv head on the generic ones).
-GENERIC_HEAD_SIZES = (64, 128, 192, 256)
+GENERIC_HEAD_SIZES = tuple(range(64, 513, 64))  # 64, 128, ..., 512
 BALANCED_MAX_SEQS = 1024
 # Per-wave streaming decode: one 16-column query block; cooperative beyond.
 STREAM_MAX_COLUMNS = 16
@@ -418,7 +418,8 @@ def prepare_pa_decode(
         raise ValueError(f"Unsupported head_dim={head_size}; must be a multiple of 64.")
     if head_size not in GENERIC_HEAD_SIZES:
         raise NotImplementedError(
-            f"head_dim={head_size} is not built; this library supports head_dim in {GENERIC_HEAD_SIZES}.")
+            f"head_dim={head_size} is not built; this library supports head_dim in {GENERIC_HEAD_SIZES} "
+            "(larger heads would not fit one wave's register file).")
     eqgs = query_length * query_group_size
     # head sizes other than 128 and more than 64 query columns per kv head
     # run on the library's generic kernels: no balanced split for them

@@ -30,12 +30,12 @@
  *   output       [B * ql, Hq, D]            bf16, f16 or float32
  * where gqa = Hq / Hkv and P is the number of context slots.
  *
- * Head sizes D = 64, 128, 192 and 256 and any ql * gqa are decoded by the
- * partition, reduce and work-list entry points; D = 128 with up to 64
- * query columns per kv head runs on the tuned kernels, every other shape on
- * generic ones (one wave per 16-column block, K and V read straight into
- * MFMA operands) with the same outputs.  The balanced decode takes D = 128
- * and up to 64 columns only.
+ * Head sizes D = 64, 128, ..., 512 (every multiple of 64 up to 512) and any
+ * ql * gqa are decoded by the partition, reduce and work-list entry points;
+ * D = 128 with up to 64 query columns per kv head runs on the tuned
+ * kernels, every other shape on generic ones (one wave per 16-column block,
+ * K and V read straight into MFMA operands) with the same outputs.  The
+ * balanced decode takes D = 128 and up to 64 columns only.
  */
 #ifndef PA_FP8_H
 #define PA_FP8_H
@@ -57,7 +57,7 @@ enum pa_fp8_dtype {
 enum pa_fp8_error {
   PA_OK = 0,
   PA_ERR_NULL_ARG = -1,       /* a required pointer is NULL */
-  PA_ERR_HEAD_SIZE = -2,      /* head_size not 64, 128, 192 or 256 (balanced decode: not 128) */
+  PA_ERR_HEAD_SIZE = -2,      /* head_size not a multiple of 64 in [64, 512] (balanced decode: not 128) */
   PA_ERR_BLOCK_SIZE = -3,     /* page size not 16 or a multiple of 32 up to 1024 */
   PA_ERR_GROUP = -4,          /* ql * gqa above an entry point's limit:
                                *  - pa_fp8_decode_balanced, pa_fp8_merge_balanced,

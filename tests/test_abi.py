@@ -198,8 +198,10 @@ def test_head_sizes_and_column_counts_without_gpu():
     # work-list pointer check (NULL here)
     for d, ql, gqa in ((64, 1, 4), (192, 2, 8), (256, 1, 16), (128, 8, 16), (256, 4, 32)):
         assert lib.pa_fp8_decode_worklist(ctypes.byref(_stream_stub(d, ql, gqa)), None) == -1, (d, ql, gqa)
-    for d in (96, 320, 512):
+    for d in (96, 576, 1024):
         assert lib.pa_fp8_decode_worklist(ctypes.byref(_stream_stub(d, 1, 4)), None) == -2, d
+    for d in (320, 384, 448, 512):
+        assert lib.pa_fp8_decode_worklist(ctypes.byref(_stream_stub(d, 1, 4)), None) == -1, d
     # partition: nothing to do for an empty batch once the shape is accepted
     pa = _lib.PartitionArgs()
     pa.abi_version = _lib.ABI_VERSION
@@ -210,7 +212,7 @@ def test_head_sizes_and_column_counts_without_gpu():
     pa.block_size, pa.num_blocks, pa.max_blocks_per_seq = 16, 64, 4
     pa.num_seqs, pa.num_kv_heads, pa.query_length, pa.query_group_size = 0, 2, 8, 16
     pa.query_dtype = pa.tmp_dtype = _lib.DTYPE_BF16
-    for d in (64, 128, 192, 256):
+    for d in (64, 128, 192, 256, 320, 384, 448, 512):
         pa.head_size = d
         pa.stride_q_tok, pa.stride_q_head = 32 * d, d
         pa.stride_to_group, pa.stride_to_part = d, 128 * d
@@ -224,7 +226,7 @@ def test_head_sizes_and_column_counts_without_gpu():
         setattr(ra, f, 4096)
     ra.num_seqs, ra.num_kv_heads, ra.num_partitions, ra.query_length, ra.query_group_size = 0, 2, 3, 8, 16
     ra.output_dtype = ra.tmp_dtype = _lib.DTYPE_BF16
-    for d, rc in ((64, 0), (192, 0), (256, 0), (96, -2)):
+    for d, rc in ((64, 0), (192, 0), (256, 0), (320, 0), (512, 0), (96, -2), (576, -2)):
         ra.head_size = d
         assert lib.pa_fp8_decode_reduce(ctypes.byref(ra), None) == rc, d
     wr = _lib.WorklistReduceArgs()
@@ -233,7 +235,7 @@ def test_head_sizes_and_column_counts_without_gpu():
         setattr(wr, f, 4096)
     wr.num_groups, wr.num_query_heads, wr.max_query_length = 0, 32, 8
     wr.output_dtype = _lib.DTYPE_BF16
-    for d, rc in ((64, 0), (256, 0), (320, -2)):
+    for d, rc in ((64, 0), (256, 0), (320, 0), (448, 0), (96, -2), (640, -2)):
         wr.head_size = d
         assert lib.pa_fp8_reduce_worklist(ctypes.byref(wr), None) == rc, d
 

@@ -1,6 +1,6 @@
 """GPU parity of the generic decode kernels against the CPU oracle.
 
-Head sizes other than 128 (64, 192, 256) and more than 64 query columns
+Head sizes other than 128 (64, 192, 256, 320, 384, 448, 512) and more than 64 query columns
 per kv head (query_length * gqa up to 128 here) -- shapes the reference's
 routes take (kernels/pa_decode_fp8.py:2084-2085, 2101, 3058) -- run on the
 library's generic kernels behind the same entry points.  Every route of
@@ -42,6 +42,12 @@ SHAPES = {
     "eq128_pt": dict(query_length=4, num_query_heads=64, num_kv_heads=2, per_token=True),  # 4 x gqa 32
     "eq80_d256": dict(head_size=256, query_length=5, num_query_heads=32, num_kv_heads=2),
     "eq128_d64_pt": dict(head_size=64, query_length=2, num_query_heads=128, num_kv_heads=2, per_token=True),
+    # head sizes above 256: one chunk buffer per wave
+    "d320": dict(head_size=320, num_query_heads=8, num_kv_heads=2),
+    "d384_mtp_pt": dict(head_size=384, query_length=2, num_query_heads=16, num_kv_heads=4, per_token=True),
+    "d448_pt": dict(head_size=448, num_query_heads=16, num_kv_heads=2, per_token=True),
+    "d512": dict(head_size=512, num_query_heads=8, num_kv_heads=1),
+    "d512_mtp_pt": dict(head_size=512, query_length=3, num_query_heads=24, num_kv_heads=2, per_token=True),
 }
 
 
@@ -74,7 +80,7 @@ def test_any_partition_count(name, P):
     assert_parity(out, ref, f"{name} P={P}")
 
 
-@pytest.mark.parametrize("name", ["d64_mtp_pt", "d192_pt", "d256_mtp_pt", "eq128_pt"])
+@pytest.mark.parametrize("name", ["d64_mtp_pt", "d192_pt", "d256_mtp_pt", "eq128_pt", "d320", "d512_mtp_pt"])
 @pytest.mark.parametrize("window", [1, 100, 600])
 def test_window_routes(name, window):
     case = build(name, sliding_window=window, ctx=[8, 90, 700, 2100])
@@ -100,7 +106,7 @@ def owner_for_any_shape():
         tp.SCHEDULES["owner"] = saved
 
 
-@pytest.mark.parametrize("name", ["d64", "d256_mtp_pt", "eq128", "eq80_d256"])
+@pytest.mark.parametrize("name", ["d64", "d256_mtp_pt", "eq128", "eq80_d256", "d320", "d512_mtp_pt"])
 @pytest.mark.parametrize("sched", ["owner", "slot"])
 def test_slot_partials_match_oracle(name, sched):
     case = build(name, ctx=[3, 100, 256, 700, 1500])
@@ -122,7 +128,8 @@ def test_slot_partials_match_oracle(name, sched):
     torch.testing.assert_close(to[f5.expand_as(to)], to_r[f5.expand_as(to_r)], atol=ATOL, rtol=RTOL)
 
 
-@pytest.mark.parametrize("name", ["d64_mtp_pt", "d192_pt", "d256", "eq128_pt", "eq80_d256"])
+@pytest.mark.parametrize("name", ["d64_mtp_pt", "d192_pt", "d256", "eq128_pt", "eq80_d256", "d320", "d448_pt",
+                                  "d512_mtp_pt"])
 @pytest.mark.parametrize("num_cu", [None, 3])
 def test_flat_pages_work_list_and_partitions(name, num_cu):
     """Page size 1024: the persistent route's work list (get_pa_metadata,
@@ -144,7 +151,7 @@ def test_flat_pages_work_list_and_partitions(name, num_cu):
         assert_parity(out, ref, f"{name} flat partitions cu={num_cu}")
 
 
-@pytest.mark.parametrize("name", ["d64_mtp_pt", "d256", "eq128_pt"])
+@pytest.mark.parametrize("name", ["d64_mtp_pt", "d256", "eq128_pt", "d384_mtp_pt", "d512"])
 def test_plain_value_layout_and_dtypes(name):
     case = build(name, block_size=64, ctx=[2, 64, 500, 1300])
     ref = torch_oracle(case, float_out=True)

@@ -248,9 +248,20 @@ def test_generic_owner_needs_enough_waves(monkeypatch):
 def test_unbuilt_head_size_is_not_implemented():
     case = make_case(batch=1, ctx=[10], seed=5, head_size=64)
     c = dict(case)
-    c["query"] = torch.zeros(1, 8, 320, dtype=torch.bfloat16)
-    with pytest.raises(NotImplementedError, match="head_dim=320"):
-        prep(c, output=torch.empty(1, 8, 320, dtype=torch.bfloat16))
+    c["query"] = torch.zeros(1, 8, 576, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError, match="head_dim=576"):
+        prep(c, output=torch.empty(1, 8, 576, dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("d", [320, 384, 448, 512])
+def test_large_head_sizes_take_the_generic_routes(d):
+    """Head sizes 320 .. 512 (multiples of 64, as the reference's routes
+    take) run on the generic kernels through every route."""
+    case = make_case(batch=2, ctx=[5, 700], head_size=d, seed=3)
+    call = prep(case)
+    assert call.route == "ps_small_block" and call._pa.head_size == d
+    call = prep(case, sliding_window=100)
+    assert call._pa.head_size == d
 
 
 def _empty_case(**kw):

@@ -108,6 +108,12 @@ VARIANTS = {
     "d192_mtp": dict(head_size=192, query_length=2, num_query_heads=8, num_kv_heads=2, per_token=True),
     "d256_pt": dict(head_size=256, per_token=True),
     "eq128": dict(query_length=8, num_query_heads=32, num_kv_heads=2, ctx_range=(8, 120)),
+    # head sizes above 256 (the generic kernels' single-buffer form)
+    "d320_window": dict(head_size=320, sliding_window=31, ctx_range=(1, 120)),
+    "d384_mtp": dict(head_size=384, query_length=2, num_query_heads=8, num_kv_heads=2),
+    "d448_pt": dict(head_size=448, per_token=True, ctx_range=(1, 90)),
+    "d512_pt_mtp": dict(head_size=512, per_token=True, query_length=3, num_query_heads=12, num_kv_heads=3,
+                        ctx_range=(3, 100)),
 }
 
 
@@ -151,7 +157,8 @@ def test_equal_keys_give_mean_of_values():
         torch.testing.assert_close(out[b], exp, atol=1e-5, rtol=1e-5)
 
 
-@pytest.mark.parametrize("ql,window,d", [(1, 0, 128), (3, 0, 128), (2, 17, 128), (1, 0, 64), (2, 9, 256)])
+@pytest.mark.parametrize("ql,window,d", [(1, 0, 128), (3, 0, 128), (2, 17, 128), (1, 0, 64), (2, 9, 256), (1, 0, 320),
+                                         (2, 13, 512)])
 def test_sdpa_library_routine(ql, window, d):
     """Each sequence reduces to torch's scaled_dot_product_attention."""
     case = make_case(query_length=ql, num_query_heads=8, num_kv_heads=2, ctx=[ql + 5, 90, 161], seed=5,
@@ -211,7 +218,8 @@ def test_gqa_heads_only_see_their_kv_head():
 
 
 @pytest.mark.parametrize("P,window,ql,d", [(1, 0, 1, 128), (3, 0, 1, 128), (8, 0, 2, 128), (6, 300, 1, 128),
-                                           (4, 77, 3, 128), (5, 0, 2, 256), (6, 120, 1, 64)])
+                                           (4, 77, 3, 128), (5, 0, 2, 256), (6, 120, 1, 64), (3, 0, 1, 320),
+                                           (4, 50, 2, 512)])
 def test_slot_partials_merge_to_full_attention(P, window, ql, d):
     """Any slot split, merged by LSE, reproduces the unsplit attention."""
     case = make_case(ctx=[ql, 255, 256, 257, 700, 1100][: 6], query_length=ql, seed=9, sliding_window=window,
