@@ -719,6 +719,22 @@ __device__ __forceinline__ void unit_softmax_pv(WaveState<1>& s, const QueryTile
   s.lsum[0] = s.lsum[0] * alpha + psum * vmul;
 }
 
+// Maximum of two non-negative floats over the wave, on their bits as
+// integers (the same order for non-negative floats; no NaN canonicalisation
+// as for float maxima): within each row of 16 lanes by DPP (quad swaps, then
+// the 8- and 16-lane mirrors), then across the four rows.
+__device__ __forceinline__ float wave_max_nonneg(float a, float b) {
+  int v = pa_max(__float_as_int(a), __float_as_int(b));
+  v = pa_max(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));
+  v = pa_max(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));
+  v = pa_max(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false));
+  v = pa_max(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false));
+  auto r = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+  v = pa_max((int)r[0], (int)r[1]);
+  r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+  return __int_as_float(pa_max((int)r[0], (int)r[1]));
+}
+
 // QK, softmax and value product of a 128-token unit of four chunks for one
 // 16-column block (the cooperative kernel's four-chunk units), as one
 // online-softmax step, with lane group g holding chunk g:
@@ -731,8 +747,16 @@ __device__ __forceinline__ void unit_softmax_pv(WaveState<1>& s, const QueryTile
 //     probabilities the lane holds (B operand) and, for head dim 16 j + c,
 //     the two 16-byte rows [half][dim][16 tokens] of the chunk's value image
 //     (A operand: two ds_read_b128 straight into the operand registers).
-// sk[c] is chunk c's slot (a missing chunk, c >= nch, points at chunk 0's
-// and is masked); tb0 the unit's first token.  References move lazily, as
+// Per logit the softmax costs a multiply and an FMA (x = logit * key scale
+// * column factor + C, with C = kPBias - m - log2(value reference) per
+// column), a share of the maximum,
+// one exponential, the sum and the value-scale product with the fp8 split;
+// masks run only on units with keys some column does not see.  The
+// value-scale reference moves on the unit's largest value scale, which each
+// wave reads with two loads per lane (the keys nobody sees have their
+// scales zeroed in LDS by the wave that loaded them).  Chunk c sits in ring
+// slot (cslot + c) mod S (a missing chunk, c >= nch, reads chunk 0's and is
+// masked); tb0 is the unit's first token.  References move lazily, as
 // unit_softmax_pv describes.
 template <bool PER_TOKEN, int S, int kSlotBytes>
 __device__ __forceinline__ void unit4_softmax_pv(WaveState<1>& s, const QueryTile<1>& q,
@@ -760,104 +784,123 @@ __device__ __forceinline__ void unit4_softmax_pv(WaveState<1>& s, const QueryTil
     const i32x4 k1 = *(const LDS_AS i32x4*)(kb + off + 1024);
     return i32x8{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
   };
-  f32x4 lg4[8];
-  i32x8 KA[2];
-  KA[0] = key_tile(0);
-  // The matrix blocks run at raised wave priority, so a wave that reaches
-  // them issues its MFMAs back to back while the other wave of the SIMD
-  // works through its softmax on the VALU.
-  __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    if (t + 1 < 8) KA[(t + 1) & 1] = key_tile(t + 1);
-    const f32x4 zz = {0.f, 0.f, 0.f, 0.f};
-    lg4[t] = mfma_fp8_k128(KA[t & 1], q.hi[0], zz);
-    lg4[t] = mfma_fp8_k128(KA[t & 1], q.lo[0], lg4[t]);
-  }
-  __builtin_amdgcn_s_setprio(0);
-  float lg[32];
-#pragma unroll
-  for (int t = 0; t < 8; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) lg[4 * t + i] = lg4[t][i];
-
   // Tokens of the lane's chunk: tok0 + k.  full: every token of the unit
   // is visible to every column (wave-uniform).
   const int tok0 = tb0 + 32 * grp;
   const bool full = nch == 4 && tb0 >= q.lo_max && tb0 + 128 <= q.hi_min;
-  // keys some column sees: [klo, khi) of the lane's 32 (empty for a missing
-  // chunk); the value scales of the others, possibly stale, are zeroed
-  int klo = 0, khi = 32;
-  if (!full) {
-    klo = pa_min(pa_max(q.lo_all - tok0, 0), 32);
-    khi = grp < nch ? pa_min(pa_max(q.hi_all - tok0, klo), 32) : klo;
+  // the column's own visible keys among the lane's 32
+  const int jl = q.vis_lo[0] - tok0;
+  const int jh = grp < nch ? q.vis_hi[0] - tok0 : jl;
+
+  // The unit's largest value scale, each lane reading tokens 2 c16 and
+  // 2 c16 + 1 of its own chunk (non-negative floats: compared as integers;
+  // the scales of keys nobody sees were zeroed in LDS, and a missing chunk
+  // reads chunk 0's), reduced while the key product runs.
+  float cmax = 0.0f;
+  if (PER_TOKEN) {
+    const f32x2 vv = *(const LDS_AS f32x2*)(sb + 32 + 2 * c16);
+    cmax = wave_max_nonneg(vv[0], vv[1]);
   }
 
-  float vsc[32];
-  float vratio = 1.0f, vmul = 1.0f, vlog = 0.0f;
-  if (PER_TOKEN) {
+  // The key product (eight tiles, the next tile's operands read ahead of
+  // this tile's MFMAs), at raised wave priority: a wave that reaches its
+  // matrix block issues it back to back while the other wave of the SIMD
+  // works through its softmax on the VALU.
+  f32x4 lg4[8];
+  {
+    i32x8 KA[2];
+    KA[0] = key_tile(0);
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int k = 0; k < 32; k += 4) {
-      const f32x4 ks = *(const LDS_AS f32x4*)(sb + k);
-      const f32x4 vs = *(const LDS_AS f32x4*)(sb + 32 + k);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        lg[k + i] *= ks[i];
-        vsc[k + i] = vs[i];
-      }
+    for (int t = 0; t < 8; ++t) {
+      if (t + 1 < 8) KA[(t + 1) & 1] = key_tile(t + 1);
+      const f32x4 zz = {0.f, 0.f, 0.f, 0.f};
+      lg4[t] = mfma_fp8_k128(KA[t & 1], q.hi[0], zz);
+      lg4[t] = mfma_fp8_k128(KA[t & 1], q.lo[0], lg4[t]);
     }
-    if (!full) {
+    __builtin_amdgcn_s_setprio(0);
+  }
+  // x = l + C0: l the base-2 logit (the key product times the per-token key
+  // scale), C0 from the current references (the column's maximum m, 0 while
+  // it has none, and the value-scale reference); -inf for keys the column
+  // does not see.
+  const float m_old = s.m2[0] == kNegInf ? 0.0f : s.m2[0];
+  float vmul = PER_TOKEN && s.vsmax > 0.0f ? s.vsmax : 1.0f;
+  const float C0 = kPBias - m_old - (PER_TOKEN ? __builtin_amdgcn_logf(vmul) : 0.0f);
+  const float post = q.fac[0];  // > 0 (prepare_query)
+  float x[32];
 #pragma unroll
-      for (int k = 0; k < 32; ++k) vsc[k] = (k >= klo && k < khi) ? vsc[k] : 0.0f;
-    }
-    float cmax = 0.0f;
+  for (int t = 0; t < 8; ++t) {
+    f32x4 ks = {1.f, 1.f, 1.f, 1.f};
+    if (PER_TOKEN) ks = *(const LDS_AS f32x4*)(sb + 4 * t);
 #pragma unroll
-    for (int k = 0; k < 32; ++k) cmax = fmaxf(cmax, vsc[k]);
-    cmax = max_over_groups(cmax);
-    const float vnew = cmax > 2.0f * s.vsmax ? cmax : s.vsmax;
-    vratio = vnew > s.vsmax && s.vsmax > 0.0f ? s.vsmax * __builtin_amdgcn_rcpf(vnew) : 1.0f;
-    vmul = vnew > 0.0f ? vnew : 1.0f;
-    vlog = __builtin_amdgcn_logf(vmul);
-    s.vsmax = vnew;
+    for (int i = 0; i < 4; ++i) x[4 * t + i] = __builtin_fmaf(lg4[t][i], PER_TOKEN ? ks[i] * post : post, C0);
   }
   if (!full) {
-    // the column's own visible keys
-    const int jl = q.vis_lo[0] - tok0;
-    const int jh = grp < nch ? q.vis_hi[0] - tok0 : jl;
+    // a real branch: speculated, these selects would run on every unit
+    asm volatile("" ::: "memory");
 #pragma unroll
-    for (int k = 0; k < 32; ++k) lg[k] = (k >= jl && k < jh) ? lg[k] : kNegInf;
+    for (int k = 0; k < 32; ++k) x[k] = (k >= jl && k < jh) ? x[k] : kNegInf;
   }
-  const float post = q.fac[0];  // > 0 (prepare_query)
-  float cmax = kNegInf;
+  float xmax = kNegInf;
 #pragma unroll
-  for (int k = 0; k < 32; ++k) cmax = fmaxf(cmax, lg[k]);
-  cmax = max_over_groups(cmax) * post;
-  const bool move = cmax > s.m2[0] + kLazyMax;
-  const float mnew = move ? cmax : s.m2[0];
-  const float muse = mnew == kNegInf ? 0.0f : mnew;
-  const float alpha = move ? __builtin_amdgcn_exp2f(s.m2[0] - muse) : 1.0f;
-  s.m2[0] = mnew;
+  for (int k = 0; k < 32; ++k) xmax = fmaxf(xmax, x[k]);
+  // probabilities 2^x (times the value scale) into the fp8 hi + lo
+  // operands PH, PL and their sum psum (stale value scales were zeroed in
+  // LDS: a masked key gives 0 * 0)
+  float psum;
+  i32x8 PH, PL;
+  auto probabilities = [&]() {
+    psum = 0.0f;
+#pragma unroll
+    for (int k8 = 0; k8 < 4; ++k8) {
+      f32x4 v0 = {1.f, 1.f, 1.f, 1.f}, v1 = v0;
+      if (PER_TOKEN) {
+        v0 = *(const LDS_AS f32x4*)(sb + 32 + 8 * k8);
+        v1 = *(const LDS_AS f32x4*)(sb + 36 + 8 * k8);
+      }
+      float pr[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float ev = __builtin_amdgcn_exp2f(x[8 * k8 + i]);
+        psum += ev;
+        pr[i] = PER_TOKEN ? ev * (i < 4 ? v0[i] : v1[i - 4]) : ev;
+      }
+      long phi, plo;
+      split8_fp8<PER_TOKEN>(pr, phi, plo);  // per-token: pr = ev * scale
+      PH[2 * k8] = (int)(uint32_t)phi;
+      PH[2 * k8 + 1] = (int)(uint32_t)((uint64_t)phi >> 32);
+      PL[2 * k8] = (int)(uint32_t)plo;
+      PL[2 * k8 + 1] = (int)(uint32_t)((uint64_t)plo >> 32);
+    }
+  };
+  // The column's maximum logit this unit is max x - C0.  The maximum
+  // reference moves to it when it passes the reference by more than
+  // kLazyMax (and on the column's first visible key); the value-scale
+  // reference moves to the unit's largest scale when that exceeds twice
+  // it.  Then x shifts by the change of C.  Every probability is at most
+  // 2^(kPBias + kLazyMax) times a value-scale ratio of at most 2.
+  const float lmax = max_over_groups(xmax) - C0;
+  const bool move = lmax > s.m2[0] + kLazyMax;
+  const bool vmove = PER_TOKEN && cmax > 2.0f * s.vsmax;  // wave-uniform
+  float alpha = 1.0f, vratio = 1.0f;
+  if (__ballot(move) || vmove) {
+    const float mnew = move ? lmax : s.m2[0];
+    const float muse = mnew == kNegInf ? 0.0f : mnew;
+    alpha = move ? __builtin_amdgcn_exp2f(s.m2[0] - muse) : 1.0f;
+    s.m2[0] = mnew;
+    if (vmove) {
+      vratio = s.vsmax > 0.0f ? s.vsmax * __builtin_amdgcn_rcpf(cmax) : 1.0f;
+      s.vsmax = cmax;
+      vmul = cmax;
+    }
+    const float dx = (kPBias - muse - (PER_TOKEN ? __builtin_amdgcn_logf(vmul) : 0.0f)) - C0;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) x[k] += dx;
+  }
+  probabilities();
   const float f = alpha * vratio;
   if (__ballot(f != 1.0f)) scale_inplace(s.acc[0], f);
-  const float bias = kPBias - muse - vlog;
-  float psum = 0.0f;
-  i32x8 PH, PL;
-#pragma unroll
-  for (int k8 = 0; k8 < 4; ++k8) {
-    float pr[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(lg[8 * k8 + i], post, bias));
-      psum += ev;
-      pr[i] = PER_TOKEN ? ev * vsc[8 * k8 + i] : ev;
-    }
-    long phi, plo;
-    split8_fp8<PER_TOKEN>(pr, phi, plo);  // per-token: pr = ev * scale
-    PH[2 * k8] = (int)(uint32_t)phi;
-    PH[2 * k8 + 1] = (int)(uint32_t)((uint64_t)phi >> 32);
-    PL[2 * k8] = (int)(uint32_t)plo;
-    PL[2 * k8 + 1] = (int)(uint32_t)((uint64_t)plo >> 32);
-  }
   // value operands (stale bytes of edge chunks were zeroed in LDS), the
   // next tile's read ahead of this tile's products
   auto value_tile = [&](int j) {
@@ -2480,6 +2523,14 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
               zero_stale_values((LDS_AS unsigned char*)smem + sl * kSlotBytes + kKBytes + hh * 2048,
                                 ub + ch * kChunk + 16 * hh, cur.lo_all, cur.hi_all, lane);
             }
+            if (U == 4 && scale_wave) {
+              // and the chunk's per-token K and V scales of those keys
+              // (lane l: K scale l < 32, else V scale l - 32), so that the
+              // softmax reads zeros there rather than stale bits
+              const int t = ub + ch * kChunk + (lane & 31);
+              if (t < cur.lo_all || t >= cur.hi_all)
+                ((LDS_AS float*)((LDS_AS unsigned char*)smem + sl * kSlotBytes + kKBytes + kVBytes))[lane] = 0.0f;
+            }
           }
           asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         }
@@ -2497,6 +2548,7 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
         qready = has_nxt && nxt.n > 0;
         if (qready) load_query(nxt);
       }
+
       // Slots of chunks before gc are free: every wave has passed this
       // unit's barrier, so it is done with them.
       while (iok && issued < gc + S) issue_next();
