@@ -12,6 +12,8 @@ from typing import Optional
 
 LIB_NAME = "libpa_fp8.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# The checked build (same kernels; every index they clamp is also recorded).
+CHECKED_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpa_fp8_checked.so")
 
 ABI_VERSION = 1
 
@@ -60,7 +62,15 @@ EXPORTED_SYMBOLS = (
     "pa_fp8_mla_plan_sizes",
     "pa_fp8_mla_plan",
     "pa_fp8_fnuz_to_fn",
+    "pa_fp8_debug_violations",
+    "pa_fp8_checked_build",
 )
+
+# Bits of pa_fp8_debug_violations (a checked build's record of clamped indices).
+VIOLATION_PAGE = 1
+VIOLATION_WORK = 2
+VIOLATION_POSITION = 4
+VIOLATION_SLOT = 8
 
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
@@ -410,6 +420,10 @@ def load(path: Optional[str] = None) -> ctypes.CDLL:
     lib.pa_fp8_mla_plan.restype = ctypes.c_int
     lib.pa_fp8_fnuz_to_fn.argtypes = [_vp, _vp, _i64, _i64, _i64, _vp, _vp]
     lib.pa_fp8_fnuz_to_fn.restype = ctypes.c_int
+    lib.pa_fp8_debug_violations.argtypes = [ctypes.POINTER(ctypes.c_uint)]
+    lib.pa_fp8_debug_violations.restype = ctypes.c_int
+    lib.pa_fp8_checked_build.argtypes = []
+    lib.pa_fp8_checked_build.restype = ctypes.c_int
     if path is None:
         _LIB = lib
     return lib
@@ -419,6 +433,17 @@ def check(rc: int, what: str) -> None:
     if rc != 0:
         msg = load().pa_fp8_error_string(rc).decode()
         raise RuntimeError(f"{what} failed: {ERRORS.get(rc, 'hipError')} ({rc}): {msg}")
+
+
+def debug_violations(lib: Optional[ctypes.CDLL] = None) -> int:
+    """VIOLATION_* bits a checked build recorded since the last call (then
+    cleared; 0 from a release build).  Synchronises the current device."""
+    lib = lib or load()
+    bits = ctypes.c_uint(0)
+    rc = lib.pa_fp8_debug_violations(ctypes.byref(bits))
+    if rc != 0:
+        raise RuntimeError(f"pa_fp8_debug_violations failed: {rc}")
+    return int(bits.value)
 
 
 def plan_slot(context_length: int, num_partitions: int, slot: int, sliding_window: int, query_length: int):

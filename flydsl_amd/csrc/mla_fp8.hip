@@ -57,6 +57,7 @@
 
 #include "mla_plan.h"
 #include "pa_fp8.h"
+#include "pa_check.h"
 
 namespace {
 
@@ -847,6 +848,7 @@ __global__ __launch_bounds__(256) void fnuz_to_fn_kernel(const unsigned char* __
   if (t >= num_rows * chunks) return;
   const int64_t r = t / chunks, c = t - r * chunks;
   int64_t sr = rows ? (int64_t)rows[r] : r;
+  pa_note(sr < 0 || sr >= num_src_rows, PA_VIOLATION_PAGE);
   sr = sr < 0 ? 0 : (sr >= num_src_rows ? num_src_rows - 1 : sr);
   const i32x4 v = *(const i32x4*)(src + sr * row_bytes + 16 * c);
   i32x4 o;
@@ -859,7 +861,31 @@ __global__ __launch_bounds__(256) void fnuz_to_fn_kernel(const unsigned char* __
   *(i32x4*)(dst + r * row_bytes + 16 * c) = o;
 }
 
+#ifdef PA_FP8_CHECKED
+// Checked builds: the decode's inputs against the ranges load_work and
+// issue_block clamp them into -- the work records the workers walk and every
+// page-list entry -- in a kernel of its own, run before the decode (the
+// decode kernel has no registers to spare for the checks).
+__global__ __launch_bounds__(256) void mla_check_kernel(const pa_mla_decode_args a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < a.num_page_indices) {
+    const int p = a.kv_page_indices[i];
+    pa_note(p < 0 || (int64_t)p >= a.num_pages, PA_VIOLATION_PAGE);
+  }
+  const int w0 = a.work_indptr[0], w1 = a.work_indptr[a.num_workers];
+  if (i >= w0 && i < w1 && i < a.num_works) {
+    const int32_t* w = a.work_info + 8 * i;
+    const int pql = w[1], qo = w[2], kv0 = w[4], kv1 = w[5];
+    pa_note(qo < 0 || qo >= a.num_rows || pql < -1 || pql >= a.num_partial || kv0 < 0 || kv1 < kv0 ||
+                kv1 > a.num_page_indices,
+            PA_VIOLATION_WORK);
+  }
+}
+#endif
+
 }  // namespace
+
+PA_CHECK_DEFINE_TAKE(pa_violations_mla)
 
 extern "C" int pa_fp8_fnuz_to_fn(const void* src, const int32_t* rows, int64_t num_rows, int64_t num_src_rows,
                                  int64_t row_bytes, void* dst, void* stream) {
@@ -892,6 +918,12 @@ extern "C" int pa_fp8_mla_decode(const pa_mla_decode_args* a, void* stream) {
       (a->split_output && !aligned16(a->split_output)))
     return PA_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
+#ifdef PA_FP8_CHECKED
+  {
+    const int64_t n = a->num_page_indices > a->num_works ? a->num_page_indices : a->num_works;
+    hipLaunchKernelGGL(mla_check_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, *a);
+  }
+#endif
   constexpr int kNht = MLA_HEAD_TILES;
   if (a->precise_p)
     hipLaunchKernelGGL((mla_fp8_decode_kernel<true, kNht>), dim3(a->num_workers), dim3(Shape<kNht>::threads), 0, s,

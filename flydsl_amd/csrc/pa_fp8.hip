@@ -40,6 +40,7 @@
 #include "pa_fp8.h"
 #include "pa_plan.h"
 #include "pa_worklist.h"
+#include "pa_check.h"
 
 namespace {
 
@@ -1080,6 +1081,7 @@ __global__ __launch_bounds__(64 * WAVES) void pa_fp8_partition_kernel(const pa_f
   const int voff_plain = lane * bs;
 
   auto clamp_page = [&](int p) -> int {
+    pa_note(p < 0 || p >= nblocks, PA_VIOLATION_PAGE);
     p = p < 0 ? 0 : p;
     return p < nblocks ? p : nblocks - 1;
   };
@@ -1736,6 +1738,7 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
   LDS_AS unsigned char* ring = (LDS_AS unsigned char*)smem + wave * kWaveBytes;
   LDS_AS unsigned char* qimg = ring + kStages * kStageBytes;
   auto clamp_page = [&](int p) -> int {
+    pa_note(p < 0 || p >= nblocks, PA_VIOLATION_PAGE);
     p = p < 0 ? 0 : p;
     return p < nblocks ? p : nblocks - 1;
   };
@@ -2047,6 +2050,7 @@ __global__ __launch_bounds__(64 * kBinWaves) void pa_fp8_bin_kernel(
 
   LDS_AS unsigned char* ring = (LDS_AS unsigned char*)smem + wave * kWaveBytes;
   auto clamp_page = [&](int p) -> int {
+    pa_note(p < 0 || p >= nblocks, PA_VIOLATION_PAGE);
     p = p < 0 ? 0 : p;
     return p < nblocks ? p : nblocks - 1;
   };
@@ -2314,6 +2318,7 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
   const int koff_lane = BS16 ? lane * 16 : (lane >> 4) * (bs * 16) + (lane & 15) * 16;
   const int voff_plain = lane * bs;
   auto clamp_page = [&](int p) -> int {
+    pa_note(p < 0 || p >= nblocks, PA_VIOLATION_PAGE);
     p = p < 0 ? 0 : p;
     return p < nblocks ? p : nblocks - 1;
   };
@@ -3051,6 +3056,7 @@ __device__ __forceinline__ bool gen_setup(GenCtx<D>& c, const GenArgs& a, int b,
 __device__ __forceinline__ int gen_page(const GenArgs& a, const int32_t* pages, int last_page, int tok) {
   int lp = pa_min(tok / a.block_size, last_page);
   int p = ld_uniform(pages, lp);
+  pa_note(p < 0 || p >= a.num_blocks, PA_VIOLATION_PAGE);
   p = p < 0 ? 0 : p;
   return p < a.num_blocks ? p : a.num_blocks - 1;
 }
@@ -3961,7 +3967,27 @@ int static_scratch(hipStream_t s, void** out) {
 
 }  // namespace
 
+PA_CHECK_DEFINE_TAKE(pa_violations_paged)
+
 extern "C" {
+
+int pa_fp8_debug_violations(unsigned int* bits) {
+  if (!bits) return PA_ERR_NULL_ARG;
+  *bits = 0;
+  int rc = pa_violations_paged(bits);
+  if (rc == 0) rc = pa_violations_mla(bits);
+  if (rc == 0) rc = pa_violations_rope_cache(bits);
+  if (rc == 0) rc = pa_violations_qk_norm_rope(bits);
+  return rc;
+}
+
+int pa_fp8_checked_build(void) {
+#ifdef PA_FP8_CHECKED
+  return 1;
+#else
+  return 0;
+#endif
+}
 
 int pa_fp8_decode_partition(const pa_fp8_partition_args* a, void* stream) {
   if (!a) return PA_ERR_NULL_ARG;

@@ -21,6 +21,7 @@
 #include <stdint.h>
 
 #include "pa_fp8.h"
+#include "pa_check.h"
 
 namespace {
 
@@ -212,6 +213,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void pa_qk_norm_rope_kernel(co
         // around the loads.  (Lanes outside the rotated part select their
         // unrotated values after the rotation, which keeps signed zeros.)
         const bool inside = lpos >= 0 && lpos < a.max_pos;
+        pa_note(rd > 0 && !inside, PA_VIOLATION_POSITION);
         if (rd > 0) {
           const int64_t crow = (int64_t)(inside ? lpos : 0) * (rd / 2) + half_off;
           b.cs[i] = load_half<VEC>(cos_tab + crow);
@@ -356,6 +358,8 @@ hipError_t dispatch(const pa_qk_norm_rope_args& a, int tpg_log2, int rpw, unsign
 bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p & (n - 1)) == 0; }
 
 }  // namespace
+
+PA_CHECK_DEFINE_TAKE(pa_violations_qk_norm_rope)
 
 extern "C" int pa_fp8_qk_norm_rope_quant(const pa_qk_norm_rope_args* a, void* stream) {
   if (!a) return PA_ERR_NULL_ARG;

@@ -26,6 +26,7 @@
 #include <stdint.h>
 
 #include "pa_fp8.h"
+#include "pa_check.h"
 
 namespace {
 
@@ -182,6 +183,7 @@ __global__ __launch_bounds__(kRcThreads) void pa_rope_cache_kernel(const pa_fp8_
       const uint32_t tc = __builtin_amdgcn_readfirstlane(u < qunits ? t : (uint32_t)T - 1);
       const int rc = row < QH ? row : QH - 1;
       int p = load_index(a.positions, tc, i64);
+      pa_note(lq[j] && (p < 0 || p >= a.max_pos), PA_VIOLATION_POSITION);
       p = p < 0 ? 0 : (p >= a.max_pos ? a.max_pos - 1 : p);  // never read outside the tables
       cs[j] = *(const i32x4*)((const uint16_t*)a.cos_cache + (int64_t)p * a.stride_cos_pos + cidx);
       sn[j] = *(const i32x4*)((const uint16_t*)a.sin_cache + (int64_t)p * a.stride_sin_pos + cidx);
@@ -228,6 +230,7 @@ __global__ __launch_bounds__(kRcThreads) void pa_rope_cache_kernel(const pa_fp8_
     vv = __builtin_nontemporal_load((const i32x4*)((const uint16_t*)a.v + (int64_t)tok * a.stride_v_tok + (int64_t)kh * a.stride_v_head + d0));
   }
   asm volatile("" ::: "memory");  // row loads issued before the tables wait on the positions
+  pa_note(live && (p < 0 || p >= a.max_pos), PA_VIOLATION_POSITION);
   p = p < 0 ? 0 : (p >= a.max_pos ? a.max_pos - 1 : p);
   const i32x4 cs = *(const i32x4*)((const uint16_t*)a.cos_cache + (int64_t)p * a.stride_cos_pos + cidx);
   const i32x4 sn = *(const i32x4*)((const uint16_t*)a.sin_cache + (int64_t)p * a.stride_sin_pos + cidx);
@@ -241,6 +244,7 @@ __global__ __launch_bounds__(kRcThreads) void pa_rope_cache_kernel(const pa_fp8_
   const int64_t bi = slot >= 0 ? slot / bs : 0;
   const int bp = slot >= 0 ? slot - (int)bi * bs : 0;
   const bool cached = live && slot >= 0 && bi < a.num_blocks;
+  pa_note(live && slot >= 0 && bi >= a.num_blocks, PA_VIOLATION_SLOT);
 
   // value cache elements of this lane's 8 dims when fp8
   uint32_t v8[2] = {0, 0};
@@ -371,6 +375,8 @@ hipError_t dispatch_rope_cache(const pa_fp8_rope_cache_args& a, unsigned grid, h
 bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
+
+PA_CHECK_DEFINE_TAKE(pa_violations_rope_cache)
 
 extern "C" int pa_fp8_rope_cache(const pa_fp8_rope_cache_args* a, void* stream) {
   if (!a) return PA_ERR_NULL_ARG;

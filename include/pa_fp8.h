@@ -11,7 +11,9 @@
  * device of the stream a call is launched on (hipStreamGetDevice; the
  * current device for the null stream), so calls are re-entrant, may target
  * any device's stream, and may be captured into a HIP graph when the caller
- * preallocates every buffer.
+ * preallocates every buffer.  A checked build (libpa_fp8_checked.so, see
+ * pa_fp8_debug_violations) also keeps one word of violation bits per source
+ * file on each device.
  *
  * Return codes: 0 on success, a positive hipError_t value when the HIP
  * runtime rejects a launch, or one of the negative PA_ERR_* codes below for
@@ -575,6 +577,27 @@ int pa_fp8_mla_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, int num_
  */
 int pa_fp8_fnuz_to_fn(const void* src, const int32_t* rows, int64_t num_rows, int64_t num_src_rows,
                       int64_t row_bytes, void* dst, void* hip_stream);
+
+/*
+ * Checked builds.  libpa_fp8_checked.so is built from the same sources with
+ * -DPA_FP8_CHECKED.  Like the release library it clamps every index it reads
+ * from caller data into range before using it as an address; it also
+ * records each value it had to clamp as one of these bits (no trap, no
+ * wait; the results are those of the release library):
+ */
+enum {
+  PA_VIOLATION_PAGE = 1,     /* block_tables / kv_page_indices entry, or fnuz row index, outside the cache */
+  PA_VIOLATION_WORK = 2,     /* MLA work record: query row, partial row or kv range outside its buffer */
+  PA_VIOLATION_POSITION = 4, /* rope position outside [0, max_pos) */
+  PA_VIOLATION_SLOT = 8      /* KV-cache slot past the last cache block */
+};
+/* ORs the bits recorded since the last call into *bits and clears them
+ * (always 0 in a release build).  Synchronises the current device; returns
+ * PA_OK or a HIP error code.  No counterpart in the reference: a debug aid
+ * for callers chasing a bad page table or slot mapping. */
+int pa_fp8_debug_violations(unsigned int* bits);
+/* 1 in a checked build, 0 in a release build. */
+int pa_fp8_checked_build(void);
 
 /* Library identification and error names. */
 const char* pa_fp8_version(void);

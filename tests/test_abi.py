@@ -34,6 +34,23 @@ def test_library_exports_every_declared_symbol():
         assert re.search(rf"\bT {name}$", out, re.M), name
 
 
+def test_checked_build_exports_every_declared_symbol():
+    """The checked build (the same sources with -DPA_FP8_CHECKED) exports the
+    same entry points and says it is checked; the release library's
+    violation reader returns 0 without touching a device."""
+    lib = _lib.load(_lib.CHECKED_LIB_PATH)
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.CHECKED_LIB_PATH], capture_output=True, text=True).stdout
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+        assert re.search(rf"\bT {name}$", out, re.M), name
+    assert lib.pa_fp8_checked_build() == 1
+    rel = _lib.load()
+    assert rel.pa_fp8_checked_build() == 0
+    assert _lib.debug_violations(rel) == 0
+    assert rel.pa_fp8_debug_violations(None) == -1
+    assert lib.pa_fp8_debug_violations(None) == -1
+
+
 def test_version_and_error_strings():
     lib = _lib.load()
     assert b"gfx950" in lib.pa_fp8_version()
