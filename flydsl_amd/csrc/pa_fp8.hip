@@ -61,6 +61,14 @@ constexpr int kStages = PA_FP8_STAGES;
 #define PA_FP8_WAVES 4
 #endif
 constexpr int kWaves = PA_FP8_WAVES;
+// Waves per workgroup of the per-wave streaming decode with one query image
+// of up to 4 columns per wave (larger images: 4 waves, for LDS).
+#ifndef PA_FP8_STREAM_WAVES
+#define PA_FP8_STREAM_WAVES 4
+#endif
+__host__ __device__ constexpr int stream_waves(int nq) { return nq == 1 ? PA_FP8_STREAM_WAVES : 4; }
+// Query images (of 4 columns) per wave of the streaming decode for eq columns.
+__host__ __device__ constexpr int stream_nq(int eq) { return eq <= 4 ? 1 : (eq <= 8 ? 2 : 4); }
 constexpr int kThreads = 64 * kWaves;
 constexpr int kHead = 128;
 constexpr int kChunk = 32;                  // tokens per wave step
@@ -1372,10 +1380,15 @@ __device__ __forceinline__ void piece_sequence(Piece& p, const pa_fp8_stream_arg
 }
 
 // Balanced split: chunks of all (sequence, kv head) pairs, sequence-major
-// with kv heads inner, cut into nw equal runs (pa_plan_run_begin).
+// with kv heads inner, cut into nw equal runs (pa_plan_run_begin).  With a
+// head group G > 1 the split runs over (sequence, group of G adjacent kv
+// heads, chunk) and each run is walked by G consecutive waves in step, wave
+// i taking head i of every group: the waves of a workgroup then read the
+// same pages of adjacent heads at the same time, and adjacent heads'
+// per-token scales, which share 128-byte lines, are fetched once.
 struct BalancedWalk {
-  int b, h, nb, c, left, first, wid, nw;
-  long long gseg, T;  // global index of chunk 0 of pair (b, h); total chunks
+  int b, h, nb, c, left, first, wid, run, G, nw;
+  long long gseg, T;  // global index of chunk 0 of pair (b, h)'s group; total (group) chunks
   Piece seq;          // sequence-level fields of b
 
   __device__ __forceinline__ bool next(Piece& p, const pa_fp8_stream_args& a, const int32_t* kv_indptr,
@@ -1387,15 +1400,15 @@ struct BalancedWalk {
     p.n = pa_min(nb - c, left);
     const bool whole = c == 0 && p.n == nb;
     p.target = whole ? -1 : 2 * wid + (first ? 0 : 1);
-    p.desc_cnt = c != 0 ? 0 : (whole ? 1 : pa_plan_run_of_chunk(gseg + nb - 1, T, nw) - wid + 1);
+    p.desc_cnt = c != 0 ? 0 : (whole ? 1 : pa_plan_run_of_chunk(gseg + nb - 1, T, nw) - run + 1);
     left -= p.n;
     first = 0;
     c += p.n;
     if (left > 0 && c == nb) {
       c = 0;
       gseg += nb;
-      if (++h == a.num_kv_heads) {
-        h = 0;
+      if ((h += G) >= a.num_kv_heads) {
+        h -= a.num_kv_heads;  // head i of the next sequence's first group
         do {
           if (b + 1 >= a.num_seqs) {  // inconsistent context lengths: stop
             left = 0;
@@ -1454,15 +1467,27 @@ struct WorklistWalk {
   }
 };
 
-// Start of run `wid` of a balanced launch over `num_workers` runs (waves
-// or workgroups): every context length is loaded once (lane l holds
-// sequences l*K .. l*K+K-1, K <= 16), scanned across the wave, and the run's
-// first (sequence, kv head, chunk) is located with a ballot and scalar
-// readlanes.  Returns false when the run is empty.
+// Head group of a balanced launch of per-wave runs over H kv heads and
+// num_workers waves for eq query columns: the largest power of two up to a
+// workgroup's waves that divides both (so a group's waves share a
+// workgroup), else 1.
+__host__ __device__ constexpr int balanced_group(int H, int num_workers, int eq) {
+  int g = stream_waves(stream_nq(eq));
+  while (g > 1 && (H % g != 0 || num_workers % g != 0)) g >>= 1;
+  return g;
+}
+
+// Start of worker `wid`'s walk in a balanced launch over `num_workers`
+// workers (waves or workgroups) in head groups of G (run wid / G, head
+// wid % G of each group): every context length is loaded once (lane l
+// holds sequences l*K .. l*K+K-1, K <= 16), scanned across the wave, and
+// the run's first (sequence, head group, chunk) is located with a ballot
+// and scalar readlanes.  Returns false when the run is empty.
 __device__ __forceinline__ bool balanced_start(BalancedWalk& w, const pa_fp8_stream_args& a,
                                                const int32_t* __restrict__ kv_indptr,
-                                               const int32_t* __restrict__ context_lengths, int wid, int lane) {
-  const int H = a.num_kv_heads;
+                                               const int32_t* __restrict__ context_lengths, int wid, int lane,
+                                               int G) {
+  const int H = a.num_kv_heads / G;  // head groups
   const int ql = a.query_length;
   const int W = a.sliding_window;
   // Chunks per sequence: lane l holds sequences l*K .. l*K+K-1.
@@ -1497,10 +1522,12 @@ __device__ __forceinline__ bool balanced_start(BalancedWalk& w, const pa_fp8_str
   const long long T = (long long)__builtin_amdgcn_readlane(incl, 63) * H;
   long long nwl = T / kMinChunksPerWave;
   nwl = nwl < 1 ? 1 : nwl;
-  const int nw = nwl < a.num_workers ? (int)nwl : a.num_workers;
-  if (wid >= nw) return false;
-  const long long g0 = pa_plan_run_begin(wid, T, nw);
-  const long long g1 = pa_plan_run_begin(wid + 1, T, nw);
+  const int runs = a.num_workers / G;
+  const int nw = nwl < runs ? (int)nwl : runs;
+  const int run = wid / G;
+  if (run >= nw) return false;
+  const long long g0 = pa_plan_run_begin(run, T, nw);
+  const long long g1 = pa_plan_run_begin(run + 1, T, nw);
   if (g1 <= g0) return false;
   // The lane whose sequences hold chunk g0, then the sequence itself.
   const uint64_t hit = __ballot(mine > 0 && (long long)excl * H <= g0 && g0 < (long long)incl * H);
@@ -1522,14 +1549,17 @@ __device__ __forceinline__ bool balanced_start(BalancedWalk& w, const pa_fp8_str
   }
   if (b0 < 0 || n0 <= 0) return false;  // as above
   const long long off = g0 - S * H;
+  const int hg = (int)(off / n0);
   w.b = b0;
   w.nb = n0;
-  w.h = (int)(off / n0);
-  w.c = (int)(off - (long long)w.h * n0);
-  w.gseg = S * H + (long long)w.h * n0;
+  w.h = hg * G + (wid - run * G);
+  w.c = (int)(off - (long long)hg * n0);
+  w.gseg = S * H + (long long)hg * n0;
   w.left = (int)(g1 - g0);
   w.first = 1;
   w.wid = wid;
+  w.run = run;
+  w.G = G;
   w.nw = nw;
   w.T = T;
   piece_sequence(w.seq, a, kv_indptr, context_lengths, b0);
@@ -1688,7 +1718,7 @@ __device__ __forceinline__ void store_piece(const pa_fp8_stream_args& a, void* _
 // before its first chunk, so they ride the same in-order vmcnt pipeline).
 // One 16-column query block (query_length * gqa <= 16).
 template <bool PER_TOKEN, bool BS16, bool WORKLIST, int NQ>
-__global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
+__global__ __launch_bounds__(64 * stream_waves(NQ)) void pa_fp8_stream_kernel(
     const pa_fp8_stream_args a, const int32_t* __restrict__ block_tables, const int32_t* __restrict__ kv_indptr,
     const int32_t* __restrict__ context_lengths, const float* __restrict__ key_scale,
     const float* __restrict__ value_scale, const int32_t* __restrict__ work_indptr,
@@ -1703,14 +1733,14 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
   constexpr int kWaveBytes = kStages * kStageBytes + 2 * kQBytes;
   constexpr int kLoadsPerChunk = 8 + (PER_TOKEN ? 1 : 0);
   static_assert(kStages == 2, "the streaming pipeline keeps one chunk in flight");
-  __shared__ __attribute__((aligned(16))) unsigned char smem[kWaves * kWaveBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char smem[stream_waves(NQ) * kWaveBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = lane >> 4;
   const int c16 = lane & 15;
-  const int wid = blockIdx.x * kWaves + wave;
+  const int wid = blockIdx.x * stream_waves(NQ) + wave;
   const int ql = a.query_length;
   const int gqa = a.query_group_size;
   const int eq = ql * gqa;
@@ -1726,7 +1756,8 @@ __global__ __launch_bounds__(kThreads) void pa_fp8_stream_kernel(
     walk.idx = ld_uniform(work_indptr, wid);
     walk.end = ld_uniform(work_indptr, wid + 1);
   } else {
-    if (!balanced_start(walk, a, kv_indptr, context_lengths, wid, lane)) return;
+    const int G = balanced_group(a.num_kv_heads, a.num_workers, eq);
+    if (!balanced_start(walk, a, kv_indptr, context_lengths, wid, lane, G)) return;
   }
   auto next_piece = [&](Piece& p) -> bool {
     if constexpr (WORKLIST)
@@ -2307,7 +2338,7 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
     walk.idx = ld_uniform(work_indptr, wid);
     walk.end = ld_uniform(work_indptr, wid + 1);
   } else {
-    if (!balanced_start(walk, a, kv_indptr, context_lengths, wid, lane)) return;
+    if (!balanced_start(walk, a, kv_indptr, context_lengths, wid, lane, 1)) return;
   }
   auto next_piece = [&](Piece& p) -> bool {
     if constexpr (WORKLIST)
@@ -2663,7 +2694,8 @@ __device__ __forceinline__ void store_out2(void* out, int dtype, int64_t off, fl
 // (running log-sum-exp), with every load of a batch of pieces issued before
 // use.  Pairs a single run held whole were written by the decode; pairs with
 // no visible key get zeros; a cut pair's pieces are partial id segdesc[0]
-// (the first run's) and the first piece (id 2r) of each following run r.
+// (the first run's) and the first piece (id 2w) of the pair's wave w in each
+// following run (w G further on with head groups of G).
 template <int J>
 __global__ __launch_bounds__(256) void pa_fp8_segment_merge_kernel(const pa_fp8_stream_args a,
                                                                    const int32_t* segdesc, const uint16_t* part_out,
@@ -2688,6 +2720,9 @@ __global__ __launch_bounds__(256) void pa_fp8_segment_merge_kernel(const pa_fp8_
   if (a.kv_indptr) rl = a.kv_indptr[b + 1] - a.kv_indptr[b];
   const int nb = rl > 0 ? pa_plan_seq_chunks(ctx, ql, a.sliding_window) : 0;
   const int d0 = 8 * (lane & 15);
+  // Runs of the per-wave split (<= 16 columns) walk head groups: the pieces
+  // of one pair are G wave ids apart.
+  const int G = eq <= 16 ? balanced_group(a.num_kv_heads, a.num_workers, eq) : 1;
   int e[J], ec[J];  // column, and the column whose row a lane past eq reads instead
 #pragma unroll
   for (int j = 0; j < J; ++j) {
@@ -2713,7 +2748,7 @@ __global__ __launch_bounds__(256) void pa_fp8_segment_merge_kernel(const pa_fp8_
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) {
         const int i = i0 + k < cnt ? i0 + k : cnt - 1;
-        const int64_t pid = i == 0 ? pid0 : 2 * (int64_t)(w0 + i);
+        const int64_t pid = i == 0 ? pid0 : 2 * ((int64_t)w0 + (int64_t)i * G);
 #pragma unroll
         for (int j = 0; j < J; ++j) {
           l[k][j] = part_lse[pid * eq + ec[j]];
@@ -3768,19 +3803,17 @@ int device_cu_count(hipStream_t s) {
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // Query DMA instructions per piece of a streaming launch (4 columns each).
-int stream_nq(int eq) { return eq <= 4 ? 1 : (eq <= 8 ? 2 : 4); }
-
 int stream_lds_bytes(int nq, bool per_token) {
   const int stage = kKBytes + kVBytes + (per_token ? kScaleBytes : 0);
-  return kWaves * (kStages * stage + 2 * nq * 1024);
+  return stream_waves(nq) * (kStages * stage + 2 * nq * 1024);
 }
 
 template <bool PT, bool BS16, bool WL, int NQ>
 hipError_t launch_stream(const pa_fp8_stream_args& a, unsigned grid, hipStream_t s, int32_t* desc, float* po,
                          float* pl) {
-  hipLaunchKernelGGL((pa_fp8_stream_kernel<PT, BS16, WL, NQ>), dim3(grid), dim3(kThreads), 0, s, a, a.block_tables,
-                     a.kv_indptr, a.context_lengths, a.key_scale, a.value_scale, a.work_indptr, a.work_info,
-                     a.partition_indptr, desc, po, pl, a.output);
+  hipLaunchKernelGGL((pa_fp8_stream_kernel<PT, BS16, WL, NQ>), dim3(grid), dim3(64 * stream_waves(NQ)), 0, s, a,
+                     a.block_tables, a.kv_indptr, a.context_lengths, a.key_scale, a.value_scale, a.work_indptr,
+                     a.work_info, a.partition_indptr, desc, po, pl, a.output);
   return hipGetLastError();
 }
 
@@ -3856,7 +3889,8 @@ hipError_t launch_bin(const pa_fp8_stream_args& a, hipStream_t s) {
 // cooperative workgroup runs.
 hipError_t dispatch_balanced(const pa_fp8_stream_args& a, hipStream_t s, int32_t* desc, float* po, float* pl) {
   const int eq = a.query_length * a.query_group_size;
-  if (eq <= 16) return dispatch_stream<false>(a, (unsigned)pa_cdiv(a.num_workers, kWaves), s, desc, po, pl);
+  if (eq <= 16)
+    return dispatch_stream<false>(a, (unsigned)pa_cdiv(a.num_workers, stream_waves(stream_nq(eq))), s, desc, po, pl);
   return coop_waves(eq) == 2 ? dispatch_coop_nw<2, false>(a, (unsigned)a.num_workers, s, desc, po, pl)
                              : dispatch_coop_nw<4, false>(a, (unsigned)a.num_workers, s, desc, po, pl);
 }
@@ -4103,7 +4137,7 @@ int pa_fp8_stream_workers(int num_cu, int query_length, int query_group_size, in
   if (eq > 16) return num_cu * coop_per_cu(coop_waves(eq));
   const int lds = stream_lds_bytes(stream_nq(eq), per_token_kv != 0);
   const int per_cu = 160 * 1024 / lds >= 2 ? 2 : 1;
-  return num_cu * per_cu * kWaves;
+  return num_cu * per_cu * stream_waves(stream_nq(eq));
 }
 
 int64_t pa_fp8_balanced_workspace_bytes(int num_seqs, int num_kv_heads, int query_length, int query_group_size,

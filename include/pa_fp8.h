@@ -211,6 +211,9 @@ int pa_fp8_decode_reduce(const pa_fp8_reduce_args* args, void* hip_stream);
  * pa_fp8_decode_balanced: no work list; the kernel cuts the chunks of all
  * (sequence, kv head) pairs into num_workers equal runs itself (stream-K),
  * so ragged batches load every wave equally without a host round trip.
+ * With up to 16 columns the runs are per wave and, when 4 (or 2) divides
+ * both num_kv_heads and num_workers, cover groups of that many adjacent kv
+ * heads walked by the waves of one workgroup in step.
  * Pairs a single wave holds whole go straight to `output`; then
  * pa_fp8_merge_balanced, on the same stream and with the same arguments
  * and workspace, merges the pieces of the pairs that were cut (and writes
