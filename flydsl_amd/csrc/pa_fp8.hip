@@ -1331,6 +1331,20 @@ __global__ __launch_bounds__(64 * WAVES) void pa_fp8_partition_kernel(const pa_f
 // Per-wave streaming decode (work list or balanced split)
 // ============================================================================
 
+// Cost of a (sequence, kv head) pair's start, in chunks, in the per-wave
+// balanced split: a run that holds more pieces (each with its query setup
+// and its output or partial store) gets fewer chunks.
+#ifndef PA_FP8_PIECE_COST
+#define PA_FP8_PIECE_COST 1
+#endif
+constexpr int kStreamPieceCost = PA_FP8_PIECE_COST;
+// The same for the cooperative kernel's workgroup runs, whose pieces also
+// start with a 64-column query setup and end in a partly filled unit.
+#ifndef PA_FP8_COOP_PIECE_COST
+#define PA_FP8_COOP_PIECE_COST 4
+#endif
+constexpr int kCoopPieceCost = PA_FP8_COOP_PIECE_COST;
+
 // A balanced launch gives every wave at least this many chunks (it uses
 // fewer waves for small problems).
 constexpr int kMinChunksPerWave = 8;
@@ -1380,38 +1394,44 @@ __device__ __forceinline__ void piece_sequence(Piece& p, const pa_fp8_stream_arg
 }
 
 // Balanced split: chunks of all (sequence, kv head) pairs, sequence-major
-// with kv heads inner, cut into nw equal runs (pa_plan_run_begin).  With a
+// with kv heads inner, each pair preceded by A units of start cost, cut into
+// nw equal runs (pa_plan_run_begin).  With a
 // head group G > 1 the split runs over (sequence, group of G adjacent kv
 // heads, chunk) and each run is walked by G consecutive waves in step, wave
 // i taking head i of every group: the waves of a workgroup then read the
 // same pages of adjacent heads at the same time, and adjacent heads'
 // per-token scales, which share 128-byte lines, are fetched once.
 struct BalancedWalk {
-  int b, h, nb, c, left, first, wid, run, G, nw;
-  long long gseg, T;  // global index of chunk 0 of pair (b, h)'s group; total (group) chunks
-  Piece seq;          // sequence-level fields of b
+  int b, h, nb, c, first, wid, run, G, A, nw;
+  // Positions in the split's cost order (a pair's group costs A, then one
+  // per chunk): of the next chunk, of the end of this run, of the current
+  // group's start; and the total.
+  long long pos, end, P, T;
+  Piece seq;  // sequence-level fields of b
 
   __device__ __forceinline__ bool next(Piece& p, const pa_fp8_stream_args& a, const int32_t* kv_indptr,
                                        const int32_t* context_lengths) {
-    if (left <= 0) return false;
+    if (pos >= end) return false;
     p = seq;
     p.h = h;
     p.tb0 = (seq.lo_all & ~(kChunk - 1)) + c * kChunk;
-    p.n = pa_min(nb - c, left);
+    const long long rem = end - pos;
+    p.n = rem < nb - c ? (int)rem : nb - c;
     const bool whole = c == 0 && p.n == nb;
     p.target = whole ? -1 : 2 * wid + (first ? 0 : 1);
-    p.desc_cnt = c != 0 ? 0 : (whole ? 1 : pa_plan_run_of_chunk(gseg + nb - 1, T, nw) - run + 1);
-    left -= p.n;
+    p.desc_cnt = c != 0 ? 0 : (whole ? 1 : pa_plan_run_of_chunk(P + A + nb - 1, T, nw) - run + 1);
     first = 0;
     c += p.n;
-    if (left > 0 && c == nb) {
+    pos += p.n;
+    if (pos < end && c == nb) {
       c = 0;
-      gseg += nb;
+      P += nb + A;
+      pos = P + A;
       if ((h += G) >= a.num_kv_heads) {
         h -= a.num_kv_heads;  // head i of the next sequence's first group
         do {
           if (b + 1 >= a.num_seqs) {  // inconsistent context lengths: stop
-            left = 0;
+            pos = end;
             break;
           }
           ++b;
@@ -1486,7 +1506,7 @@ __host__ __device__ constexpr int balanced_group(int H, int num_workers, int eq)
 __device__ __forceinline__ bool balanced_start(BalancedWalk& w, const pa_fp8_stream_args& a,
                                                const int32_t* __restrict__ kv_indptr,
                                                const int32_t* __restrict__ context_lengths, int wid, int lane,
-                                               int G) {
+                                               int G, int A) {
   const int H = a.num_kv_heads / G;  // head groups
   const int ql = a.query_length;
   const int W = a.sliding_window;
@@ -1508,7 +1528,7 @@ __device__ __forceinline__ bool balanced_start(BalancedWalk& w, const pa_fp8_str
   for (int k = 0; k < 16; ++k) {
     const bool real = k < K && lane * K + k < B;
     cnt[k] = real && rl[k] > 0 ? pa_plan_seq_chunks(cnt[k], ql, W) : 0;
-    mine += cnt[k];
+    mine += cnt[k] > 0 ? cnt[k] + A : 0;
   }
   int incl = mine;
 #pragma unroll
@@ -1538,28 +1558,34 @@ __device__ __forceinline__ bool balanced_start(BalancedWalk& w, const pa_fp8_str
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
     const int ck = __builtin_amdgcn_readlane(cnt[k], ls);
+    const int qk = ck > 0 ? ck + A : 0;
     if (b0 < 0 && k < K) {
-      if ((S + ck) * H > g0) {
+      if ((S + qk) * H > g0) {
         b0 = ls * K + k;
         n0 = ck;
       } else {
-        S += ck;
+        S += qk;
       }
     }
   }
   if (b0 < 0 || n0 <= 0) return false;  // as above
   const long long off = g0 - S * H;
-  const int hg = (int)(off / n0);
+  const int q0 = n0 + A;  // cost of one group of sequence b0
+  const int hg = (int)(off / q0);
+  const int o = (int)(off - (long long)hg * q0);
   w.b = b0;
   w.nb = n0;
   w.h = hg * G + (wid - run * G);
-  w.c = (int)(off - (long long)hg * n0);
-  w.gseg = S * H + (long long)hg * n0;
-  w.left = (int)(g1 - g0);
+  w.c = o > A ? o - A : 0;  // a start inside the group's overhead takes chunk 0
+  w.P = S * H + (long long)hg * q0;
+  w.pos = w.P + A + w.c;
+  w.end = g1;
+  if (w.pos >= w.end) return false;  // the run holds only overhead
   w.first = 1;
   w.wid = wid;
   w.run = run;
   w.G = G;
+  w.A = A;
   w.nw = nw;
   w.T = T;
   piece_sequence(w.seq, a, kv_indptr, context_lengths, b0);
@@ -1757,7 +1783,7 @@ __global__ __launch_bounds__(64 * stream_waves(NQ)) void pa_fp8_stream_kernel(
     walk.end = ld_uniform(work_indptr, wid + 1);
   } else {
     const int G = balanced_group(a.num_kv_heads, a.num_workers, eq);
-    if (!balanced_start(walk, a, kv_indptr, context_lengths, wid, lane, G)) return;
+    if (!balanced_start(walk, a, kv_indptr, context_lengths, wid, lane, G, kStreamPieceCost)) return;
   }
   auto next_piece = [&](Piece& p) -> bool {
     if constexpr (WORKLIST)
@@ -2338,7 +2364,7 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
     walk.idx = ld_uniform(work_indptr, wid);
     walk.end = ld_uniform(work_indptr, wid + 1);
   } else {
-    if (!balanced_start(walk, a, kv_indptr, context_lengths, wid, lane, 1)) return;
+    if (!balanced_start(walk, a, kv_indptr, context_lengths, wid, lane, 1, kCoopPieceCost)) return;
   }
   auto next_piece = [&](Piece& p) -> bool {
     if constexpr (WORKLIST)

@@ -3,8 +3,9 @@ pa_fp8_stream_kernel / pa_fp8_coop_kernel and the partial ids that
 pa_fp8_segment_merge_kernel reads), with head groups.
 
 The split lays the chunks of every (sequence, head group of G adjacent kv
-heads) end to end and cuts them into equal runs; the G waves of a run walk
-head i of each group in step.  The model restates the kernel's start
+heads) end to end, each group preceded by A units of start cost (1 for the
+per-wave kernel, 4 for the cooperative one), and cuts them into equal runs;
+the G waves of a run walk head i of each group in step.  The model restates the kernel's start
 search, walk and merge addressing on random batches and checks what the
 GPU results depend on: every chunk of every (sequence, kv head) pair is
 computed exactly once, a pair held whole writes its output row, and for a
@@ -51,16 +52,19 @@ def stream_nq(eq):
 
 
 def balanced_group(H, workers, eq):
+    if eq > 16:  # cooperative workgroup runs: no head groups
+        return 1
     g = stream_waves(stream_nq(eq))
     while g > 1 and (H % g or workers % g):
         g //= 2
     return g
 
 
-def walk(nbs, H, workers, G, wid):
-    """Pieces (b, h, c, n, target, desc_cnt) of worker wid."""
+def walk(nbs, H, workers, G, wid, A=0):
+    """Pieces (b, h, c, n, target, desc_cnt) of worker wid; each (sequence,
+    head group) costs A before its chunks in the split's order."""
     Hg = H // G
-    T = sum(nbs) * Hg
+    T = sum(n + A for n in nbs if n) * Hg
     nw = min(max(1, T // MIN_CHUNKS_PER_WAVE), workers // G)
     run = wid // G
     if run >= nw:
@@ -70,32 +74,35 @@ def walk(nbs, H, workers, G, wid):
         return []
     S = 0
     for b0, n0 in enumerate(nbs):
-        if n0 > 0 and (S + n0) * Hg > g0:
+        q = n0 + A if n0 else 0
+        if n0 > 0 and (S + q) * Hg > g0:
             break
-        S += n0
+        S += q
     off = g0 - S * Hg
-    hg, c = divmod(off, n0)
-    b, nb, h = b0, n0, hg * G + (wid - run * G)
-    gseg, left, first = S * Hg + hg * n0, g1 - g0, True
+    hg, o = divmod(off, n0 + A)
+    b, nb, h, c = b0, n0, hg * G + (wid - run * G), max(o - A, 0)
+    P = S * Hg + hg * (n0 + A)
+    pos, end, first = P + A + c, g1, True
     out = []
-    while left > 0:
-        n = min(nb - c, left)
+    while pos < end:
+        n = min(nb - c, end - pos)
         whole = c == 0 and n == nb
         target = -1 if whole else 2 * wid + (0 if first else 1)
-        desc = 0 if c else (1 if whole else run_of_chunk(gseg + nb - 1, T, nw) - run + 1)
+        desc = 0 if c else (1 if whole else run_of_chunk(P + A + nb - 1, T, nw) - run + 1)
         out.append((b, h, c, n, target, desc))
-        left -= n
         first = False
         c += n
-        if left > 0 and c == nb:
+        pos += n
+        if pos < end and c == nb:
             c = 0
-            gseg += nb
+            P += nb + A
+            pos = P + A
             h += G
             if h >= H:
                 h -= H
                 while True:
                     if b + 1 >= len(nbs):
-                        left = 0
+                        pos = end
                         break
                     b += 1
                     nb = nbs[b]
@@ -104,12 +111,12 @@ def walk(nbs, H, workers, G, wid):
     return out
 
 
-def check(ctxs, H, ql, window, workers, eq):
+def check(ctxs, H, ql, window, workers, eq, A=0):
     nbs = [seq_chunks(c, ql, window) for c in ctxs]
     G = balanced_group(H, workers, eq)
     pieces = {}
     for wid in range(workers):
-        for b, h, c, n, target, desc in walk(nbs, H, workers, G, wid):
+        for b, h, c, n, target, desc in walk(nbs, H, workers, G, wid, A):
             pieces.setdefault((b, h), []).append((c, n, target, desc))
     for b, nb in enumerate(nbs):
         for h in range(H):
@@ -139,7 +146,7 @@ def test_every_chunk_once_and_merge_reads_the_written_pieces(seed):
     window = rng.choice([0, 0, 100, 1000])
     eq = ql * rng.choice([1, 2, 4, 8, 16])
     workers = rng.choice([4, 6, 8, 12, 16, 64, 2048])
-    check(ctxs, H, ql, window, workers, eq)
+    check(ctxs, H, ql, window, workers, eq, A=rng.choice([0, 1, 2, 4, 5]))
 
 
 def test_head_groups_of_the_benchmark_shapes():
@@ -152,3 +159,6 @@ def test_head_groups_of_the_benchmark_shapes():
     assert check([900, 3000, 5], 4, 1, 0, 7, 4) == 1
     # more than 4 columns (two query images per wave) keep 4-wave groups
     assert check([900, 3000, 5], 8, 2, 0, 64, 8) == 4
+    # the shipped start costs: per-wave runs (A = 1), cooperative workgroup runs (A = 4, no groups)
+    assert check([2048, 17, 32768, 1, 700] * 8, 8, 1, 0, 2048, 4, A=1) == 4
+    assert check([4096, 8000, 5000, 6144] * 16, 4, 4, 0, 512, 64, A=4) == 1
