@@ -594,10 +594,11 @@ enum {
   PA_VIOLATION_POSITION = 4, /* rope position outside [0, max_pos) */
   PA_VIOLATION_SLOT = 8      /* KV-cache slot past the last cache block */
 };
-/* ORs the bits recorded since the last call into *bits and clears them
- * (always 0 in a release build).  Synchronises the current device; returns
- * PA_OK or a HIP error code.  No counterpart in the reference: a debug aid
- * for callers chasing a bad page table or slot mapping. */
+/* ORs the bits recorded on the current device since the last call into
+ * *bits and clears them (always 0 in a release build; each device keeps its
+ * own bits).  Synchronises the current device; returns PA_OK or a HIP error
+ * code.  No counterpart in the reference: a debug aid for callers chasing a
+ * bad page table or slot mapping. */
 int pa_fp8_debug_violations(unsigned int* bits);
 /* 1 in a checked build, 0 in a release build. */
 int pa_fp8_checked_build(void);
