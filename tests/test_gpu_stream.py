@@ -106,6 +106,9 @@ BALANCED_CASES = {
     "mtp_ql2_gqa2_pt": dict(batch=6, query_length=2, num_query_heads=4, num_kv_heads=2, per_token=True,
                             ctx_range=(2, 4000)),
     "gqa1": dict(batch=5, num_query_heads=8, num_kv_heads=8, ctx_range=(1, 2500)),
+    # head groups of 2 over 6 kv heads and of 4 over 12 (three groups per sequence)
+    "gqa4_h6_pt": dict(batch=5, num_query_heads=24, num_kv_heads=6, per_token=True, ctx=[1, 700, 33, 4000, 1500]),
+    "gqa2_h12": dict(batch=4, num_query_heads=24, num_kv_heads=12, ctx=[900, 17, 2600, 5]),
     "page64_ragged": dict(batch=7, block_size=64, ctx=[1, 64, 65, 900, 4000, 130, 2049], per_token=True),
     "uniform_data": dict(batch=6, dist="uniform", ctx_range=(1, 3000)),
     # 6, 12 and 24 query columns: the merge's last 16-column block is part-filled
