@@ -2337,7 +2337,9 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
   static_assert(S >= 2 * U, "the refill after a unit's barrier covers the next unit");
   // Chunk slot: keys, values, per-token K then V scales.
   constexpr int kSlotBytes = kKBytes + kVBytes + (PER_TOKEN ? kScaleBytes : 0);
-  constexpr int kDmaPerWave = 8 / NW;  // of a chunk's 8 one-KiB key/value loads
+  // Chunk j of the launch is loaded whole by wave j % NW: 8 one-KiB key and
+  // value loads and, with per-token scales, one scale load.
+  constexpr int kChunkLoads = 8 + (PER_TOKEN ? 1 : 0);
   __shared__ __attribute__((aligned(16))) unsigned char smem[S * kSlotBytes];
 
   const int tid = threadIdx.x;
@@ -2354,8 +2356,6 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
   const int nblocks = a.num_blocks;
   const int e = wave * 16 + c16;  // this lane's query column
   // The last wave also loads every chunk's per-token scales; loads per chunk:
-  const bool scale_wave = PER_TOKEN && wave == NW - 1;
-  const int lpc = kDmaPerWave + (scale_wave ? 1 : 0);
 
   using Walk = typename std::conditional<WORKLIST, WorklistWalk, BalancedWalk>::type;
   Walk walk;
@@ -2396,41 +2396,36 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
   int itb = 0, ih = 0, ilast = 0, irem = 0, iw = 0;
   int ipos = 0;  // position of the next chunk in its piece
   int64_t ibt = 0;
-  // This wave's share of every chunk, fixed for the launch: load i = wave *
-  // kDmaPerWave + j of a chunk's eight 1 KiB loads is keys for i < 4 (else
-  // values), 16-token half hh = (i >> 1) & 1, 1 KiB piece q2 = i & 1.  A
-  // wave's loads are all keys or all values, so each chunk costs it one
-  // address (page base + in-page offset) plus per-lane constants.
-  const bool wk = wave < NW / 2;
-  const uint8_t* const rbase = (const uint8_t*)(wk ? a.key_cache : a.value_cache);
-  const int64_t rstride_head = wk ? a.stride_k_head : a.stride_v_head;
-  const int64_t rstride_block = wk ? a.stride_k_block : a.stride_v_block;
-  // In-page offset of a chunk at page slot s0: (s0 >> sh1) << sh2.
-  const int sh1 = (!wk && a.trans_v) ? 4 : 0;
-  const int sh2 = wk ? 4 : (a.trans_v ? 11 : 0);
-  int loff[kDmaPerWave], ldsoff[kDmaPerWave];
-  bool hsel[kDmaPerWave];
+  // A chunk's eight 1 KiB loads, fixed for the launch: load i is keys for
+  // i < 4 (else values), 16-token half hh = (i >> 1) & 1, 1 KiB piece
+  // q2 = i & 1.  The wave that loads a chunk computes its key and value page
+  // addresses once (page base + in-page offset) and adds per-lane constants.
+  // In-page offset of a chunk at page slot s0: keys s0 << 4, values
+  // (s0 >> vsh1) << vsh2.
+  const int vsh1 = a.trans_v ? 4 : 0;
+  const int vsh2 = a.trans_v ? 11 : 0;
+  int loff[8];
 #pragma unroll
-  for (int j = 0; j < kDmaPerWave; ++j) {
-    const int i = wave * kDmaPerWave + j;
+  for (int i = 0; i < 8; ++i) {
+    const bool ki = i < 4;
     const int hh = (i >> 1) & 1, q2 = i & 1;
-    hsel[j] = hh != 0;
     if (BS16)
-      loff[j] = (wk ? koff_lane : lane * 16) + q2 * 1024;
-    else if (wk)
-      loff[j] = hh * 256 + q2 * (4 * bs * 16) + koff_lane;
+      loff[i] = (ki ? koff_lane : lane * 16) + q2 * 1024;
+    else if (ki)
+      loff[i] = hh * 256 + q2 * (4 * bs * 16) + koff_lane;
     else if (a.trans_v)
-      loff[j] = hh * 2048 + q2 * 1024 + lane * 16;
+      loff[i] = hh * 2048 + q2 * 1024 + lane * 16;
     else
-      loff[j] = hh * 16 + q2 * (64 * bs) + voff_plain;
-    ldsoff[j] = (wk ? hh * kKHalf : kKBytes + hh * 2048) + q2 * 1024;
+      loff[i] = hh * 16 + q2 * (64 * bs) + voff_plain;
   }
-  const uint8_t* ibase = rbase;  // rbase + ih * rstride_head
+  const uint8_t* ikb = (const uint8_t*)a.key_cache;    // + ih * stride_k_head
+  const uint8_t* ivb = (const uint8_t*)a.value_cache;  // + ih * stride_v_head
   // Page strides fit 31 bits (checked on the host), so a page's offset is
   // one unsigned 32 x 32 -> 64-bit product.
-  const uint32_t rsb = (uint32_t)rstride_block;
+  const uint32_t ksb = (uint32_t)a.stride_k_block;
+  const uint32_t vsb = (uint32_t)a.stride_v_block;
   const uint32_t ssb = (uint32_t)a.stride_ks_block;
-  // the scale wave's lane: its scale row base for the piece's kv head
+  // a scale load's lane: its scale row base for the piece's kv head
   const int tt = (lane & 7) * 4;
   const float* const sbase0 = ((lane & 8) ? value_scale : key_scale) + (BS16 ? (tt & 15) : tt);
   const float* sbase = sbase0;
@@ -2457,7 +2452,8 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
     ipos = 0;
     iw = which;
     iok = true;
-    ibase = rbase + (int64_t)ih * rstride_head;
+    ikb = (const uint8_t*)a.key_cache + (int64_t)ih * a.stride_k_head;
+    ivb = (const uint8_t*)a.value_cache + (int64_t)ih * a.stride_v_head;
     if (PER_TOKEN) sbase = sbase0 + (int64_t)ih * a.stride_ks_head;
     nlp = -1;
     fetch_pages();
@@ -2473,27 +2469,38 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
   int issued = 0;    // chunks this workgroup has issued
   int islot = 0;     // their next slot: issued % S
   auto issue_next = [&]() {
-    const int p0 = clamp_page(np0);
-    const int p1 = BS16 ? clamp_page(np1) : p0;
-    const int64_t inpage = BS16 ? 0 : (int64_t)(((itb & (bs - 1)) >> sh1) << sh2);
-    LDS_AS unsigned char* sk = (LDS_AS unsigned char*)smem + islot * kSlotBytes;
-    islot = islot + 1 == S ? 0 : islot + 1;
-    const uint8_t* pb0 = ibase + (uint64_t)(uint32_t)p0 * rsb + inpage;
-    const uint8_t* pb1 = BS16 ? ibase + (uint64_t)(uint32_t)p1 * rsb : pb0;
-    // Four-chunk units: key token r of the chunk at unit position c goes to
-    // row r ^ 4c of its 16-token half (lane l of a key load fetches token
-    // (l & 15) ^ 4c), so the QK reads -- four tokens of each of the unit's
-    // four chunks per 16 lanes -- hit 16 different rows instead of the same
-    // banks of four slots.
-    const int kswz = (U == 4 && wk) ? (ipos & 3) << 6 : 0;
+    if (issued % NW == wave) {  // workgroup-uniform: every wave walks the same chunks
+      const int p0 = clamp_page(np0);
+      const int p1 = BS16 ? clamp_page(np1) : p0;
+      const int s0 = itb & (bs - 1);
+      const int64_t kin = BS16 ? 0 : (int64_t)(s0 << 4);
+      const int64_t vin = BS16 ? 0 : (int64_t)((s0 >> vsh1) << vsh2);
+      LDS_AS unsigned char* sk = (LDS_AS unsigned char*)smem + islot * kSlotBytes;
+      const uint8_t* k0 = ikb + (uint64_t)(uint32_t)p0 * ksb + kin;
+      const uint8_t* k1 = BS16 ? ikb + (uint64_t)(uint32_t)p1 * ksb : k0;
+      const uint8_t* v0 = ivb + (uint64_t)(uint32_t)p0 * vsb + vin;
+      const uint8_t* v1 = BS16 ? ivb + (uint64_t)(uint32_t)p1 * vsb : v0;
+      // Four-chunk units: key token r of the chunk at unit position c goes to
+      // row r ^ 4c of its 16-token half (lane l of a key load fetches token
+      // (l & 15) ^ 4c), so the QK reads -- four tokens of each of the unit's
+      // four chunks per 16 lanes -- hit 16 different rows instead of the same
+      // banks of four slots.
+      const int kswz = U == 4 ? (ipos & 3) << 6 : 0;
 #pragma unroll
-    for (int j = 0; j < kDmaPerWave; ++j)
-      lds_dma16(((BS16 && hsel[j]) ? pb1 : pb0) + (loff[j] ^ kswz), sk + ldsoff[j]);
-    if (scale_wave && lane < 16) {
-      const int pg = BS16 ? (tt >= 16 ? p1 : p0) : p0;
-      const int sidx = BS16 ? 0 : (itb & (bs - 1));
-      lds_dma16_cached(sbase + (uint64_t)(uint32_t)pg * ssb + sidx, sk + kKBytes + kVBytes);
+      for (int i = 0; i < 8; ++i) {
+        const int hh = (i >> 1) & 1, q2 = i & 1;
+        const uint8_t* src =
+            i < 4 ? ((BS16 && hh) ? k1 : k0) + (loff[i] ^ kswz) : ((BS16 && hh) ? v1 : v0) + loff[i];
+        const int dst = (i < 4 ? hh * kKHalf : kKBytes + hh * 2048) + q2 * 1024;
+        lds_dma16(src, sk + dst);
+      }
+      if (PER_TOKEN && lane < 16) {
+        const int pg = BS16 ? (tt >= 16 ? p1 : p0) : p0;
+        const int sidx = BS16 ? 0 : (itb & (bs - 1));
+        lds_dma16_cached(sbase + (uint64_t)(uint32_t)pg * ssb + sidx, sk + kKBytes + kVBytes);
+      }
     }
+    islot = islot + 1 == S ? 0 : islot + 1;
     ++issued;
     ++ipos;
     itb += kChunk;
@@ -2550,42 +2557,37 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
         asm volatile("s_barrier" ::: "memory");
         while (issued < gc + nch) issue_next();
       }
-      // This wave's loads of the unit: up to two newer chunks may stay in
-      // flight (loads retire in order; more newer chunks, or query rows
-      // issued in between, are only waited for early).
-      const int newer = issued - gc - nch;
-      if (newer >= 2) {
-        if (scale_wave)
-          __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * (kDmaPerWave + 1)));
-        else
-          __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * kDmaPerWave));
-      } else if (newer == 1) {
-        if (scale_wave)
-          __builtin_amdgcn_s_waitcnt(vmcnt_only(kDmaPerWave + 1));
-        else
-          __builtin_amdgcn_s_waitcnt(vmcnt_only(kDmaPerWave));
-      } else {
+      // This wave's chunks of the unit: its chunks issued after them (chunk
+      // j is this wave's when j % NW == wave) may stay in flight (loads
+      // retire in order; query rows issued in between are only waited for
+      // early).
+      const int own_newer = (issued + NW - 1 - wave) / NW - (gc + nch + NW - 1 - wave) / NW;
+      if (own_newer >= 3)
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(3 * kChunkLoads));
+      else if (own_newer == 2)
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * kChunkLoads));
+      else if (own_newer == 1)
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(kChunkLoads));
+      else
         __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-      }
       // Value bytes of page slots outside the sequence's visible keys
       // [lo_all, hi_all) -- a page's tail past the context, slots before a
       // window -- may hold any byte, e4m3fn NaN included, which a zero
-      // probability does not cancel.  The wave that loaded a 16-token value
-      // half zeroes them (edge units only; workgroup-uniform test), so the
-      // value products need no masks.
-      if (!wk) {
+      // probability does not cancel.  The wave that loaded a chunk zeroes
+      // them (edge units only; workgroup-uniform test), so the value
+      // products need no masks.
+      {
         const int ub = cur.tb0 + u * (U * kChunk);
         if (ub < cur.lo_all || ub + nch * kChunk > cur.hi_all) {
           for (int ch = 0; ch < nch; ++ch) {
+            if ((gc + ch) % NW != wave) continue;
             int sl = cslot + ch;
             sl = sl >= S ? sl - S : sl;
 #pragma unroll
-            for (int j = 0; j < kDmaPerWave; j += 2) {
-              const int hh = ((wave * kDmaPerWave + j) >> 1) & 1;  // this wave's loads j, j + 1
+            for (int hh = 0; hh < 2; ++hh)
               zero_stale_values((LDS_AS unsigned char*)smem + sl * kSlotBytes + kKBytes + hh * 2048,
                                 ub + ch * kChunk + 16 * hh, cur.lo_all, cur.hi_all, lane);
-            }
-            if (U == 4 && scale_wave) {
+            if (U == 4 && PER_TOKEN) {
               // and the chunk's per-token K and V scales of those keys
               // (lane l: K scale l < 32, else V scale l - 32), so that the
               // softmax reads zeros there rather than stale bits
