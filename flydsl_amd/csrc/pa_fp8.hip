@@ -69,7 +69,6 @@ constexpr int kWaves = PA_FP8_WAVES;
 __host__ __device__ constexpr int stream_waves(int nq) { return nq == 1 ? PA_FP8_STREAM_WAVES : 4; }
 // Query images (of 4 columns) per wave of the streaming decode for eq columns.
 __host__ __device__ constexpr int stream_nq(int eq) { return eq <= 4 ? 1 : (eq <= 8 ? 2 : 4); }
-constexpr int kThreads = 64 * kWaves;
 constexpr int kHead = 128;
 constexpr int kChunk = 32;                  // tokens per wave step
 // Key image of one chunk in LDS: two 16-token halves, each [8 dim chunks]
