@@ -828,13 +828,10 @@ __device__ __forceinline__ void unit4_softmax_pv(WaveState<1>& s, const QueryTil
     }
     __builtin_amdgcn_s_setprio(0);
   }
-  // x = l + C0: l the base-2 logit (the key product times the per-token key
-  // scale), C0 from the current references (the column's maximum m, 0 while
-  // it has none, and the value-scale reference); -inf for keys the column
-  // does not see.
-  const float m_old = s.m2[0] == kNegInf ? 0.0f : s.m2[0];
-  float vmul = PER_TOKEN && s.vsmax > 0.0f ? s.vsmax : 1.0f;
-  const float C0 = kPBias - m_old - (PER_TOKEN ? __builtin_amdgcn_logf(vmul) : 0.0f);
+  // y: the key product times the per-token key scale (the base-2 logit is
+  // y * post, post > 0), -inf for keys the column does not see.  The unit's
+  // maximum is taken on y, so the references settle before any exponent is
+  // formed and every x = y * post + C is computed once, with the final C.
   const float post = q.fac[0];  // > 0 (prepare_query)
   float x[32];
 #pragma unroll
@@ -842,7 +839,7 @@ __device__ __forceinline__ void unit4_softmax_pv(WaveState<1>& s, const QueryTil
     f32x4 ks = {1.f, 1.f, 1.f, 1.f};
     if (PER_TOKEN) ks = *(const LDS_AS f32x4*)(sb + 4 * t);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[4 * t + i] = __builtin_fmaf(lg4[t][i], PER_TOKEN ? ks[i] * post : post, C0);
+    for (int i = 0; i < 4; ++i) x[4 * t + i] = PER_TOKEN ? lg4[t][i] * ks[i] : lg4[t][i];
   }
   if (!full) {
     // a real branch: speculated, these selects would run on every unit
@@ -853,6 +850,28 @@ __device__ __forceinline__ void unit4_softmax_pv(WaveState<1>& s, const QueryTil
   float xmax = kNegInf;
 #pragma unroll
   for (int k = 0; k < 32; ++k) xmax = fmaxf(xmax, x[k]);
+  // The column's maximum base-2 logit this unit is max y * post.  The
+  // maximum reference moves to it when it passes the reference by more than
+  // kLazyMax (and on the column's first visible key); the value-scale
+  // reference moves to the unit's largest scale when that exceeds twice it.
+  // Every probability is then at most 2^(kPBias + kLazyMax) times a
+  // value-scale ratio of at most 2.
+  const float lmax = max_over_groups(xmax) * post;
+  const bool move = lmax > s.m2[0] + kLazyMax;
+  const bool vmove = PER_TOKEN && cmax > 2.0f * s.vsmax;  // wave-uniform
+  const float mnew = move ? lmax : s.m2[0];
+  const float muse = mnew == kNegInf ? 0.0f : mnew;
+  const float alpha = move ? __builtin_amdgcn_exp2f(s.m2[0] - muse) : 1.0f;
+  s.m2[0] = mnew;
+  float vratio = 1.0f;
+  if (vmove) {
+    vratio = s.vsmax > 0.0f ? s.vsmax * __builtin_amdgcn_rcpf(cmax) : 1.0f;
+    s.vsmax = cmax;
+  }
+  const float vmul = PER_TOKEN && s.vsmax > 0.0f ? s.vsmax : 1.0f;
+  // x = y * post + C, C from the settled references (the column's maximum m,
+  // 0 while it has none, and the value-scale reference)
+  const float C = kPBias - muse - (PER_TOKEN ? __builtin_amdgcn_logf(vmul) : 0.0f);
   // probabilities 2^x (times the value scale) into the fp8 hi + lo
   // operands PH, PL and their sum psum (stale value scales were zeroed in
   // LDS: a masked key gives 0 * 0)
@@ -870,7 +889,7 @@ __device__ __forceinline__ void unit4_softmax_pv(WaveState<1>& s, const QueryTil
       float pr[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float ev = __builtin_amdgcn_exp2f(x[8 * k8 + i]);
+        const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(x[8 * k8 + i], post, C));
         psum += ev;
         pr[i] = PER_TOKEN ? ev * (i < 4 ? v0[i] : v1[i - 4]) : ev;
       }
@@ -882,30 +901,6 @@ __device__ __forceinline__ void unit4_softmax_pv(WaveState<1>& s, const QueryTil
       PL[2 * k8 + 1] = (int)(uint32_t)((uint64_t)plo >> 32);
     }
   };
-  // The column's maximum logit this unit is max x - C0.  The maximum
-  // reference moves to it when it passes the reference by more than
-  // kLazyMax (and on the column's first visible key); the value-scale
-  // reference moves to the unit's largest scale when that exceeds twice
-  // it.  Then x shifts by the change of C.  Every probability is at most
-  // 2^(kPBias + kLazyMax) times a value-scale ratio of at most 2.
-  const float lmax = max_over_groups(xmax) - C0;
-  const bool move = lmax > s.m2[0] + kLazyMax;
-  const bool vmove = PER_TOKEN && cmax > 2.0f * s.vsmax;  // wave-uniform
-  float alpha = 1.0f, vratio = 1.0f;
-  if (__ballot(move) || vmove) {
-    const float mnew = move ? lmax : s.m2[0];
-    const float muse = mnew == kNegInf ? 0.0f : mnew;
-    alpha = move ? __builtin_amdgcn_exp2f(s.m2[0] - muse) : 1.0f;
-    s.m2[0] = mnew;
-    if (vmove) {
-      vratio = s.vsmax > 0.0f ? s.vsmax * __builtin_amdgcn_rcpf(cmax) : 1.0f;
-      s.vsmax = cmax;
-      vmul = cmax;
-    }
-    const float dx = (kPBias - muse - (PER_TOKEN ? __builtin_amdgcn_logf(vmul) : 0.0f)) - C0;
-#pragma unroll
-    for (int k = 0; k < 32; ++k) x[k] += dx;
-  }
   probabilities();
   const float f = alpha * vratio;
   if (__ballot(f != 1.0f)) scale_inplace(s.acc[0], f);
