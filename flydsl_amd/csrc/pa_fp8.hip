@@ -2349,7 +2349,6 @@ __global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8
   const int bs_shift = BS16 ? 4 : __builtin_ctz((unsigned)bs);
   const int nblocks = a.num_blocks;
   const int e = wave * 16 + c16;  // this lane's query column
-  // The last wave also loads every chunk's per-token scales; loads per chunk:
 
   using Walk = typename std::conditional<WORKLIST, WorklistWalk, BalancedWalk>::type;
   Walk walk;
