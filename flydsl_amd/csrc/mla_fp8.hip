@@ -186,12 +186,16 @@ __device__ __forceinline__ void rescale_acc(f32x4 (&o)[16][2][NHT], int ht, floa
 // builtin's DMA is in flight, the compiler's wait insertion takes every LDS
 // read to be unordered behind it and waits for each with lgkmcnt(0), which
 // serialises the pipelined key reads.  The DMA is awaited explicitly
-// (vmcnt(0) and a barrier before its stage is read).
+// (vmcnt(0) and a barrier before its stage is read).  The compiler sets M0
+// (an input operand); an LDS DMA must not read M0 in the cycle after an
+// SALU wrote it (the wait state hipcc puts between its own M0 write and
+// such a load), which the compiler cannot see inside the statement, hence
+// the s_nop.
 __device__ __forceinline__ void lds_dma16(const void* gsrc, LDS_AS void* ldst) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt"
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
                :
-               : "v"(gsrc), "s"((unsigned)(uintptr_t)ldst)
-               : "memory", "m0");
+               : "v"(gsrc), "{m0}"((unsigned)(uintptr_t)ldst)
+               : "memory");
 }
 
 constexpr int vmcnt_only(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | (7 << 4) | (15 << 8); }

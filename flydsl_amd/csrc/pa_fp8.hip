@@ -2316,9 +2316,12 @@ constexpr int kFarToken = 1 << 30;  // first token of a unit's missing chunk
 constexpr int coop_slots(int nw, bool worklist) { return nw == 4 && !worklist ? 9 : 6; }
 constexpr int coop_unit(int nw, bool worklist) { return nw == 4 && !worklist ? 4 : 2; }
 constexpr int coop_wgs_per_cu(int nw, bool worklist) { return nw == 4 && !worklist ? 2 : 3; }
+// Waves per SIMD those workgroups need (a workgroup's waves sit on distinct
+// SIMDs): the occupancy the kernel is compiled for.
+constexpr int coop_waves_per_simd(int nw, bool worklist) { return (coop_wgs_per_cu(nw, worklist) * nw + 3) / 4; }
 
 template <int NW, bool PER_TOKEN, bool BS16, bool WORKLIST>
-__global__ __launch_bounds__(64 * NW, coop_wgs_per_cu(NW, WORKLIST)) void pa_fp8_coop_kernel(
+__global__ __launch_bounds__(64 * NW, coop_waves_per_simd(NW, WORKLIST)) void pa_fp8_coop_kernel(
     const pa_fp8_stream_args a, const int32_t* __restrict__ block_tables, const int32_t* __restrict__ kv_indptr,
     const int32_t* __restrict__ context_lengths, const float* __restrict__ key_scale,
     const float* __restrict__ value_scale, const int32_t* __restrict__ work_indptr,
