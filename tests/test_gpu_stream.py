@@ -225,6 +225,34 @@ def test_balanced_prepared_inside_capture_replays():
         assert torch.equal(out, eager), f"replay {i}"
 
 
+def test_balanced_concurrent_streams():
+    """Decodes on two side streams with no ordering between them (a per-wave
+    and a cooperative balanced launch, each with its workspace from its own
+    stream): the library holds no mutable state they could share, so each
+    matches the oracle, on every one of several overlapping rounds."""
+    cases = [make_case(batch=9, ctx_range=(1, 6000), per_token=True, seed=143),
+             make_case(batch=5, query_length=4, num_query_heads=32, num_kv_heads=2, per_token=True,
+                       ctx_range=(4, 5000), seed=147)]
+    refs = [torch_oracle(c, float_out=False) for c in cases]
+    devs = [to_dev(c) for c in cases]
+    outs = [torch.empty(d["query"].shape, dtype=torch.bfloat16, device=DEV) for d in devs]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    for rnd in range(3):
+        print(f"[concurrent] round {rnd}", flush=True)
+        with balanced():
+            for d, out, s in zip(devs, outs, streams):
+                with torch.cuda.stream(s):
+                    out.fill_(float("nan"))
+                    pa_decode_ps_launch(out, d["query"], d["key_cache"], d["value_cache"], d["context_lengths"],
+                                        None, None, d["softmax_scale"], d["key_scale"], d["value_scale"],
+                                        block_tables=d["block_tables"])
+        torch.cuda.synchronize()
+        for i, (out, ref) in enumerate(zip(outs, refs)):
+            assert_parity(out, ref, f"concurrent stream {i} round {rnd}")
+
+
 WORKLIST_CASES = {
     "gqa4": dict(batch=6, ctx=[1, 300, 1025, 4096, 7000, 2500]),
     "gqa8_pt": dict(batch=5, num_query_heads=16, num_kv_heads=2, per_token=True, ctx_range=(1, 6000)),
