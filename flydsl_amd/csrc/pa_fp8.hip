@@ -2725,7 +2725,11 @@ __global__ __launch_bounds__(256) void pa_fp8_segment_merge_kernel(const pa_fp8_
                                                                    const int32_t* segdesc, const uint16_t* part_out,
                                                                    const float* part_lse) {
   constexpr int kCols = 4 * J;      // columns per wave
-  constexpr int kBatch = 16 / J;    // pieces whose loads are in flight together
+  // pieces whose loads are in flight together: two for 16-column blocks,
+  // which keeps the kernel at four waves per SIMD (126 VGPRs; four pieces
+  // take 170), so 1024 pairs of 64 columns merge in one round of
+  // workgroups
+  constexpr int kBatch = J == 4 ? 2 : 16 / J;
   static_assert(kHead == 128, "16 lanes cover one 256-byte bf16 row");
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
