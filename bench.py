@@ -69,7 +69,7 @@ def parse_args():
     p.add_argument("--steps", type=int, default=100)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--config", default="c2_llama8b",
-                   help="c1_tiny|c2_llama8b|c3_ragged|c4_window|c5_mtp|all (decode), c3_ragged_p1024 "
+                   help="c1_tiny|c2_llama8b|c3_ragged|c4_window|c5_mtp|all (decode), c3_ragged_p1024|c5_mtp_p1024 "
                         "(work-list route), c2_d64|c2_d256 (head sizes 64 and 256), "
                         "rope_decode_llama8b|rope_prefill_llama8b (KV-cache writer), "
                         "qknr_prefill_v4|qknr_decode_v4 (fused RMSNorm + GPT-J RoPE + fp8 quant), "

@@ -2848,6 +2848,80 @@ __global__ __launch_bounds__(256) void pa_fp8_worklist_reduce_kernel(const pa_fp
              o0, o1);
 }
 
+// Work-list merge for head size 128 with query heads in blocks of eight:
+// one wave per (reduce group, query row, block).  Load j of a piece reads
+// two float32 rows (query heads 2 j, 2 j + 1 of the block, 1 KiB of
+// consecutive bytes): lane l takes head 2 j + l / 32 and head dims
+// 4 (l % 32) .. + 3.  Two pieces are in flight at a time, folded as the
+// balanced merge folds them (a piece without visible keys gets weight 0).
+// Against one wave per output row, a group is looked up by 8x fewer waves,
+// and each load instruction moves 1 KiB instead of 512 bytes.
+__global__ __launch_bounds__(256) void pa_fp8_worklist_reduce8_kernel(const pa_fp8_worklist_reduce_args a) {
+  constexpr int J = 4;       // loads per piece
+  constexpr int kBatch = 2;  // pieces in flight
+  const int lane = threadIdx.x & 63;
+  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int Hq = a.num_query_heads, mq = a.max_query_length;
+  const int nhb = Hq / 8;
+  if (w >= (int64_t)a.num_groups * mq * nhb) return;
+  const int hb = (int)(w % nhb);
+  const int qi = (int)((w / nhb) % mq);
+  const int g = (int)(w / ((int64_t)nhb * mq));
+  const int p0 = a.reduce_indptr[g], p1 = a.reduce_indptr[g + 1];
+  if (p1 <= p0) return;
+  const int qo0 = a.reduce_final_map[2 * g], qo1 = a.reduce_final_map[2 * g + 1];
+  if (qi >= qo1 - qo0) return;
+  const int32_t* pmap = a.reduce_partial_map + p0;
+  const int n = p1 - p0;
+  const int d0 = 4 * (lane & 31);
+  int qh[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) qh[j] = 8 * hb + 2 * j + (lane >> 5);
+  float M[J], tot[J];
+  f32x4 o[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    M[j] = kNegInf;
+    tot[j] = 0.0f;
+    o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int i0 = 0; i0 < n; i0 += kBatch) {
+    float l[kBatch][J];
+    f32x4 x[kBatch][J];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int i = i0 + k < n ? i0 + k : n - 1;
+      const int64_t prow = (int64_t)pmap[i] + qi;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        l[k][j] = a.partial_lse[prow * a.stride_pl_row + qh[j]];
+        x[k][j] = *(const f32x4*)(a.partial_output + prow * a.stride_po_row + (int64_t)qh[j] * kHead + d0);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const bool in = i0 + k < n;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const float lk = in ? l[k][j] : kNegInf;
+        const float Mn = fmaxf(M[j], lk);
+        const float fold = M[j] == kNegInf ? 0.0f : __expf(M[j] - Mn);
+        const float wk = lk == kNegInf ? 0.0f : __expf(lk - Mn);
+        tot[j] = tot[j] * fold + wk;
+        const f32x4 xv = lk == kNegInf ? f32x4{0.f, 0.f, 0.f, 0.f} : x[k][j];
+        o[j] = o[j] * fold + xv * wk;
+        M[j] = Mn;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const float inv = tot[j] > 0.0f ? 1.0f / tot[j] : 0.0f;
+    store_out4(a.output, a.output_dtype,
+               (int64_t)(qo0 + qi) * a.stride_out_tok + (int64_t)qh[j] * a.stride_out_head + d0, o[j] * inv);
+  }
+}
+
 // One wave per (sequence, kv head, column); lane l covers head dims 2l,
 // 2l+1.  For each batch of up to 32 slots every load -- the slot's max and
 // sum (one slot per lane) and the lane's two values of every slot's partial
@@ -4270,6 +4344,22 @@ int pa_fp8_reduce_worklist(const pa_fp8_worklist_reduce_args* a, void* stream) {
   if ((rows + 3) / 4 > 0x7fffffffLL) return PA_ERR_SHAPE;
   const dim3 grid((unsigned)((rows + 3) / 4));
   hipStream_t s = (hipStream_t)stream;
+  // Head size 128 and at least 128 output rows per group (query length x
+  // query heads; multi-token prediction): eight heads per wave, two pieces
+  // in flight.  With fewer rows per group the one-row waves are few and
+  // their eight pieces in flight suit groups cut into many pieces.  Measured
+  // (kernel us): bench workload c5_mtp_p1024, 256 rows per group, 32 -> 12.8;
+  // c3_ragged_p1024, 32 rows per group and up to about 30 pieces, 4.7 with
+  // one row per wave against 7.2 with eight heads.
+  if (a->head_size == kHead && a->num_query_heads % 8 == 0 &&
+      (int64_t)a->max_query_length * a->num_query_heads >= 128 && ((uintptr_t)a->partial_output & 15u) == 0 &&
+      ((uintptr_t)a->output & 15u) == 0 && a->stride_po_row % 4 == 0 && a->stride_out_tok % 4 == 0 &&
+      a->stride_out_head % 4 == 0) {
+    const int64_t waves = rows / 8;
+    hipLaunchKernelGGL(pa_fp8_worklist_reduce8_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, *a);
+    hipError_t err = hipGetLastError();
+    return err == hipSuccess ? PA_OK : (int)err;
+  }
   switch (a->head_size) {
     case 64: hipLaunchKernelGGL(pa_fp8_generic_worklist_reduce_kernel<1>, grid, dim3(256), 0, s, *a); break;
     case 192: hipLaunchKernelGGL(pa_fp8_generic_worklist_reduce_kernel<3>, grid, dim3(256), 0, s, *a); break;

@@ -14,6 +14,8 @@ fp8; per-tensor scales [1] or per-token-per-head scales [NB, Hkv, bs, 1]
   c5_mtp     B256, ql4, Hq64/Hkv4,  bs64, ctx U[4096, 8192], per token
   c3_ragged_p1024  C3's batch on 1024-token pages: the persistent
              (work-list) route of get_pa_metadata + pa_decode_ps_launch
+  c5_mtp_p1024     C5's batch on 1024-token pages: the same route with
+             64 query columns per kv head (cooperative bins)
   c2_d64, c2_d256  C2's batch at head sizes 64 and 256 (the generic kernels)
 """
 
@@ -57,6 +59,7 @@ CONFIGS: Dict[str, DecodeConfig] = {
     "c4_window": DecodeConfig("c4_window", 32, 1, 32, 8, 16, "uniform:8192:32768", False, sliding_window=4096),
     "c5_mtp": DecodeConfig("c5_mtp", 256, 4, 64, 4, 64, "uniform:4096:8192", True),
     "c3_ragged_p1024": DecodeConfig("c3_ragged_p1024", 128, 1, 32, 8, 1024, "lognormal:2048:1.0:16:32768", True),
+    "c5_mtp_p1024": DecodeConfig("c5_mtp_p1024", 256, 4, 64, 4, 1024, "uniform:4096:8192", True),
     "c2_d64": DecodeConfig("c2_d64", 64, 1, 32, 8, 16, "fixed:4096", False, head_size=64),
     "c2_d256": DecodeConfig("c2_d256", 64, 1, 32, 8, 16, "fixed:4096", False, head_size=256),
 }
