@@ -606,15 +606,6 @@ __device__ __forceinline__ void unit_softmax_pv(WaveState<1>& s, const QueryTile
                                                 const LDS_AS float* const (&ssc)[NCH], int grp, int c16,
                                                 const int (&tb)[NCH]) {
   static_assert(NCH == 2 || NCH == 4, "units of two or four chunks");
-  bool edge[NCH];
-  int jlo[NCH], jhi[NCH];
-#pragma unroll
-  for (int ch = 0; ch < NCH; ++ch) {
-    edge[ch] = tb[ch] < q.lo_all || tb[ch] + kChunk > q.hi_all;
-    const int tok0 = tb[ch] + 8 * grp;
-    jlo[ch] = pa_min(pa_max(q.lo_all - tok0, 0), 8);
-    jhi[ch] = pa_min(pa_max(q.hi_all - tok0, jlo[ch]), 8);
-  }
   auto scales = [&](int ch, int off, float (&x)[8]) {
     const LDS_AS float* ss = ssc[ch] + off + 8 * grp;
     const f32x4 x0 = *(const LDS_AS f32x4*)ss;
@@ -626,19 +617,17 @@ __device__ __forceinline__ void unit_softmax_pv(WaveState<1>& s, const QueryTile
     }
   };
 
-  float vsc[NCH][8];
+  // Value scales are read where they are used: the loading wave zeroed the
+  // scales of keys no column sees, so no mask applies to them.
   float vratio = 1.0f, vmul = 1.0f, vlog = 0.0f;
   if (PER_TOKEN) {
     float cmax = 0.0f;
 #pragma unroll
     for (int ch = 0; ch < NCH; ++ch) {
-      scales(ch, 32, vsc[ch]);
-      if (__builtin_expect(edge[ch], 0)) {
+      float vs[8];
+      scales(ch, 32, vs);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) vsc[ch][j] = (j >= jlo[ch] && j < jhi[ch]) ? vsc[ch][j] : 0.0f;
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) cmax = fmaxf(cmax, vsc[ch][j]);
+      for (int j = 0; j < 8; ++j) cmax = fmaxf(cmax, vs[j]);
     }
     cmax = max_over_groups(cmax);
     const float vnew = cmax > 2.0f * s.vsmax ? cmax : s.vsmax;
@@ -687,12 +676,13 @@ __device__ __forceinline__ void unit_softmax_pv(WaveState<1>& s, const QueryTile
   i32x8 PH = {0, 0, 0, 0, 0, 0, 0, 0}, PL = PH;
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch) {
-    float pr[8];
+    float pr[8], vs[8];
+    if (PER_TOKEN) scales(ch, 32, vs);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float ev = __builtin_amdgcn_exp2f(__builtin_fmaf(lg[ch][j], post, bias));
       psum += ev;
-      pr[j] = PER_TOKEN ? ev * vsc[ch][j] : ev;
+      pr[j] = PER_TOKEN ? ev * vs[j] : ev;
     }
     long phi, plo;
     split8_fp8(pr, phi, plo);
@@ -2583,7 +2573,7 @@ __global__ __launch_bounds__(64 * NW, coop_waves_per_simd(NW, WORKLIST)) void pa
             for (int hh = 0; hh < 2; ++hh)
               zero_stale_values((LDS_AS unsigned char*)smem + sl * kSlotBytes + kKBytes + hh * 2048,
                                 ub + ch * kChunk + 16 * hh, cur.lo_all, cur.hi_all, lane);
-            if (U == 4 && PER_TOKEN) {
+            if (PER_TOKEN) {
               // and the chunk's per-token K and V scales of those keys
               // (lane l: K scale l < 32, else V scale l - 32), so that the
               // softmax reads zeros there rather than stale bits
