@@ -263,6 +263,9 @@ WORKLIST_CASES = {
     "coop_ql4_gqa16_pt": dict(batch=4, query_length=4, num_query_heads=32, num_kv_heads=2, per_token=True,
                               ctx_range=(4, 6000)),
     "coop_gqa32": dict(batch=4, num_query_heads=32, num_kv_heads=1, ctx_range=(1, 7000)),
+    # 128 output rows per reduce group (query length x query heads): the
+    # reduce's eight-heads-per-wave form, after the bin kernel
+    "ql2_gqa8_h64": dict(batch=5, query_length=2, num_query_heads=64, num_kv_heads=8, ctx_range=(2, 6000)),
 }
 
 
